@@ -1,0 +1,118 @@
+/*
+ * llmopt_qlinear.h -- C ABI of libllmopt_qlinear.so, the gfx950 (MI355X)
+ * fused dequantize-and-multiply library behind llmopt.quantization.QuantLinear.
+ *
+ * Storage layout consumed (identical to the reference's, quantizers.py:83-97,
+ * 100-142, 204-239):
+ *   qweight, bits 1 - 7  : uint8 [N, ldq], two codes per byte; column k is in
+ *                          byte k>>1, even k in bits 0-3, odd k in bits 4-7.
+ *   qweight, bits 8      : uint8 (asymmetric) or int8 (symmetric) [N, ldq].
+ *   scales, zeros        : fp32 [N, K/group], row-major, contiguous.
+ *   dequantized weight   : w[n,k] = (q[n,k] - z) * s   evaluated in fp32 with a
+ *                          single rounding, z = zeros[n, k/group] (asymmetric),
+ *                          2^(bits-1) (symmetric, bits < 8) or 0 (symmetric 8-bit).
+ *
+ * Conventions:
+ *   - Every pointer is a device pointer on the current HIP device, owned by the
+ *     caller. The library keeps no tensors and allocates no device memory;
+ *     scratch space for split-K comes in through `workspace`.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream). Work is
+ *     enqueued asynchronously; nothing synchronises the host.
+ *   - Return value: LLMOPT_OK (0) or a negative LLMOPT_ERR_* code. The message of
+ *     the last failure on the calling thread is llmopt_q_last_error().
+ *   - Reentrant: no mutable global state; calls from several host threads on
+ *     different streams are independent.
+ *   - group_size <= 0 means one group spanning the whole row.
+ *   - dtype codes: LLMOPT_DTYPE_F32 / F16 / BF16.
+ *
+ * The reference (Python on torch) has no C interface; each entry point below
+ * names the Python function whose work it replaces.
+ */
+#ifndef LLMOPT_QLINEAR_H_
+#define LLMOPT_QLINEAR_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LLMOPT_QLINEAR_ABI_VERSION 1
+
+#define LLMOPT_DTYPE_F32 0
+#define LLMOPT_DTYPE_F16 1
+#define LLMOPT_DTYPE_BF16 2
+
+#define LLMOPT_OK 0
+#define LLMOPT_ERR_INVALID_ARG (-1)
+#define LLMOPT_ERR_UNSUPPORTED (-2)
+#define LLMOPT_ERR_HIP (-3)
+#define LLMOPT_ERR_WORKSPACE (-4)
+
+/* Kernel selection for llmopt_q_linear_ex. AUTO is what llmopt_q_linear uses. */
+#define LLMOPT_ALGO_AUTO 0
+#define LLMOPT_ALGO_GENERIC 1 /* any shape and dtype; scalar dequant + fp32 dot */
+#define LLMOPT_ALGO_DECODE 2  /* MFMA skinny GEMM, M <= 64 */
+#define LLMOPT_ALGO_PREFILL 3 /* MFMA GEMM with weight tiles dequantized into LDS */
+
+/* ABI version of the loaded library (LLMOPT_QLINEAR_ABI_VERSION). */
+int llmopt_q_abi_version(void);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* llmopt_q_last_error(void);
+
+/*
+ * Split packed bytes into nibble codes.
+ * Replaces unpack_int4 (src/llmopt/quantization/quantizers.py:92-97):
+ *   codes[r, c] = (packed[r, c>>1] >> (4*(c&1))) & 0xF   for c < columns.
+ * packed: uint8 [rows, packed_cols]; codes: uint8 [rows, columns], columns <= 2*packed_cols.
+ */
+int llmopt_q_unpack(const uint8_t* packed, uint8_t* codes, int64_t rows, int64_t packed_cols,
+                    int64_t columns, void* stream);
+
+/*
+ * Dense weight from the packed form, bit-identical to the reference.
+ * Replaces dequantize + dequantize_codes (quantizers.py:204-239):
+ *   out[n, k] = dtype((q[n,k] - z) * s)   (fp32 arithmetic, round-to-nearest-even cast).
+ * qweight: [N, ldq] bytes; zeros may be NULL when symmetric; signed_codes = 1 when
+ * an 8-bit qweight is int8. out: [N, K] of out_dtype.
+ */
+int llmopt_q_dequant(const void* qweight, int64_t ldq, const float* scales, const float* zeros,
+                     void* out, int out_dtype, int64_t N, int64_t K, int bits, int group_size,
+                     int symmetric, int signed_codes, void* stream);
+
+/*
+ * Bytes of workspace llmopt_q_linear may use for these sizes (0 if none).
+ */
+size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size);
+
+/*
+ * y = x @ dequant(qweight)^T + bias, without materialising the dense weight.
+ * Replaces QuantLinear.forward (src/llmopt/quantization/quant_linear.py:93-113):
+ * the reference dequantizes into a cached dense weight and calls F.linear.
+ * x: [M, K] act_dtype with row stride ldx; y: [M, N] act_dtype with row stride ldy;
+ * bias: [N] act_dtype or NULL. Accumulation is fp32. M == 0 is a no-op.
+ */
+int llmopt_q_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                    int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                    void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                    int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/*
+ * llmopt_q_linear with an explicit kernel choice (LLMOPT_ALGO_*). Returns
+ * LLMOPT_ERR_UNSUPPORTED when the chosen kernel cannot take these arguments.
+ * No counterpart in the reference: lets tests and benchmarks pin one kernel.
+ */
+int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                       int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                       void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                       int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
+                       void* stream, int algo);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLMOPT_QLINEAR_H_ */

@@ -1,0 +1,187 @@
+// C ABI of libllmopt_qlinear.so (declared in include/llmopt_qlinear.h).
+//
+// Validates arguments the way the reference's torch code would reject them, fills the
+// kernel argument block and picks the kernel: the MFMA skinny GEMM for M <= 64, the MFMA
+// LDS-dequant GEMM for larger M, and the generic kernel for shapes, alignments or dtypes
+// the fast kernels do not take. Error text is kept per host thread.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/llmopt_qlinear.h"
+#include "qcommon.hpp"
+#include "qkernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, args);
+  va_end(args);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return LLMOPT_OK;
+  return fail(LLMOPT_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+bool valid_dtype(int dt) {
+  return dt == LLMOPT_DTYPE_F32 || dt == LLMOPT_DTYPE_F16 || dt == LLMOPT_DTYPE_BF16;
+}
+
+// Shared validation of the packed-weight description; fills the format fields of `a`.
+int describe_weight(llmopt::LinearArgs& a, const void* qweight, int64_t ldq, const float* scales,
+                    const float* zeros, int64_t N, int64_t K, int bits, int group_size,
+                    int symmetric, int signed_codes) {
+  // Widths below 8 share the two-codes-per-byte storage (quantizers.py:236,273).
+  if (bits < 1 || bits > 8) return fail(LLMOPT_ERR_INVALID_ARG, "unsupported bit width: %d", bits);
+  if (N < 0 || K < 0) return fail(LLMOPT_ERR_INVALID_ARG, "negative shape N=%lld K=%lld",
+                                  (long long)N, (long long)K);
+  const int64_t group = group_size <= 0 ? K : group_size;
+  if (K > 0 && (group <= 0 || K % group != 0))
+    return fail(LLMOPT_ERR_INVALID_ARG, "in_features=%lld not divisible by group_size=%lld",
+                (long long)K, (long long)group);
+  const int fmt = bits == 8 ? llmopt::kByte : llmopt::kNibble;
+  const int64_t need = fmt == llmopt::kNibble ? (K + 1) / 2 : K;
+  if (ldq < need)
+    return fail(LLMOPT_ERR_INVALID_ARG, "packed row of %lld bytes cannot hold %lld columns",
+                (long long)ldq, (long long)K);
+  if (fmt == llmopt::kNibble && signed_codes)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "sub-byte codes must be stored as uint8");
+  if (N > 0 && K > 0) {
+    if (!qweight || !scales) return fail(LLMOPT_ERR_INVALID_ARG, "null qweight or scales");
+    if (!symmetric && !zeros) return fail(LLMOPT_ERR_INVALID_ARG, "asymmetric grid needs zeros");
+  }
+  a.qw = static_cast<const uint8_t*>(qweight);
+  a.ldq = ldq;
+  a.scales = scales;
+  a.zeros = symmetric ? nullptr : zeros;
+  a.N = N;
+  a.K = K;
+  a.group = group > 0 ? group : 1;
+  a.G = group > 0 ? K / group : 0;
+  a.fmt = fmt;
+  a.bits = bits;
+  a.symmetric = symmetric ? 1 : 0;
+  a.signed_codes = signed_codes ? 1 : 0;
+  a.zero_const = (symmetric && bits < 8) ? float(1 << (bits - 1)) : 0.0f;
+  return LLMOPT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmopt_q_abi_version(void) { return LLMOPT_QLINEAR_ABI_VERSION; }
+
+const char* llmopt_q_last_error(void) { return g_last_error.c_str(); }
+
+int llmopt_q_unpack(const uint8_t* packed, uint8_t* codes, int64_t rows, int64_t packed_cols,
+                    int64_t columns, void* stream) {
+  if (rows < 0 || packed_cols < 0 || columns < 0)
+    return fail(LLMOPT_ERR_INVALID_ARG, "negative unpack shape");
+  if (columns > 2 * packed_cols)
+    return fail(LLMOPT_ERR_INVALID_ARG, "columns=%lld exceeds 2 * packed_cols=%lld",
+                (long long)columns, (long long)(2 * packed_cols));
+  if (rows > 0 && columns > 0 && (!packed || !codes))
+    return fail(LLMOPT_ERR_INVALID_ARG, "null unpack pointer");
+  return hip_status(llmopt::launch_unpack(packed, codes, rows, packed_cols, columns,
+                                          static_cast<hipStream_t>(stream)),
+                    "unpack launch");
+}
+
+int llmopt_q_dequant(const void* qweight, int64_t ldq, const float* scales, const float* zeros,
+                     void* out, int out_dtype, int64_t N, int64_t K, int bits, int group_size,
+                     int symmetric, int signed_codes, void* stream) {
+  if (!valid_dtype(out_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", out_dtype);
+  llmopt::LinearArgs a{};
+  const int rc = describe_weight(a, qweight, ldq, scales, zeros, N, K, bits, group_size,
+                                 symmetric, signed_codes);
+  if (rc != LLMOPT_OK) return rc;
+  if (N > 0 && K > 0 && !out) return fail(LLMOPT_ERR_INVALID_ARG, "null output");
+  return hip_status(llmopt::launch_dequant(a, out, out_dtype, static_cast<hipStream_t>(stream)),
+                    "dequant launch");
+}
+
+size_t llmopt_q_linear_workspace(int64_t, int64_t, int64_t, int, int) { return 0; }
+
+int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                       int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                       void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                       int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
+                       void* stream, int algo) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (!valid_dtype(act_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", act_dtype);
+  if (M < 0) return fail(LLMOPT_ERR_INVALID_ARG, "negative M=%lld", (long long)M);
+  llmopt::LinearArgs a{};
+  int rc = describe_weight(a, qweight, ldq, scales, zeros, N, K, bits, group_size, symmetric,
+                           signed_codes);
+  if (rc != LLMOPT_OK) return rc;
+  if (M == 0 || N == 0) return LLMOPT_OK;
+  if (ldx < K || ldy < N)
+    return fail(LLMOPT_ERR_INVALID_ARG, "row strides ldx=%lld ldy=%lld below K=%lld N=%lld",
+                (long long)ldx, (long long)ldy, (long long)K, (long long)N);
+  if (!x || !y) return fail(LLMOPT_ERR_INVALID_ARG, "null activation or output");
+  a.x = x;
+  a.bias = bias;
+  a.y = y;
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.M = M;
+  a.act = act_dtype;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (K == 0) {
+    // An empty reduction: the reference's F.linear returns the bias (or zeros).
+    a.K = 0;
+    return hip_status(llmopt::launch_linear_generic(a, s), "linear launch");
+  }
+
+  bool fits = false;
+  hipError_t err = hipSuccess;
+  switch (algo) {
+    case LLMOPT_ALGO_AUTO:
+      if (M <= 64) {
+        err = llmopt::launch_linear_decode(a, s, &fits);
+      } else {
+        err = llmopt::launch_linear_prefill(a, s, &fits);
+      }
+      if (!fits) err = llmopt::launch_linear_generic(a, s);
+      break;
+    case LLMOPT_ALGO_GENERIC:
+      err = llmopt::launch_linear_generic(a, s);
+      break;
+    case LLMOPT_ALGO_DECODE:
+      err = llmopt::launch_linear_decode(a, s, &fits);
+      if (!fits) return fail(LLMOPT_ERR_UNSUPPORTED, "decode kernel does not take these arguments");
+      break;
+    case LLMOPT_ALGO_PREFILL:
+      err = llmopt::launch_linear_prefill(a, s, &fits);
+      if (!fits) return fail(LLMOPT_ERR_UNSUPPORTED, "prefill kernel does not take these arguments");
+      break;
+    default:
+      return fail(LLMOPT_ERR_INVALID_ARG, "unknown algo %d", algo);
+  }
+  return hip_status(err, "linear launch");
+}
+
+int llmopt_q_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                    int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                    void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                    int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  return llmopt_q_linear_ex(x, M, K, ldx, qweight, ldq, scales, zeros, bias, y, N, ldy, act_dtype,
+                            bits, group_size, symmetric, signed_codes, workspace, workspace_bytes,
+                            stream, LLMOPT_ALGO_AUTO);
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+// Shared device helpers for the gfx950 quantized-linear kernels.
+//
+// Storage formats (the reference layout, src/llmopt/quantization/quantizers.py:83-97):
+//   kNibble : bits 2 and 4. uint8 [N, ldq]; column k in byte k>>1, even k in bits 0-3.
+//   kByte   : bits 8. uint8 (asymmetric) or int8 (symmetric) [N, ldq], one code per byte.
+// Group metadata: fp32 scales/zeros [N, G], G = K / group, row-major.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llmopt {
+
+enum : int { kNibble = 0, kByte = 1 };
+enum : int { kDtF32 = 0, kDtF16 = 1, kDtBf16 = 2 };
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// ---- scalar conversions ----------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// fp32 -> bf16, round to nearest even; NaN becomes the canonical 0x7FC0 (torch's c10::BFloat16).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return float(__builtin_bit_cast(_Float16, h));
+}
+
+// fp32 -> fp16 with the hardware conversion (round to nearest even in the default mode).
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, _Float16(f));
+}
+
+// Activation element types. `raw` is the storage word; load/store convert through fp32.
+struct ActF32 {
+  using raw = float;
+  static constexpr int id = kDtF32;
+  __device__ static float load(raw v) { return v; }
+  __device__ static raw store(float f) { return f; }
+};
+struct ActF16 {
+  using raw = uint16_t;
+  static constexpr int id = kDtF16;
+  static constexpr uint32_t kOne2 = 0x3C003C00u;       // (1.0, 1.0)
+  static constexpr uint32_t kNibbleMagic2 = 0x64006400u;  // 1024.0: OR-ing an int < 1024 gives 1024+q
+  static constexpr float kNibbleOffset = 1024.0f;
+  __device__ static float load(raw v) { return f16_to_f32(v); }
+  __device__ static raw store(float f) { return f32_to_f16_rne(f); }
+};
+struct ActBf16 {
+  using raw = uint16_t;
+  static constexpr int id = kDtBf16;
+  static constexpr uint32_t kOne2 = 0x3F803F80u;        // (1.0, 1.0)
+  static constexpr uint32_t kNibbleMagic2 = 0x43004300u;  // 128.0: OR-ing an int < 128 gives 128+q
+  static constexpr float kNibbleOffset = 128.0f;
+  __device__ static float load(raw v) { return bf16_to_f32(v); }
+  __device__ static raw store(float f) { return f32_to_bf16_rne(f); }
+};
+
+// ---- code access -----------------------------------------------------------------------------
+
+// Numeric value of code k of one weight row, exactly as the reference reads it:
+// nibble storage -> (byte >> 4*(k&1)) & 0xF; uint8 -> 0..255; int8 -> -128..127.
+__device__ __forceinline__ float code_value(const uint8_t* row, int64_t k, int fmt, int signed_codes) {
+  if (fmt == kNibble) {
+    const uint32_t b = row[k >> 1];
+    return float((b >> ((k & 1) * 4)) & 0xFu);
+  }
+  const uint8_t b = row[k];
+  return signed_codes ? float(int8_t(b)) : float(b);
+}
+
+// The reference's fp32 dequantization of one code: (q - z) * s with one rounding at each
+// step, never contracted into an fma (the subtraction is exact for integer-valued z).
+__device__ __forceinline__ float dequant_exact(float q, float z, float s) {
+  const float d = __fsub_rn(q, z);
+  return __fmul_rn(d, s);
+}
+
+// Fast exact division of small non-negative integers by a runtime divisor (< 2^16, dividend
+// < 2^16): q = umulhi(c, ceil(2^32 / d)). A divisor of 1 is encoded as magic 0.
+__device__ __forceinline__ uint32_t div_small(uint32_t c, uint32_t magic) {
+  return magic ? __umulhi(c, magic) : c;
+}
+
+}  // namespace llmopt

@@ -1,0 +1,127 @@
+// Unpack and dequantize kernels: the device form of unpack_int4 / dequantize
+// (src/llmopt/quantization/quantizers.py:92-97, 204-239). Both are bit-exact with the
+// reference's torch arithmetic: codes are pure bit operations, and the dense weight is
+// (q - z) * s in fp32 with one rounding per operation, then a round-to-nearest-even cast.
+#include "qcommon.hpp"
+#include "qkernels.hpp"
+
+namespace llmopt {
+namespace {
+
+// Four packed bytes -> eight codes, low nibble first.
+__device__ __forceinline__ u32x2 split_nibbles(uint32_t w) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+  u32x2 out;
+  out.x = (lo & 0xFFu) | ((hi & 0xFFu) << 8) | ((lo & 0xFF00u) << 8) | ((hi & 0xFF00u) << 16);
+  out.y = ((lo >> 16) & 0xFFu) | (((hi >> 16) & 0xFFu) << 8) | ((lo >> 24) << 16) | ((hi >> 24) << 24);
+  return out;
+}
+
+// Rows whose full packed width is unpacked, with 4-byte-aligned packed rows and 8-byte-aligned
+// output rows: each thread turns one packed dword into eight codes.
+__global__ void __launch_bounds__(256) unpack_words_kernel(const uint32_t* packed, u32x2* codes,
+                                                           int64_t words) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < words;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    codes[i] = split_nibbles(packed[i]);
+  }
+}
+
+// Any geometry: one thread per packed byte, writing the one or two codes that fall below
+// `columns`.
+__global__ void __launch_bounds__(256) unpack_bytes_kernel(const uint8_t* packed, uint8_t* codes,
+                                                           int64_t rows, int64_t packed_cols,
+                                                           int64_t columns) {
+  const int64_t total = rows * packed_cols;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = i / packed_cols;
+    const int64_t j = i - r * packed_cols;
+    const uint8_t b = packed[i];
+    const int64_t c = 2 * j;
+    uint8_t* out = codes + r * columns;
+    if (c < columns) out[c] = b & 0x0F;
+    if (c + 1 < columns) out[c + 1] = b >> 4;
+  }
+}
+
+template <class Out>
+__device__ __forceinline__ void store_elem(void* out, int64_t idx, float v) {
+  static_cast<typename Out::raw*>(out)[idx] = Out::store(v);
+}
+
+// Dense weight: each thread produces eight consecutive columns of one row.
+template <class Out>
+__global__ void __launch_bounds__(256) dequant_kernel(const LinearArgs a, void* out) {
+  const int64_t chunks = (a.K + 7) / 8;
+  const int64_t total = a.N * chunks;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t n = i / chunks;
+    const int64_t k0 = (i - n * chunks) * 8;
+    const uint8_t* row = a.qw + n * a.ldq;
+    const float* srow = a.scales + n * a.G;
+    const float* zrow = a.symmetric ? nullptr : a.zeros + n * a.G;
+    int64_t g = k0 / a.group;
+    int64_t in_group = k0 - g * a.group;
+    const int64_t k_end = k0 + 8 < a.K ? k0 + 8 : a.K;
+    for (int64_t k = k0; k < k_end; ++k) {
+      if (in_group == a.group) {
+        ++g;
+        in_group = 0;
+      }
+      const float q = code_value(row, k, a.fmt, a.signed_codes);
+      const float z = zrow ? zrow[g] : a.zero_const;
+      store_elem<Out>(out, n * a.K + k, dequant_exact(q, z, srow[g]));
+      ++in_group;
+    }
+  }
+}
+
+int grid_for(int64_t work, int per_block) {
+  int64_t blocks = (work + per_block - 1) / per_block;
+  if (blocks > 65536) blocks = 65536;
+  return blocks < 1 ? 1 : int(blocks);
+}
+
+}  // namespace
+
+hipError_t launch_unpack(const uint8_t* packed, uint8_t* codes, int64_t rows, int64_t packed_cols,
+                         int64_t columns, hipStream_t stream) {
+  if (rows == 0 || columns == 0) return hipSuccess;
+  const bool whole_rows = columns == 2 * packed_cols;
+  const bool aligned = (reinterpret_cast<uintptr_t>(packed) % 4 == 0) &&
+                       (reinterpret_cast<uintptr_t>(codes) % 8 == 0) && (packed_cols % 4 == 0);
+  if (whole_rows && aligned) {
+    const int64_t words = rows * packed_cols / 4;
+    hipLaunchKernelGGL(unpack_words_kernel, dim3(grid_for(words, 256)), dim3(256), 0, stream,
+                       reinterpret_cast<const uint32_t*>(packed), reinterpret_cast<u32x2*>(codes),
+                       words);
+  } else {
+    hipLaunchKernelGGL(unpack_bytes_kernel, dim3(grid_for(rows * packed_cols, 256)), dim3(256), 0,
+                       stream, packed, codes, rows, packed_cols, columns);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant(const LinearArgs& a, void* out, int out_dtype, hipStream_t stream) {
+  if (a.N == 0 || a.K == 0) return hipSuccess;
+  const dim3 grid(grid_for(a.N * ((a.K + 7) / 8), 256));
+  switch (out_dtype) {
+    case kDtF32:
+      hipLaunchKernelGGL(dequant_kernel<ActF32>, grid, dim3(256), 0, stream, a, out);
+      break;
+    case kDtF16:
+      hipLaunchKernelGGL(dequant_kernel<ActF16>, grid, dim3(256), 0, stream, a, out);
+      break;
+    case kDtBf16:
+      hipLaunchKernelGGL(dequant_kernel<ActBf16>, grid, dim3(256), 0, stream, a, out);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace llmopt

@@ -1,0 +1,206 @@
+"""Torch-facing wrappers over the C ABI of ``libllmopt_qlinear.so``.
+
+These are the only entry points the quantization layer uses on HIP devices:
+
+* :func:`unpack_nibbles` replaces ``unpack_int4`` (``quantizers.py:92-97``),
+* :func:`dequantize` replaces ``dequantize`` (``quantizers.py:231-239``),
+* :func:`quant_linear` replaces the dequantize-then-``F.linear`` body of
+  ``QuantLinear.forward`` (``quant_linear.py:93-113``).
+
+Each wrapper checks what torch would check (dtypes, devices, shapes), passes raw
+device pointers and the current HIP stream to the library, and raises if the
+library is missing or reports an error. Nothing here computes on the host.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from llmopt.kernels._lib import ALGO_AUTO, DTYPE_CODES, call, load_library
+
+__all__ = ["dequantize", "quant_linear", "unpack_nibbles"]
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _same_device(x: torch.Tensor, *others: torch.Tensor | None) -> None:
+    for other in others:
+        if other is not None and other.device != x.device:
+            raise RuntimeError(
+                "Expected all tensors to be on the same device, but found at least two devices, "
+                f"{x.device} and {other.device}!"
+            )
+
+
+def _metadata(tensor: torch.Tensor, rows: int, groups: int, what: str) -> torch.Tensor:
+    """fp32 contiguous ``[rows, groups]`` view of scales/zeros, broadcasting like torch."""
+    if tensor.dtype != torch.float32:
+        tensor = tensor.to(torch.float32)
+    if tuple(tensor.shape) != (rows, groups):
+        try:
+            tensor = tensor.expand(rows, groups)
+        except RuntimeError as exc:
+            raise RuntimeError(
+                f"{what} of shape {tuple(tensor.shape)} does not broadcast to ({rows}, {groups})"
+            ) from exc
+    return tensor.contiguous()
+
+
+def _weight_args(qt, device: torch.device):  # noqa: ANN001, ANN202 - QuantizedTensor
+    """Validated (qweight, ldq, scales, zeros, N, K, group, signed) for a QuantizedTensor."""
+    rows, cols = (int(d) for d in qt.shape)
+    bits = int(qt.bits)
+    if not 1 <= bits <= 8:
+        raise ValueError(f"unsupported bit width: {bits}")
+    group = cols if qt.group_size is None or qt.group_size <= 0 else int(qt.group_size)
+    if cols % group:
+        raise RuntimeError(
+            f"shape '[{rows}, {cols // group}, {group}]' is invalid for input of size {rows * cols}"
+        )
+    qweight = qt.qweight
+    _same_device(qweight, qt.scales, None if qt.symmetric else qt.zeros)
+    if qweight.device != device:
+        _same_device(torch.empty(0, device=device), qweight)
+    if bits < 8 and qweight.dtype != torch.uint8:
+        raise TypeError(f"{bits}-bit codes must be packed as uint8, got {qweight.dtype}")
+    if bits == 8 and qweight.dtype not in (torch.uint8, torch.int8):
+        raise TypeError(f"8-bit codes must be uint8 or int8, got {qweight.dtype}")
+    qweight = qweight.contiguous()
+    if qweight.dim() != 2 or qweight.shape[0] != rows:
+        raise RuntimeError(f"qweight of shape {tuple(qweight.shape)} does not match weight {rows}x{cols}")
+    needed = cols if bits == 8 else (cols + 1) // 2
+    if qweight.shape[1] < needed:
+        raise RuntimeError(
+            f"qweight row of {qweight.shape[1]} bytes cannot hold {cols} {bits}-bit codes"
+        )
+    groups = cols // group if cols else 0
+    scales = _metadata(qt.scales, rows, groups, "scales")
+    zeros = None if qt.symmetric else _metadata(qt.zeros, rows, groups, "zeros")
+    signed = qweight.dtype == torch.int8
+    return qweight, int(qweight.shape[1]), scales, zeros, rows, cols, int(qt.group_size), signed
+
+
+def unpack_nibbles(packed: torch.Tensor, columns: int) -> torch.Tensor:
+    """``unpack_int4`` on a HIP tensor: ``[..., P]`` uint8 -> ``[..., min(columns, 2P)]``."""
+    if packed.dtype != torch.uint8:
+        raise TypeError(f"packed nibbles must be uint8, got {packed.dtype}")
+    packed = packed.contiguous()
+    width = packed.shape[-1] if packed.dim() else 1
+    keep = len(range(2 * width)[:columns])
+    out = torch.empty(*packed.shape[:-1], keep, dtype=torch.uint8, device=packed.device)
+    rows = packed.numel() // width if width else 0
+    if out.numel() == 0:
+        return out
+    lib = load_library()
+    call(
+        lib.llmopt_q_unpack(
+            packed.data_ptr(), out.data_ptr(), rows, width, keep, _stream_handle(packed.device)
+        ),
+        "llmopt_q_unpack",
+    )
+    return out
+
+
+def dequantize(qt, dtype: torch.dtype = torch.float32) -> torch.Tensor:  # noqa: ANN001
+    """Dense ``[N, K]`` weight from a QuantizedTensor whose tensors live on a HIP device.
+
+    The kernel evaluates the reference's fp32 ``(q - z) * s`` bit for bit and casts to
+    fp32, fp16 or bf16 with round-to-nearest-even; other dtypes are produced from the
+    fp32 result with ``.to(dtype)``, the same final step the reference takes.
+    """
+    device = qt.qweight.device
+    qweight, ldq, scales, zeros, rows, cols, group, signed = _weight_args(qt, device)
+    native = dtype if dtype in DTYPE_CODES else torch.float32
+    out = torch.empty(rows, cols, dtype=native, device=device)
+    if out.numel():
+        lib = load_library()
+        call(
+            lib.llmopt_q_dequant(
+                qweight.data_ptr(),
+                ldq,
+                scales.data_ptr(),
+                zeros.data_ptr() if zeros is not None else None,
+                out.data_ptr(),
+                DTYPE_CODES[native],
+                rows,
+                cols,
+                int(qt.bits),
+                group,
+                int(bool(qt.symmetric)),
+                int(signed),
+                _stream_handle(device),
+            ),
+            "llmopt_q_dequant",
+        )
+    return out if native == dtype else out.to(dtype)
+
+
+def quant_linear(
+    x: torch.Tensor,
+    qt,  # noqa: ANN001 - QuantizedTensor
+    bias: torch.Tensor | None,
+    compute_dtype: torch.dtype,
+    algo: int = ALGO_AUTO,
+) -> torch.Tensor:
+    """``F.linear(x, dequantize(qt, compute_dtype), bias)`` without a dense weight.
+
+    Raises the errors ``F.linear`` would raise for mismatched dtypes, devices or shapes.
+    """
+    if x.dtype != compute_dtype:
+        raise RuntimeError(
+            f"expected m1 and m2 to have the same dtype, but got: {x.dtype} != {compute_dtype}"
+        )
+    if compute_dtype not in DTYPE_CODES:
+        raise TypeError(f"compute_dtype {compute_dtype} is not supported by the HIP kernels")
+    if bias is not None and bias.dtype != compute_dtype:
+        raise RuntimeError(
+            f"self and mat2 must have the same dtype, but got {bias.dtype} and {compute_dtype}"
+        )
+    _same_device(x, qt.qweight, qt.scales, bias)
+    qweight, ldq, scales, zeros, rows, cols, group, signed = _weight_args(qt, x.device)
+    if x.dim() == 0 or x.shape[-1] != cols:
+        lead = x.numel() // x.shape[-1] if x.dim() and x.shape[-1] else 0
+        raise RuntimeError(
+            f"mat1 and mat2 shapes cannot be multiplied ({lead}x{x.shape[-1] if x.dim() else 0} "
+            f"and {cols}x{rows})"
+        )
+    lead_shape = x.shape[:-1]
+    x2 = x.reshape(-1, cols)
+    if cols and x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    ldx = x2.stride(0) if m > 1 else cols
+    y = torch.empty(m, rows, dtype=compute_dtype, device=x.device)
+    if m and rows:
+        if bias is not None:
+            bias = bias.contiguous()
+        lib = load_library()
+        call(
+            lib.llmopt_q_linear_ex(
+                x2.data_ptr(),
+                m,
+                cols,
+                max(ldx, cols),
+                qweight.data_ptr(),
+                ldq,
+                scales.data_ptr(),
+                zeros.data_ptr() if zeros is not None else None,
+                bias.data_ptr() if bias is not None else None,
+                y.data_ptr(),
+                rows,
+                rows,
+                DTYPE_CODES[compute_dtype],
+                int(qt.bits),
+                group,
+                int(bool(qt.symmetric)),
+                int(signed),
+                None,
+                0,
+                _stream_handle(x.device),
+                int(algo),
+            ),
+            "llmopt_q_linear",
+        )
+    return y.reshape(*lead_shape, rows)

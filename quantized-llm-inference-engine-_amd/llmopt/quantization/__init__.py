@@ -1,0 +1,52 @@
+"""Weight quantization: RTN, GPTQ, packed storage and ``QuantLinear``.
+
+Exports the same names as the reference's ``src/llmopt/quantization/__init__.py:30-49``.
+"""
+
+from __future__ import annotations
+
+from llmopt.quantization.calibration import (
+    CalibrationHarness,
+    CalibrationResult,
+    HessianCollector,
+    apply_quantization,
+)
+from llmopt.quantization.quant_linear import (
+    QuantLinear,
+    QuantLinearConfig,
+    quantize_model_,
+    replace_linear_modules,
+)
+from llmopt.quantization.quantizers import (
+    GPTQQuantizer,
+    QuantizedTensor,
+    Quantizer,
+    RoundToNearestQuantizer,
+    build_quantizer,
+    choose_qparams,
+    dequantize,
+    pack_int4,
+    quantize_to_codes,
+    unpack_int4,
+)
+
+__all__ = [
+    "CalibrationHarness",
+    "CalibrationResult",
+    "GPTQQuantizer",
+    "HessianCollector",
+    "QuantLinear",
+    "QuantLinearConfig",
+    "QuantizedTensor",
+    "Quantizer",
+    "RoundToNearestQuantizer",
+    "apply_quantization",
+    "build_quantizer",
+    "choose_qparams",
+    "dequantize",
+    "pack_int4",
+    "quantize_model_",
+    "quantize_to_codes",
+    "replace_linear_modules",
+    "unpack_int4",
+]

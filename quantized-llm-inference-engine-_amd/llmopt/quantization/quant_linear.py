@@ -1,0 +1,233 @@
+"""``QuantLinear``: a linear layer whose weight stays packed on the device.
+
+Same class, constructor, attributes and error behaviour as the reference
+(``src/llmopt/quantization/quant_linear.py:18-207``). What differs is how
+``forward`` gets its answer:
+
+* On a HIP device the packed codes, scales and zeros are read directly by the
+  fused dequantize-and-multiply kernels (``llmopt.kernels``): a split-K MFMA
+  skinny GEMM for decode-sized batches and an MFMA GEMM that dequantizes weight
+  tiles into LDS for prefill-sized batches. No dense copy of the weight is ever
+  materialised, and there is no host fallback: a missing kernel library raises.
+* On the host the reference sequence is kept: dequantize once into
+  ``compute_dtype``, cache, and call ``F.linear``.
+
+``qweight`` is registered as a buffer (the reference keeps it as a plain
+attribute, ``quant_linear.py:57,81``), so ``module.to(device)`` moves the codes
+together with ``scales`` and ``qzeros`` and ``state_dict`` keeps them.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import nn
+
+from llmopt.quantization.quantizers import QuantizedTensor, dequantize
+from llmopt.utils.logging import get_logger
+
+__all__ = ["QuantLinear", "QuantLinearConfig", "quantize_model_", "replace_linear_modules"]
+
+logger = get_logger("quant.nn")
+
+
+class QuantLinearConfig:
+    """Bit width, group size, grid symmetry and compute dtype of a :class:`QuantLinear`.
+
+    Defaults follow ``quant_linear.py:18-33``: 4 bits, group 128, symmetric, fp16.
+    """
+
+    __slots__ = ("bits", "compute_dtype", "group_size", "symmetric")
+
+    def __init__(
+        self,
+        bits: int = 4,
+        group_size: int = 128,
+        symmetric: bool = True,
+        compute_dtype: torch.dtype = torch.float16,
+    ) -> None:
+        self.bits = bits
+        self.group_size = group_size
+        self.symmetric = symmetric
+        self.compute_dtype = compute_dtype
+
+
+class QuantLinear(nn.Module):
+    """Linear layer over a packed :class:`QuantizedTensor` weight.
+
+    ``forward(x)`` equals ``F.linear(x, dequantize(weight, compute_dtype), bias)``;
+    ``x`` (and ``bias``) must already be in ``compute_dtype``, as ``F.linear``
+    requires of its operands.
+    """
+
+    def __init__(
+        self,
+        in_features: int,
+        out_features: int,
+        config: QuantLinearConfig | None = None,
+        bias: bool = True,
+        device: torch.device | str | None = None,
+    ) -> None:
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.config = config or QuantLinearConfig()
+        self.register_buffer("qweight", None)
+        self.register_buffer("qzeros", torch.zeros(0), persistent=True)
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_features, device=device))
+        else:
+            self.register_buffer("bias", None)
+        self._cached_weight: torch.Tensor | None = None
+
+    @classmethod
+    def from_float(
+        cls,
+        linear: nn.Linear,
+        quantized: QuantizedTensor,
+        compute_dtype: torch.dtype | None = None,
+    ) -> QuantLinear:
+        """Wrap ``quantized`` with the geometry and bias of ``linear`` (``quant_linear.py:66-87``)."""
+        config = QuantLinearConfig(
+            bits=quantized.bits,
+            group_size=quantized.group_size,
+            symmetric=quantized.symmetric,
+            compute_dtype=compute_dtype or linear.weight.dtype,
+        )
+        module = cls(linear.in_features, linear.out_features, config, bias=linear.bias is not None)
+        module.qweight = quantized.qweight
+        module.register_buffer("scales", quantized.scales)
+        module.register_buffer("qzeros", quantized.zeros)
+        if linear.bias is not None:
+            module.bias.data = linear.bias.data.clone()  # type: ignore[union-attr]
+        module.invalidate()
+        return module
+
+    def invalidate(self) -> None:
+        """Forget the host-side dense weight; the next host forward rebuilds it."""
+        self._cached_weight = None
+
+    def _apply(self, fn, recurse: bool = True):  # noqa: ANN001, ANN202 - nn.Module signature
+        self._cached_weight = None
+        return super()._apply(fn, recurse)
+
+    def quantized_tensor(self) -> QuantizedTensor:
+        """The packed weight as a :class:`QuantizedTensor` view of this module's buffers."""
+        if self.qweight is None or not hasattr(self, "scales"):
+            raise RuntimeError("QuantLinear has no quantized weight; call from_float()")
+        return QuantizedTensor(
+            qweight=self.qweight,
+            scales=self.scales,  # type: ignore[arg-type]
+            zeros=self.qzeros,
+            bits=self.config.bits,
+            group_size=self.config.group_size,
+            symmetric=self.config.symmetric,
+            shape=(self.out_features, self.in_features),
+        )
+
+    def _dequantized_weight(self) -> torch.Tensor:
+        """Dense ``[out, in]`` weight in ``compute_dtype`` (cached on the host)."""
+        if self._cached_weight is None:
+            tensor = self.quantized_tensor()
+            weight = dequantize(tensor, self.config.compute_dtype)
+            if tensor.qweight.device.type == "cuda":
+                return weight
+            self._cached_weight = weight.to(tensor.qweight.device)
+        return self._cached_weight
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.device.type == "cuda":
+            from llmopt.kernels import ops
+
+            return ops.quant_linear(x, self.quantized_tensor(), self.bias, self.config.compute_dtype)
+        return torch.nn.functional.linear(x, self._dequantized_weight(), self.bias)
+
+    def extra_repr(self) -> str:
+        return (
+            f"in_features={self.in_features}, out_features={self.out_features}, "
+            f"bits={self.config.bits}, bias={self.bias is not None}"
+        )
+
+
+def replace_linear_modules(
+    model: nn.Module,
+    replacements: dict[nn.Module, nn.Module],
+) -> nn.Module:
+    """Swap every child found in ``replacements`` for its value, in place."""
+    if not replacements:
+        return model
+    located: dict[nn.Module, tuple[nn.Module, str]] = {}
+    for parent in model.modules():
+        for name, child in parent.named_children():
+            if child in replacements:
+                located[child] = (parent, name)
+    for child, (parent, name) in located.items():
+        setattr(parent, name, replacements[child])
+    return model
+
+
+def quantize_model_(
+    model: nn.Module,
+    *,
+    bits: int = 4,
+    group_size: int = 128,
+    symmetric: bool = True,
+    strategy: str = "rtn",
+    calibration_batches: list[torch.Tensor] | None = None,
+    ignore_layers: tuple[str, ...] = ("lm_head", "embed_tokens"),
+    inplace: bool = True,
+) -> nn.Module:
+    """Replace every eligible ``nn.Linear`` with a :class:`QuantLinear` (``quant_linear.py:139-207``).
+
+    Layers whose name contains an ``ignore_layers`` token stay dense. When the
+    group size does not divide ``in_features`` the layer uses
+    ``gcd(in_features, group_size)`` instead. With ``strategy="gptq"`` and
+    calibration batches, per-layer Hessians are collected with forward hooks
+    (collection stops at the first batch the model cannot run). ``inplace`` is
+    accepted for API parity; the model is always modified in place.
+    """
+    from llmopt.quantization.quantizers import build_quantizer
+
+    del inplace
+    targets: list[tuple[str, nn.Linear]] = []
+    for name, module in model.named_modules():
+        if not isinstance(module, nn.Linear):
+            continue
+        if any(token in name for token in ignore_layers):
+            continue
+        if module.in_features % group_size:
+            logger.debug(
+                "%s: in_features=%d is not a multiple of group_size=%d, using %d instead",
+                name,
+                module.in_features,
+                group_size,
+                math.gcd(module.in_features, group_size),
+            )
+        targets.append((name, module))
+
+    hessians: dict[nn.Module, torch.Tensor] = {}
+    if strategy == "gptq" and calibration_batches:
+        from llmopt.quantization.calibration import HessianCollector
+
+        for _, module in targets:
+            with HessianCollector([module], device=module.weight.device) as collector:
+                for batch in calibration_batches:
+                    try:
+                        model(batch.to(module.weight.device))
+                    except Exception:  # noqa: BLE001 - calibration is best effort
+                        break
+                hessians.update(collector.results())
+
+    replacements: dict[nn.Module, nn.Module] = {}
+    for _, module in targets:
+        group = math.gcd(module.in_features, group_size) or group_size
+        quantizer = build_quantizer(strategy, bits=bits, group_size=group, symmetric=symmetric)
+        quantized = quantizer.quantize(module.weight.detach().to(torch.float32), hessians.get(module))
+        replacements[module] = QuantLinear.from_float(
+            module, quantized, compute_dtype=module.weight.dtype
+        )
+        module.weight.data = quantized.dequantize().to(module.weight.dtype)
+
+    replace_linear_modules(model, replacements)
+    return model

@@ -1,0 +1,299 @@
+"""Parity of the gfx950 kernels with the CPU oracle, through the C ABI.
+
+* unpack and dequantize: bit-exact with the oracle for every bit width, grid, group
+  size and output dtype (fp32 exactly; bf16/fp16 as the round-to-nearest-even cast of
+  the oracle's fp32 value).
+* quantized linear (every kernel: generic, decode, prefill, and the automatic choice):
+  max|y - y_ref| / max|y_ref| <= 1e-2 for bf16/fp16 and <= 2e-3 for fp32, where y_ref is
+  the reference's own sequence (oracle dequantization, cast to the compute dtype,
+  ``F.linear`` on the CPU). At full Llama-3-8B projection sizes the check uses sampled
+  output columns, a torch fp32 GPU matmul of the bit-exact dequantized weight, and two
+  size-independent properties: one-hot activation rows must return the dequantized
+  weight column bit for bit, and scaling x by 2 must scale y by 2 exactly.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from llmopt.kernels import ops
+from llmopt.kernels._lib import ALGO_AUTO, ALGO_DECODE, ALGO_GENERIC, ALGO_PREFILL
+from llmopt.quantization import QuantizedTensor, RoundToNearestQuantizer, dequantize, unpack_int4
+from oracle import quant_oracle as qo
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+NP_NAMES = {torch.float32: "float32", torch.float16: "float16", torch.bfloat16: "bfloat16"}
+TOL = {torch.float32: 2e-3, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+
+
+def _host_qt(rows, cols, bits, group, symmetric, seed, scale=0.02):
+    gen = torch.Generator().manual_seed(seed)
+    w = torch.randn(rows, cols, generator=gen) * scale
+    return RoundToNearestQuantizer(bits, group, symmetric).quantize(w)
+
+
+def _to_device(qt: QuantizedTensor) -> QuantizedTensor:
+    return QuantizedTensor(
+        qweight=qt.qweight.to(DEV),
+        scales=qt.scales.to(DEV),
+        zeros=qt.zeros.to(DEV),
+        bits=qt.bits,
+        group_size=qt.group_size,
+        symmetric=qt.symmetric,
+        shape=qt.shape,
+    )
+
+
+def _oracle_dense(qt: QuantizedTensor) -> np.ndarray:
+    return qo.dequantize(
+        qt.qweight.cpu().numpy(), qt.scales.cpu().numpy(), qt.zeros.cpu().numpy(),
+        qt.bits, qt.group_size, qt.symmetric, qt.shape,
+    )
+
+
+def _bits_of(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu()
+    if t.dtype == torch.float32:
+        return t.view(torch.int32).numpy()
+    return t.view(torch.int16).numpy()
+
+
+def _expected_bits(dense32: np.ndarray, dtype: torch.dtype) -> np.ndarray:
+    if dtype == torch.float32:
+        return dense32.view(np.int32)
+    if dtype == torch.bfloat16:
+        return qo.bf16_bits(dense32).view(np.int16)
+    return dense32.astype(np.float16).view(np.int16)
+
+
+def _rel_err(y: torch.Tensor, ref: torch.Tensor) -> float:
+    y = y.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    denom = float(ref.abs().max())
+    return float((y - ref).abs().max()) / (denom if denom > 0 else 1.0)
+
+
+def _reference_linear(x_cpu, dense32, bias_cpu, dtype, cols=None):
+    """The reference's sequence: dense weight cast to compute dtype, then F.linear on the CPU."""
+    w = torch.from_numpy(qo.round_to_dtype(dense32 if cols is None else dense32[cols], NP_NAMES[dtype]))
+    b = None if bias_cpu is None else (bias_cpu if cols is None else bias_cpu[cols])
+    return qo.reference_linear(x_cpu, w.to(dtype), b)
+
+
+# ---- unpack ------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize(
+    "shape,columns",
+    [((4, 8), 16), ((3, 88), 176), ((5, 7), 13), ((2, 3, 16), 32), ((4096, 2048), 4096), ((1, 256), 512), ((6, 10), 4)],
+)
+def test_unpack_bit_exact(shape, columns):
+    gen = torch.Generator().manual_seed(sum(shape) + columns)
+    packed = torch.randint(0, 256, shape, generator=gen, dtype=torch.int32).to(torch.uint8)
+    got = unpack_int4(packed.to(DEV), columns)
+    np.testing.assert_array_equal(got.cpu().numpy(), qo.unpack_nibbles(packed.numpy(), columns))
+
+
+def test_unpack_every_byte_value_and_views():
+    packed = torch.arange(256, dtype=torch.int32).to(torch.uint8).reshape(1, 256)
+    np.testing.assert_array_equal(unpack_int4(packed.to(DEV), 512).cpu().numpy(), qo.unpack_nibbles(packed.numpy(), 512))
+    # A transposed (non-contiguous) input is read through its values, like the reference.
+    base = torch.randint(0, 256, (16, 12), dtype=torch.int32).to(torch.uint8)
+    view = base.to(DEV).t()
+    np.testing.assert_array_equal(unpack_int4(view, 32).cpu().numpy(), qo.unpack_nibbles(base.t().numpy(), 32))
+
+
+# ---- dequantize --------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("symmetric", [False, True])
+@pytest.mark.parametrize("rows,cols,group", [(48, 256, 128), (64, 176, 16), (33, 96, 32), (16, 512, 0)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_dequant_bit_exact(bits, symmetric, rows, cols, group, dtype):
+    qt = _host_qt(rows, cols, bits, group if group else cols, symmetric, seed=rows + cols + bits)
+    if group == 0:
+        qt = QuantizedTensor(qt.qweight, qt.scales, qt.zeros, qt.bits, 0, qt.symmetric, qt.shape)
+    got = dequantize(_to_device(qt), dtype)
+    assert got.dtype == dtype and got.shape == (rows, cols)
+    np.testing.assert_array_equal(_bits_of(got), _expected_bits(_oracle_dense(qt), dtype))
+
+
+def test_dequant_extreme_scales_bit_exact():
+    # Denormal products, bf16 overflow to infinity and non-integer zero points.
+    qt = _host_qt(8, 128, 4, 32, False, seed=5)
+    scales = qt.scales.clone()
+    scales[0] = 1e-41
+    scales[1] = 3e37
+    scales[2] = -0.37
+    zeros = qt.zeros.clone()
+    zeros[3] = 2.5
+    odd = QuantizedTensor(qt.qweight, scales, zeros, 4, 32, False, qt.shape)
+    dense = _oracle_dense(odd)
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
+        np.testing.assert_array_equal(_bits_of(dequantize(_to_device(odd), dtype)), _expected_bits(dense, dtype))
+
+
+def test_dequant_full_size_gate_up_bit_exact():
+    qt = _host_qt(28672, 4096, 4, 128, False, seed=0)
+    got = dequantize(_to_device(qt), torch.bfloat16)
+    np.testing.assert_array_equal(_bits_of(got), _expected_bits(_oracle_dense(qt), torch.bfloat16))
+
+
+# ---- quantized linear: small shapes against the CPU reference sequence ------------------------
+
+SMALL_SHAPES = [  # (N, K, group)
+    (48, 256, 128),
+    (32, 64, 64),  # tiny-model k/v projection
+    (64, 176, 16),  # tiny-model down_proj: 88-byte packed rows
+    (200, 512, 128),  # N not a multiple of any tile
+    (96, 384, 64),
+]
+
+
+@pytest.mark.parametrize("algo", [ALGO_AUTO, ALGO_GENERIC, ALGO_DECODE, ALGO_PREFILL])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("bits,symmetric", [(4, False), (4, True), (8, False), (8, True), (2, False)])
+@pytest.mark.parametrize("n,k,group", SMALL_SHAPES)
+@pytest.mark.parametrize("m", [1, 5, 16, 33, 64, 200])
+def test_linear_small_shapes(algo, dtype, bits, symmetric, n, k, group, m):
+    qt = _host_qt(n, k, bits, group, symmetric, seed=n * 7 + k + bits)
+    gen = torch.Generator().manual_seed(m + n)
+    x = torch.randn(m, k, generator=gen).to(dtype)
+    try:
+        y = ops.quant_linear(x.to(DEV), _to_device(qt), None, dtype, algo=algo)
+    except NotImplementedError:
+        assert algo in (ALGO_DECODE, ALGO_PREFILL)  # outside that kernel's envelope
+        if algo == ALGO_DECODE:
+            assert m > 64 or dtype == torch.float32 or group % 64 or k % 64
+        return
+    ref = _reference_linear(x, _oracle_dense(qt), None, dtype)
+    assert y.dtype == dtype and y.shape == (m, n)
+    assert _rel_err(y, ref) <= TOL[dtype], (algo, dtype, bits, symmetric, n, k, m)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [1, 40, 300])
+def test_linear_bias_and_leading_dims(dtype, m):
+    qt = _host_qt(96, 256, 4, 128, False, seed=3)
+    gen = torch.Generator().manual_seed(m)
+    x = torch.randn(m, 256, generator=gen).to(dtype)
+    bias = torch.randn(96, generator=gen).to(dtype)
+    y = ops.quant_linear(x.to(DEV).reshape(1, m, 256), _to_device(qt), bias.to(DEV), dtype)
+    ref = _reference_linear(x, _oracle_dense(qt), bias, dtype)
+    assert y.shape == (1, m, 96)
+    assert _rel_err(y.reshape(m, 96), ref) <= TOL[dtype]
+
+
+def test_linear_strided_and_one_dimensional_inputs():
+    qt = _host_qt(64, 256, 4, 128, True, seed=8)
+    dqt = _to_device(qt)
+    big = torch.randn(7, 512).to(torch.bfloat16)
+    strided = big.to(DEV)[:, 128:384]  # row stride 512, 16-byte aligned start
+    y = ops.quant_linear(strided, dqt, None, torch.bfloat16)
+    ref = _reference_linear(big[:, 128:384].contiguous(), _oracle_dense(qt), None, torch.bfloat16)
+    assert _rel_err(y, ref) <= 1e-2
+    odd = big.to(DEV)[:, 3:259]  # misaligned start: taken by the generic kernel
+    ref_odd = _reference_linear(big[:, 3:259].contiguous(), _oracle_dense(qt), None, torch.bfloat16)
+    assert _rel_err(ops.quant_linear(odd, dqt, None, torch.bfloat16), ref_odd) <= 1e-2
+    v = torch.randn(256).to(torch.bfloat16)
+    y1 = ops.quant_linear(v.to(DEV), dqt, None, torch.bfloat16)
+    assert y1.shape == (64,)
+    assert _rel_err(y1, _reference_linear(v[None], _oracle_dense(qt), None, torch.bfloat16)[0]) <= 1e-2
+
+
+def test_linear_empty_batch_and_errors():
+    dqt = _to_device(_host_qt(32, 128, 4, 64, False, seed=1))
+    y = ops.quant_linear(torch.empty(0, 128, dtype=torch.bfloat16, device=DEV), dqt, None, torch.bfloat16)
+    assert y.shape == (0, 32)
+    with pytest.raises(RuntimeError):
+        ops.quant_linear(torch.randn(2, 128, device=DEV), dqt, None, torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        ops.quant_linear(torch.randn(2, 100, device=DEV, dtype=torch.bfloat16), dqt, None, torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        bad_bias = torch.zeros(32, device=DEV)
+        ops.quant_linear(torch.randn(2, 128, device=DEV, dtype=torch.bfloat16), dqt, bad_bias, torch.bfloat16)
+
+
+def test_linear_is_deterministic():
+    dqt = _to_device(_host_qt(4096, 4096, 4, 128, False, seed=2))
+    for m in (1, 32, 512):
+        x = torch.randn(m, 4096, device=DEV).to(torch.bfloat16)
+        a = ops.quant_linear(x, dqt, None, torch.bfloat16)
+        b = ops.quant_linear(x, dqt, None, torch.bfloat16)
+        assert torch.equal(a, b)
+
+
+# ---- full Llama-3-8B projection sizes ---------------------------------------------------------
+
+PROJECTIONS = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (28672, 4096), "down": (4096, 14336)}
+
+
+@pytest.fixture(scope="module")
+def projections():
+    out = {}
+    for i, (name, (n, k)) in enumerate(PROJECTIONS.items()):
+        qt = _host_qt(n, k, 4, 128, False, seed=i)
+        out[name] = (qt, _to_device(qt), _oracle_dense(qt))
+    return out
+
+
+@pytest.mark.parametrize("name", list(PROJECTIONS))
+@pytest.mark.parametrize("m", [1, 8, 32, 64, 256, 2048])
+def test_projection_sampled_columns_and_gpu_fp32(projections, name, m):
+    qt, dqt, dense = projections[name]
+    n, k = qt.shape
+    gen = torch.Generator().manual_seed(m)
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16)
+    y = ops.quant_linear(x.to(DEV), dqt, None, torch.bfloat16)
+    cols = np.sort(np.random.default_rng(m).choice(n, size=256, replace=False))
+    ref = _reference_linear(x, dense, None, torch.bfloat16, cols=cols)
+    assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= 1e-2
+    w32 = dequantize(dqt, torch.bfloat16).float()  # bit-exact (checked above)
+    ref_gpu = torch.matmul(x.to(DEV).float(), w32.t().contiguous())
+    assert _rel_err(y, ref_gpu) <= 1e-2
+
+
+@pytest.mark.parametrize("name", list(PROJECTIONS))
+@pytest.mark.parametrize("m", [1, 64, 2048])
+def test_projection_one_hot_rows_return_weight_columns(projections, name, m):
+    _, dqt, dense = projections[name]
+    n, k = dense.shape
+    picks = np.random.default_rng(k + m).choice(k, size=m, replace=m > k)
+    x = torch.zeros(m, k, dtype=torch.bfloat16)
+    x[torch.arange(m), torch.from_numpy(picks)] = 1.0
+    y = ops.quant_linear(x.to(DEV), dqt, None, torch.bfloat16)
+    expect = qo.bf16_bits(np.ascontiguousarray(dense[:, picks].T)).view(np.int16)
+    np.testing.assert_array_equal(_bits_of(y), expect)
+
+
+@pytest.mark.parametrize("m", [1, 32, 2048])
+def test_projection_scaling_by_two_is_exact(projections, m):
+    _, dqt, _ = projections["down"]
+    x = torch.randn(m, 14336, device=DEV).to(torch.bfloat16)
+    y1 = ops.quant_linear(x, dqt, None, torch.bfloat16)
+    y2 = ops.quant_linear(x * 2, dqt, None, torch.bfloat16)
+    assert torch.equal(y2, y1 * 2)
+
+
+@pytest.mark.parametrize("bits,symmetric,m", [(8, False, 1), (8, False, 32), (8, False, 2048), (2, False, 1), (2, False, 2048), (8, True, 32)])
+def test_down_projection_bit_width_sweep(bits, symmetric, m):
+    qt = _host_qt(4096, 14336, bits, 128, symmetric, seed=bits)
+    dqt = _to_device(qt)
+    dense = _oracle_dense(qt)
+    x = torch.randn(m, 14336, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    y = ops.quant_linear(x.to(DEV), dqt, None, torch.bfloat16)
+    cols = np.sort(np.random.default_rng(bits + m).choice(4096, size=128, replace=False))
+    ref = _reference_linear(x, dense, None, torch.bfloat16, cols=cols)
+    assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= 1e-2
+
+
+def test_fp32_compute_single_linear_config():
+    # The reference's CPU configuration: K = N = 4096, fp32, M = 1, RTN b4 asym g128.
+    qt = _host_qt(4096, 4096, 4, 128, False, seed=0)
+    x = torch.randn(1, 4096, generator=torch.Generator().manual_seed(1))
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None, torch.float32)
+    ref = _reference_linear(x, _oracle_dense(qt), None, torch.float32)
+    assert _rel_err(y, ref) <= 2e-3

@@ -1,0 +1,192 @@
+"""QuantLinear and the model-wide helpers on the host, against the reference's contract.
+
+Includes the reference's own quantization tests (tests/test_engine_and_serving.py:73-96),
+run on a small decoder-shaped model with the same awkward shapes as the reference's tiny
+preset: hidden 64, FFN 176 (so group 64 falls back to gcd(176, 64) = 16 and the packed
+row of down_proj is 88 bytes), and 32-wide k/v projections.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from llmopt.quantization import (
+    QuantLinear,
+    QuantLinearConfig,
+    RoundToNearestQuantizer,
+    quantize_model_,
+    replace_linear_modules,
+)
+from llmopt.quantization.calibration import (
+    CalibrationHarness,
+    HessianCollector,
+    apply_quantization,
+)
+from oracle import quant_oracle as qo
+
+
+class _Block(nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.q_proj = nn.Linear(64, 64, bias=False)
+        self.k_proj = nn.Linear(64, 32, bias=False)
+        self.v_proj = nn.Linear(64, 32, bias=False)
+        self.o_proj = nn.Linear(64, 64, bias=False)
+        self.gate_proj = nn.Linear(64, 176, bias=False)
+        self.up_proj = nn.Linear(64, 176, bias=False)
+        self.down_proj = nn.Linear(176, 64, bias=False)
+
+    def forward(self, h: torch.Tensor) -> torch.Tensor:
+        q, k, v = self.q_proj(h), self.k_proj(h), self.v_proj(h)
+        mix = torch.cat([k, v], dim=-1) * q.sigmoid()
+        h = h + self.o_proj(mix)
+        return h + self.down_proj(torch.nn.functional.silu(self.gate_proj(h)) * self.up_proj(h))
+
+
+class TinyDecoder(nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.embed_tokens = nn.Embedding(256, 64)
+        self.layers = nn.ModuleList([_Block(), _Block()])
+        self.lm_head = nn.Linear(64, 256, bias=False)
+        for p in self.parameters():
+            with torch.no_grad():
+                p.copy_(torch.randn_like(p) * 0.02)
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        h = self.embed_tokens(ids)
+        for layer in self.layers:
+            h = layer(h)
+        return self.lm_head(h)
+
+
+def _tiny():
+    torch.manual_seed(0)
+    return TinyDecoder()
+
+
+def test_quantize_model_replaces_linears_and_shrinks_storage():
+    model = _tiny()
+    float_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    quantize_model_(model, bits=4, group_size=64)
+    layers = [m for m in model.modules() if isinstance(m, QuantLinear)]
+    assert len(layers) == 14
+    assert isinstance(model.lm_head, nn.Linear) and not isinstance(model.lm_head, QuantLinear)
+    packed = sum(
+        m.qweight.numel() * m.qweight.element_size()
+        + m.scales.numel() * m.scales.element_size()
+        + m.qzeros.numel() * m.qzeros.element_size()
+        for m in layers
+    )
+    assert packed < float_bytes
+    down = model.layers[0].down_proj
+    assert down.config.group_size == 16 and down.qweight.shape == (64, 88)
+
+
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_quantized_model_still_runs(bits):
+    model = _tiny()
+    quantize_model_(model, bits=bits, group_size=64)
+    out = model(torch.randint(0, 256, (1, 8)))
+    assert torch.isfinite(out).all()
+
+
+def test_forward_equals_reference_sequence():
+    torch.manual_seed(1)
+    linear = nn.Linear(256, 48, bias=True)
+    qt = RoundToNearestQuantizer(4, 128, False).quantize(linear.weight.detach())
+    module = QuantLinear.from_float(linear, qt)
+    x = torch.randn(5, 256)
+    dense = qo.dequantize(qt.qweight.numpy(), qt.scales.numpy(), qt.zeros.numpy(), 4, 128, False, (48, 256))
+    expect = qo.reference_linear(x, torch.from_numpy(dense), linear.bias.detach())
+    torch.testing.assert_close(module(x), expect, rtol=0, atol=0)
+    assert module.config.compute_dtype == torch.float32
+    assert module(x[0]).shape == (48,)
+    assert module(torch.randn(2, 3, 256)).shape == (2, 3, 48)
+
+
+def test_forward_errors_follow_f_linear():
+    linear = nn.Linear(64, 16, bias=False)
+    qt = RoundToNearestQuantizer(4, 64, True).quantize(linear.weight.detach())
+    module = QuantLinear.from_float(linear, qt, compute_dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        module(torch.randn(2, 64))  # fp32 input, bf16 compute dtype
+    assert module(torch.randn(2, 64, dtype=torch.bfloat16)).dtype == torch.bfloat16
+    empty = QuantLinear(64, 16)
+    with pytest.raises(RuntimeError, match="no quantized weight"):
+        empty(torch.randn(1, 64, dtype=torch.float16))
+
+
+def test_constructor_defaults_and_repr():
+    module = QuantLinear(32, 8)
+    cfg = module.config
+    assert (cfg.bits, cfg.group_size, cfg.symmetric, cfg.compute_dtype) == (4, 128, True, torch.float16)
+    assert module.qweight is None and module.qzeros.numel() == 0
+    assert isinstance(module.bias, nn.Parameter) and module.bias.shape == (8,)
+    assert QuantLinear(32, 8, bias=False).bias is None
+    assert module.extra_repr() == "in_features=32, out_features=8, bits=4, bias=True"
+    cfg2 = QuantLinearConfig(bits=8, group_size=64, symmetric=False, compute_dtype=torch.bfloat16)
+    with pytest.raises(AttributeError):
+        cfg2.extra = 1  # __slots__
+
+
+def test_cache_invalidate_and_state_dict():
+    linear = nn.Linear(64, 16, bias=False)
+    qt = RoundToNearestQuantizer(8, 32, True).quantize(linear.weight.detach())
+    module = QuantLinear.from_float(linear, qt)
+    x = torch.randn(1, 64)
+    module(x)
+    assert module._cached_weight is not None
+    module.invalidate()
+    assert module._cached_weight is None
+    state = module.state_dict()
+    assert {"qweight", "scales", "qzeros"} <= set(state)
+    assert state["qweight"].dtype == torch.int8
+    # Moving or casting the module drops the host cache and leaves the codes untouched.
+    module(x)
+    module.to(torch.float64)
+    assert module._cached_weight is None and module.qweight.dtype == torch.int8
+
+
+def test_replace_linear_modules_swaps_children():
+    model = nn.Sequential(nn.Linear(4, 4), nn.ReLU(), nn.Linear(4, 2))
+    new = nn.Identity()
+    replace_linear_modules(model, {model[2]: new})
+    assert model[2] is new
+    assert replace_linear_modules(model, {}) is model
+
+
+def test_gptq_strategy_with_calibration_batches():
+    model = _tiny()
+    batches = CalibrationHarness(num_samples=2, seq_length=16, seed=3).synthetic(256)
+    quantize_model_(model, bits=4, group_size=64, strategy="gptq", calibration_batches=batches)
+    assert isinstance(model.layers[1].up_proj, QuantLinear)
+    assert torch.isfinite(model(batches[0])).all()
+
+
+def test_hessian_collector_closed_form():
+    layer = nn.Linear(8, 4)
+    x1, x2 = torch.randn(3, 8), torch.randn(2, 5, 8)
+    with HessianCollector([layer]) as collector:
+        layer(x1)
+        layer(x2)
+    rows = torch.cat([x1, x2.reshape(-1, 8)])
+    torch.testing.assert_close(collector.hessian_for(layer), (2.0 / 13) * rows.T @ rows)
+    assert collector.count == 2 and layer in collector.results()
+    assert HessianCollector([nn.Linear(2, 2)]).hessian_for(layer) is None
+
+
+def test_apply_quantization_writes_dequantized_weights():
+    model = _tiny()
+    before = model.layers[0].q_proj.weight.detach().clone()
+    result = apply_quantization(model, strategy="rtn", bits=4, group_size=16)
+    after = model.layers[0].q_proj.weight.detach()
+    qt = result.quantizers["layers.0.q_proj"]
+    np.testing.assert_array_equal(after.numpy(), qt.dequantize().numpy())
+    assert result.per_layer_error["layers.0.q_proj"] > 0
+    assert not torch.equal(before, after)
+    assert result.compression_ratio > 1 and "layers to 4-bit" in result.summary()
+    assert "quantized=rtn-4bit" in repr(model.layers[0].q_proj)
