@@ -93,6 +93,24 @@ __device__ __forceinline__ float dequant_exact(float q, float z, float s) {
   return __fmul_rn(d, s);
 }
 
+// ---- buffer loads ---------------------------------------------------------------------------------
+// A raw buffer resource over `bytes` bytes at `base` (gfx9 data format word). Loads take a
+// per-lane 32-bit byte offset plus a wave-uniform one; addressing stays 32-bit, which keeps
+// one VGPR per stream instead of a 64-bit pointer.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, int(bytes), 0x00020000);
+}
+// Streaming loads are marked volatile (bit 31 of the cache-policy operand, a compiler-only flag):
+// they then stay in program order, where a prefetch ring puts them, instead of being sunk next
+// to their first use, which would expose the full memory latency on every use.
+constexpr int kLoadInOrder = int(0x80000000u);
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), kLoadInOrder);
+}
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(voff), int(soff), kLoadInOrder));
+}
+
 // Fast exact division of small non-negative integers by a runtime divisor (< 2^16, dividend
 // < 2^16): q = umulhi(c, ceil(2^32 / d)). A divisor of 1 is encoded as magic 0.
 __device__ __forceinline__ uint32_t div_small(uint32_t c, uint32_t magic) {

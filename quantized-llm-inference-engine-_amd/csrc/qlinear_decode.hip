@@ -71,6 +71,31 @@ struct Codes<Act, kNibble> {
   }
 };
 
+// The same nibble operand with the mask in a VGPR and the magic in an SGPR, so each pair is a
+// single v_and_or_b32 (gfx9 VOP3 takes no literal and one scalar operand): 7 VALU ops per 8
+// codes instead of 11.
+struct NibbleConsts {
+  uint32_t mask;   // 0x000F000F, VGPR
+  uint32_t magic;  // Act::kNibbleMagic2, SGPR
+  template <class Act>
+  __device__ static NibbleConsts make(uint32_t opaque_zero) {
+    NibbleConsts c;
+    c.mask = 0x000F000Fu | opaque_zero;
+    c.magic = Act::kNibbleMagic2 | opaque_zero;
+    asm("" : "+v"(c.mask));
+    asm("" : "+s"(c.magic));
+    return c;
+  }
+  __device__ u32x4 operand(uint32_t d) const {
+    u32x4 r;
+    r.x = (d & mask) | magic;
+    r.y = ((d >> 4) & mask) | magic;
+    r.z = ((d >> 8) & mask) | magic;
+    r.w = ((d >> 12) & mask) | magic;
+    return r;
+  }
+};
+
 template <>
 struct Codes<ActF16, kByte> {
   static constexpr float kOffset = 1024.0f;
@@ -292,6 +317,431 @@ __global__ void __launch_bounds__(NW * 64)
   }
 }
 
+// ---- streaming kernel (small M) ---------------------------------------------------------------
+//
+// One workgroup owns NTT tiles of 16 output features and all of K; its NW waves split K by
+// steps (one step = 64 packed bytes per row), interleaved so that at any moment the waves
+// read adjacent bytes of the same rows.
+//
+// * Everything but the codes is staged into LDS once, at the start, with wide coalesced loads:
+//   the activation block x[M, K] (permuted into the MFMA operand order), the per-step sums
+//   sum_k x[m, k] that the zero-point correction needs, and the workgroup's slice of scales
+//   and zeros (a contiguous block of rows, interleaved as (s, z) pairs). Reading scales and
+//   zeros from memory per step instead -- one 4-byte lane load per row and step -- doubles the
+//   kernel time: those loads touch as many cache lines as the codes themselves.
+// * Codes stream through a ring of P = NTT*Q register slots per lane: a slot holds the 16
+//   bytes of one (step, tile) item and is refilled with the item P positions ahead as soon as
+//   it has been consumed. Every refill is issued unconditionally (positions past the end
+//   re-read the last step), so the loads form one static sequence and the in-order completion
+//   counter lets each wave keep P items (P KB) in flight.
+// * Per-wave partial sums are combined through LDS in a fixed wave order.
+constexpr size_t kStreamLds = 96 * 1024;
+constexpr int kStageBatch = 8;  // 16-byte activation pieces staged per thread, at most
+constexpr int kMetaBatch = 2;   // 16-byte scale (and zero) pieces staged per thread, at most
+
+template <int FMT>
+struct StreamGeom {
+  using C = Chunk<FMT, 16>;
+  static constexpr int kNM = C::kMfma;         // 16-byte activation pieces per lane and step
+  static constexpr int kStepPieces = 4 * kNM;  // pieces per activation row and step
+  // LDS layout: x [M][steps*kStepPieces + 1] 16-byte pieces, then kNM zero pieces that lanes
+  // of rows m >= M read instead | xsum [steps][16] floats (rows m >= M zero) |
+  // meta [rows][2G + 2] floats. Row paddings keep lanes of different rows on different banks.
+  __host__ __device__ static size_t x_pieces(int64_t M, int64_t steps) {
+    return size_t(M) * size_t(steps * kStepPieces + 1) + kNM;
+  }
+  __host__ __device__ static size_t xsum_floats(int64_t steps) { return size_t(steps) * 16; }
+  static size_t lds_bytes(int64_t M, int64_t steps, int64_t G, int ntt) {
+    return x_pieces(M, steps) * 16 + xsum_floats(steps) * 4 + size_t(ntt) * 16 * (2 * G + 2) * 4;
+  }
+};
+
+// RM: output rows per lane that carry data (1 when M == 1, else 4; the MFMA output gives each
+// lane rows 4*(lane/16) + r, r < 4).
+template <class Act, int FMT, int NTT, int Q, int NW, int RM>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4, 8)))
+    decode_stream_kernel(const LinearArgs a, int steps, uint32_t group_magic) {
+  using Geo = StreamGeom<FMT>;
+  using C = typename Geo::C;
+  using Raw = typename Act::raw;
+  using Op = Codes<Act, FMT>;
+  constexpr int NM = Geo::kNM;
+  constexpr int P = NTT * Q;
+  constexpr int kThreads = NW * 64;
+
+  extern __shared__ u32x4 lds[];
+  const int M = int(a.M);
+  const int G = int(a.G);
+  const int row_pieces = steps * Geo::kStepPieces;
+  const int kRow = row_pieces + 1;
+  u32x4* const zero_lds = lds + Geo::x_pieces(M, steps) - NM;
+  float* const xsum_lds = reinterpret_cast<float*>(lds + Geo::x_pieces(M, steps));  // [steps][16]
+  float* const meta_lds = xsum_lds + Geo::xsum_floats(steps);  // [NTT*16][2G+2]: (s, z) pairs
+  const int meta_row = 2 * G + 2;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;
+  const int kq = lane >> 4;
+  const int64_t tile0 = int64_t(blockIdx.x) * NTT;
+  const bool asym = !a.symmetric;
+  const int my_steps = steps / NW;  // the host guarantees NW | steps
+
+  // Per-lane byte offset of this lane's row in each tile (rows past N repeat row N-1; their
+  // sums are never stored). The step offset is wave-uniform and goes in the scalar slot.
+  const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
+  uint32_t qoff[NTT];
+#pragma unroll
+  for (int t = 0; t < NTT; ++t) {
+    int64_t n = (tile0 + t) * 16 + col;
+    n = n < a.N ? n : a.N - 1;
+    qoff[t] = uint32_t(n * a.ldq + kq * 16);
+  }
+
+  u32x4 ring[P];
+  // Item (q, t): this wave's q-th step (global step q*NW + wave) of tile t.
+  auto load_item = [&](int p, int q) {
+    q = q < my_steps ? q : my_steps - 1;
+    ring[p] = buf_load16(wq, qoff[p % NTT], uint32_t(q * NW + wave) * C::kBytes);
+  };
+
+  // ---- prologue: the ring's first P items, then the activation and metadata loads ----
+  // (the staging data is waited for once, behind the ring loads, which are then in hand
+  // when the main loop starts)
+#pragma unroll
+  for (int p = 0; p < P; ++p) load_item(p, p / NTT);
+  const Raw* xg = static_cast<const Raw*>(a.x);
+  const int pieces = M * row_pieces;
+  u32x4 xv[kStageBatch];
+#pragma unroll
+  for (int e = 0; e < kStageBatch; ++e) {
+    if (e * kThreads < pieces) {  // uniform
+      int idx = tid + e * kThreads;
+      idx = idx < pieces ? idx : pieces - 1;
+      const int m = idx / row_pieces;
+      const int c = idx - m * row_pieces;
+      xv[e] = *reinterpret_cast<const u32x4*>(xg + m * a.ldx + 8 * c);
+    }
+  }
+  // The workgroup's scales/zeros: rows [tile0*16, tile0*16 + 16*NTT) are one contiguous run of
+  // 16*NTT*G floats. Pieces past the end of the tensors read as zero (buffer range check).
+  const int meta_pieces = (NTT * 16 * G + 3) / 4;
+  const uint32_t meta_base = uint32_t(tile0 * 16 * G * 4);
+  const auto ms = make_rsrc(a.scales, uint32_t(a.N * a.G * 4));
+  const auto mz = make_rsrc(asym ? a.zeros : a.scales, uint32_t(a.N * a.G * 4));
+  u32x4 sv[kMetaBatch], zv[kMetaBatch];
+#pragma unroll
+  for (int e = 0; e < kMetaBatch; ++e) {
+    if (e * kThreads < meta_pieces) {  // uniform
+      const uint32_t off = meta_base + uint32_t(tid + e * kThreads) * 16;
+      sv[e] = buf_load16(ms, off, 0);
+      zv[e] = buf_load16(mz, off, 0);
+    }
+  }
+
+  // ---- write the staged data to LDS ----
+  for (int i = tid; i < NM; i += kThreads) zero_lds[i] = u32x4{0u, 0u, 0u, 0u};
+  for (int i = tid; i < steps * 16; i += kThreads)
+    if ((i & 15) >= M) xsum_lds[i] = 0.0f;
+#pragma unroll
+  for (int e = 0; e < kStageBatch; ++e) {
+    if (e * kThreads < pieces) {  // uniform
+      const int idx = tid + e * kThreads;
+      const int m = idx / row_pieces;
+      const int c = idx - m * row_pieces;
+      // Sum of this piece's 8 activations, then over the kStepPieces consecutive lanes that
+      // hold the pieces of one step (kThreads and row_pieces are multiples of kStepPieces).
+      const uint32_t w4[4] = {xv[e].x, xv[e].y, xv[e].z, xv[e].w};
+      float sum = 0.0f;
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        sum += Act::load(Raw(w4[h] & 0xFFFFu)) + Act::load(Raw(w4[h] >> 16));
+#pragma unroll
+      for (int off = 1; off < Geo::kStepPieces; off <<= 1) sum += __shfl_xor(sum, off, 64);
+      if (idx < pieces) {
+        lds[m * kRow + c] = arrange<Act, FMT>(xv[e]);
+        if ((c & (Geo::kStepPieces - 1)) == 0) xsum_lds[(c / Geo::kStepPieces) * 16 + m] = sum;
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < kMetaBatch; ++e) {
+    if (e * kThreads < meta_pieces) {  // uniform
+      const int first = (tid + e * kThreads) * 4;
+      const uint32_t s4[4] = {sv[e].x, sv[e].y, sv[e].z, sv[e].w};
+      const uint32_t z4[4] = {zv[e].x, zv[e].y, zv[e].z, zv[e].w};
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int f = first + h;
+        if (f < NTT * 16 * G) {
+          const int row = f / G;
+          const int g = f - row * G;
+          float2 sz;
+          sz.x = __uint_as_float(s4[h]);
+          sz.y = __uint_as_float(z4[h]);
+          *reinterpret_cast<float2*>(meta_lds + row * meta_row + 2 * g) = sz;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const uint32_t flip = (FMT == kByte && a.signed_codes) ? 0x80808080u : 0u;
+  const float z_shift = Op::kOffset + ((FMT == kByte && a.signed_codes) ? 128.0f : 0.0f);
+  const float z_const = a.zero_const + z_shift;
+
+  f32x4 tot[NTT];
+#pragma unroll
+  for (int t = 0; t < NTT; ++t) tot[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
+  // Lanes of rows m >= M read the zero pieces.
+  const u32x4* const xrow = col < M ? lds + col * kRow + kq * NM : zero_lds;
+  const int xstep = col < M ? 4 * NM : 0;
+
+  for (int q0 = 0; q0 < my_steps; q0 += Q) {  // the host guarantees Q | my_steps
+#pragma unroll
+    for (int qq = 0; qq < Q; ++qq) {
+      const int q = q0 + qq;
+      const int step = q * NW + wave;
+      const int g = int(div_small(uint32_t(step), group_magic));
+      u32x4 xa[NM];
+#pragma unroll
+      for (int j = 0; j < NM; ++j) xa[j] = xrow[step * xstep + j];
+      float xsum[RM];
+      if constexpr (RM == 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(xsum_lds + step * 16 + 4 * kq);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xsum[r] = v[r];
+      } else {
+        xsum[0] = xsum_lds[step * 16 + 4 * kq];
+      }
+#pragma unroll
+      for (int t = 0; t < NTT; ++t) {
+        const int p = qq * NTT + t;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (FMT == kNibble) {
+          const uint32_t words[4] = {ring[p].x, ring[p].y, ring[p].z, ring[p].w};
+#pragma unroll
+          for (int j = 0; j < NM; ++j) acc = Mfma16<Act>::run(xa[j], nib.operand(words[j]), acc);
+        } else {
+          const uint32_t words[4] = {ring[p].x, ring[p].y, ring[p].z, ring[p].w};
+#pragma unroll
+          for (int j = 0; j < NM; ++j) acc = Mfma16<Act>::run(xa[j], Op::operand(words, j, flip), acc);
+        }
+        const float2 sz = *reinterpret_cast<const float2*>(meta_lds + (t * 16 + col) * meta_row + 2 * g);
+        const float zc = asym ? sz.y + z_shift : z_const;
+#pragma unroll
+        for (int r = 0; r < RM; ++r)
+          tot[t][r] = __builtin_fmaf(sz.x, __builtin_fmaf(-zc, xsum[r], acc[r]), tot[t][r]);
+      }
+#pragma unroll
+      for (int t = 0; t < NTT; ++t) load_item(qq * NTT + t, q + Q);
+    }
+  }
+
+  // ---- fixed-order reduction over the waves: red[wave][t][m][16] ----
+  __syncthreads();  // every wave is done reading the staged data
+  float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int t = 0; t < NTT; ++t)
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+      const int m = 4 * kq + r;
+      if (m < M) red[((wave * NTT + t) * M + m) * 16 + col] = tot[t][r];
+    }
+  __syncthreads();
+  const Raw* bias = static_cast<const Raw*>(a.bias);
+  Raw* y = static_cast<Raw*>(a.y);
+  const int outs = NTT * M * 16;
+  for (int e = tid; e < outs; e += kThreads) {
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += red[w * outs + e];
+    const int t = e / (M * 16);
+    const int rem = e - t * M * 16;
+    const int m = rem >> 4;
+    const int64_t n = (tile0 + t) * 16 + (rem & 15);
+    if (n < a.N) {
+      if (bias) v += Act::load(bias[n]);
+      y[m * a.ldy + n] = Act::store(v);
+    }
+  }
+}
+
+// ---- one-shot kernel (M <= 4, nibble codes, group 128) ------------------------------------------
+//
+// One workgroup owns one tile of 16 output features; its waves split K into contiguous chunks of
+// C steps (C*128 codes per row), one chunk per wave. A wave issues every load it needs up front
+// -- its share of the tile's scales and zeros, its activation slice, then its C code loads --
+// and only then starts waiting, so the whole chunk (C KB of codes) is in flight at once and the
+// grid as a whole streams the weight at the rate HBM can deliver.
+// * The tile's scales and zeros (16 rows x G floats each, one contiguous run of the [N, G]
+//   tensors) are loaded once per workgroup with coalesced 16-byte lane loads into LDS; loading
+//   each wave's groups separately costs about as much time again as all the codes' latency.
+// * The activation slice goes through a wave-private LDS region, permuted into the MFMA operand
+//   order, with per-step sums for the zero-point term.
+// * One barrier makes the staged data visible; the final cross-wave reduction needs two more.
+template <int C, int MMAX>
+struct OneShotGeom {
+  static constexpr int kStepPieces = 16;                     // 16-byte x pieces per row and step
+  static constexpr int kRowPieces = C * kStepPieces + 1;     // padded LDS row of a wave's slice
+  static constexpr int kWavePieces = MMAX * kRowPieces + 4;  // + four zero pieces
+  static constexpr int kXPerLane = (MMAX * C * kStepPieces + 63) / 64;
+  // Scale / zero rows of the tile in LDS: G + 4 floats (keeps 16-byte alignment and puts the
+  // 16 rows on distinct banks for the per-step reads).
+  __host__ __device__ static int meta_stride(int64_t G) { return int(G) + 4; }
+  static size_t lds_bytes(int nw, int64_t G) {
+    const size_t stage = size_t(nw) * (kWavePieces * 16 + C * 16 * 4) + size_t(2) * 16 * meta_stride(G) * 4;
+    const size_t red = size_t(nw) * 4 * 64 * 4;
+    return stage > red ? stage : red;
+  }
+};
+
+template <class Act, int C, int MMAX, int RM, bool INTER = false>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)))
+    decode_oneshot_kernel(const LinearArgs a) {
+  using Geo = OneShotGeom<C, MMAX>;
+  using Raw = typename Act::raw;
+  constexpr int NM = 4;
+
+  extern __shared__ u32x4 lds[];
+  const int M = int(a.M);
+  const int G = int(a.G);
+  const int nw = int(blockDim.x) >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;
+  const int kq = lane >> 4;
+  const int64_t tile = blockIdx.x;
+  const bool asym = !a.symmetric;
+  // Item i of this wave is step `step0 + i * sstride`: a contiguous chunk per wave, or (INTER)
+  // interleaved over the waves. Measured on MI355X, contiguous chunks are as fast or faster.
+  const int step0 = INTER ? wave : wave * C;
+  const int sstride = INTER ? nw : 1;
+
+  int64_t n = tile * 16 + col;
+  n = n < a.N ? n : a.N - 1;  // rows past N repeat row N-1; their sums are never stored
+
+  // LDS: [wave x slices | wave xsums | scales [16][G+4] | zeros [16][G+4]]
+  u32x4* const xw = lds + wave * Geo::kWavePieces;
+  u32x4* const zero4 = xw + MMAX * Geo::kRowPieces;
+  float* const xsum = reinterpret_cast<float*>(lds + nw * Geo::kWavePieces) + wave * C * 16;  // [C][16]
+  const int mstride = Geo::meta_stride(G);
+  float* const s_lds = reinterpret_cast<float*>(lds + nw * Geo::kWavePieces) + nw * C * 16;
+  float* const z_lds = s_lds + 16 * mstride;
+
+  // ---- issue every load: the tile's scales/zeros, the activation slice, the chunk's codes ----
+  const int meta_pieces = 16 * G / 4;  // the host guarantees G % 4 == 0
+  const bool meta_loader = tid < meta_pieces;
+  const uint32_t meta_bytes = uint32_t(a.N * a.G * 4);
+  const auto ms = make_rsrc(a.scales, meta_bytes);
+  const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_bytes);
+  const uint32_t mo = uint32_t(tile * 16 * a.G * 4) + uint32_t(meta_loader ? tid : 0) * 16;
+  const u32x4 sv = buf_load16(ms, mo, 0);  // past the end of the tensors: zeros
+  const u32x4 zv = buf_load16(mz, mo, 0);
+
+  const Raw* xg = static_cast<const Raw*>(a.x) + int64_t(step0) * 128;
+  u32x4 xv[Geo::kXPerLane];
+#pragma unroll
+  for (int e = 0; e < Geo::kXPerLane; ++e) {
+    int idx = lane + 64 * e;
+    idx = idx < M * C * 16 ? idx : 0;
+    const int m = idx / (C * 16);
+    const int c = idx - m * (C * 16);
+    xv[e] = *reinterpret_cast<const u32x4*>(xg + m * a.ldx + (c >> 4) * (sstride * 128) + 8 * (c & 15));
+  }
+  const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
+  const uint32_t qoff = uint32_t(n * a.ldq + kq * 16);
+  u32x4 w[C];
+#pragma unroll
+  for (int i = 0; i < C; ++i) w[i] = buf_load16(wq, qoff, uint32_t(step0 + i * sstride) * 64);
+
+  // ---- stage scales/zeros and this wave's activation slice in LDS ----
+  if (meta_loader) {
+    const int row = (tid * 4) / G;
+    const int g = tid * 4 - row * G;
+    *reinterpret_cast<u32x4*>(s_lds + row * mstride + g) = sv;
+    *reinterpret_cast<u32x4*>(z_lds + row * mstride + g) = zv;
+  }
+  if (lane < NM) zero4[lane] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = lane; i < C * 16; i += 64)
+    if ((i & 15) >= M) xsum[i] = 0.0f;
+#pragma unroll
+  for (int e = 0; e < Geo::kXPerLane; ++e) {
+    const int idx = lane + 64 * e;
+    const int m = idx / (C * 16);
+    const int c = idx - m * (C * 16);
+    const uint32_t w4[4] = {xv[e].x, xv[e].y, xv[e].z, xv[e].w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) sum += Act::load(Raw(w4[h] & 0xFFFFu)) + Act::load(Raw(w4[h] >> 16));
+    // The 16 pieces of one step sit in 16 consecutive lanes.
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+    if (idx < M * C * 16) {
+      xw[m * Geo::kRowPieces + c] = arrange<Act, kNibble>(xv[e]);
+      if ((c & 15) == 0) xsum[(c >> 4) * 16 + m] = sum;
+    }
+  }
+  __syncthreads();
+
+  // ---- compute ----
+  const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
+  const float z_shift = Act::kNibbleOffset;
+  const float z_const = a.zero_const + z_shift;
+  const u32x4* const xrow = col < M ? xw + col * Geo::kRowPieces + kq * NM : zero4;
+  const int xstep = col < M ? 4 * NM : 0;
+  const float* const srow = s_lds + col * mstride + step0;
+  const float* const zrow = z_lds + col * mstride + step0;
+  f32x4 tot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < C; ++i) {
+    u32x4 xa[NM];
+#pragma unroll
+    for (int j = 0; j < NM; ++j) xa[j] = xrow[i * xstep + j];
+    float xs[RM];
+    if constexpr (RM == 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(xsum + i * 16 + 4 * kq);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xs[r] = v[r];
+    } else {
+      xs[0] = xsum[i * 16 + 4 * kq];
+    }
+    const float s = srow[i * sstride];
+    const float zc = asym ? zrow[i * sstride] + z_shift : z_const;
+    const uint32_t words[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NM; ++j) acc = Mfma16<Act>::run(xa[j], nib.operand(words[j]), acc);
+#pragma unroll
+    for (int r = 0; r < RM; ++r) tot[r] = __builtin_fmaf(s, __builtin_fmaf(-zc, xs[r], acc[r]), tot[r]);
+  }
+
+  // ---- fixed-order reduction over the waves (the K chunks): red[wave][r][lane] ----
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int r = 0; r < RM; ++r) red[(wave * 4 + r) * 64 + lane] = tot[r];
+  __syncthreads();
+  if (tid < 16 * M) {
+    const int m = tid >> 4;
+    const int c = tid & 15;
+    const int src_lane = c + 16 * (m >> 2);
+    const int r = m & 3;
+    float v = 0.0f;
+    for (int w2 = 0; w2 < nw; ++w2) v += red[(w2 * 4 + r) * 64 + src_lane];
+    const int64_t nn = tile * 16 + c;
+    if (nn < a.N) {
+      if (a.bias) v += Act::load(static_cast<const Raw*>(a.bias)[nn]);
+      static_cast<Raw*>(a.y)[m * a.ldy + nn] = Act::store(v);
+    }
+  }
+}
+
 // ---- dispatch ----------------------------------------------------------------------------------
 
 template <class Act, int FMT, int CB, int MB, int NT, int NW>
@@ -329,9 +779,139 @@ hipError_t launch_act(const LinearArgs& a, int cb, uint32_t magic, hipStream_t s
   return launch_cb<Act, kByte, 16>(a, magic, stream);
 }
 
-}  // namespace
 
-hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* fits) {
+template <class Act, int FMT, int NTT, int Q, int NW>
+hipError_t launch_stream_cfg(const LinearArgs& a, int steps, uint32_t magic, hipStream_t stream) {
+  const int64_t tiles = (a.N + 15) / 16;
+  const int64_t blocks = (tiles + NTT - 1) / NTT;
+  const size_t stage = StreamGeom<FMT>::lds_bytes(a.M, steps, a.G, NTT);
+  const size_t red = size_t(NW) * NTT * a.M * 16 * sizeof(float);
+  const size_t lds = stage > red ? stage : red;
+  if (a.M == 1) {
+    hipLaunchKernelGGL((decode_stream_kernel<Act, FMT, NTT, Q, NW, 1>), dim3(unsigned(blocks)),
+                       dim3(NW * 64), lds, stream, a, steps, magic);
+  } else {
+    hipLaunchKernelGGL((decode_stream_kernel<Act, FMT, NTT, Q, NW, 4>), dim3(unsigned(blocks)),
+                       dim3(NW * 64), lds, stream, a, steps, magic);
+  }
+  return hipGetLastError();
+}
+
+// Tiles per workgroup: two when there are enough tiles for every CU to take several.
+inline int stream_ntt(const LinearArgs& a) { return (a.N + 15) / 16 >= 4 * 256 ? 2 : 1; }
+
+template <class Act, int FMT, int NW>
+hipError_t launch_stream_nw(const LinearArgs& a, int steps, int q, uint32_t magic, hipStream_t stream) {
+  if (stream_ntt(a) == 2) return launch_stream_cfg<Act, FMT, 2, 2, NW>(a, steps, magic, stream);
+  if (q == 4) return launch_stream_cfg<Act, FMT, 1, 4, NW>(a, steps, magic, stream);
+  return launch_stream_cfg<Act, FMT, 1, 2, NW>(a, steps, magic, stream);
+}
+
+template <class Act, int FMT>
+hipError_t launch_stream(const LinearArgs& a, int nw, int steps, int q, uint32_t magic,
+                         hipStream_t stream) {
+  if (nw == 8) return launch_stream_nw<Act, FMT, 8>(a, steps, q, magic, stream);
+  return launch_stream_nw<Act, FMT, 4>(a, steps, q, magic, stream);
+}
+
+template <class Act, int C, int MMAX, int RM>
+hipError_t launch_oneshot_cfg(const LinearArgs& a, int nw, hipStream_t stream) {
+  const size_t lds = OneShotGeom<C, MMAX>::lds_bytes(nw, a.G);
+  auto kernel = decode_oneshot_kernel<Act, C, MMAX, RM>;
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kernel, dim3(unsigned((a.N + 15) / 16)), dim3(unsigned(nw * 64)), lds, stream, a);
+  return hipGetLastError();
+}
+
+template <class Act>
+hipError_t launch_oneshot(const LinearArgs& a, int c, int nw, hipStream_t stream) {
+  if (a.M == 1) {
+    if (c == 16) return launch_oneshot_cfg<Act, 16, 1, 1>(a, nw, stream);
+    if (c == 8) return launch_oneshot_cfg<Act, 8, 1, 1>(a, nw, stream);
+    return launch_oneshot_cfg<Act, 4, 1, 1>(a, nw, stream);
+  }
+  if (c == 8) return launch_oneshot_cfg<Act, 8, 4, 4>(a, nw, stream);
+  return launch_oneshot_cfg<Act, 4, 4, 4>(a, nw, stream);
+}
+
+// M <= 4, 2/4-bit codes, group 128: the one-shot kernel.
+bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
+  if (a.fmt != kNibble || a.M > 4 || a.group != 128 || a.K % 128 != 0 || a.G % 4 != 0) return false;
+  if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
+  if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
+  const int64_t tiles = (a.N + 15) / 16;
+  if (tiles > 0x7FFFFFFF) return false;
+  const int64_t steps = a.K / 128;
+  // Chunk length: the shortest that keeps a tile within 16 waves. Short chunks spread the
+  // per-wave compute over more waves, which finish as their data lands; on MI355X 4-step chunks
+  // beat 8 and 16 on every Llama-3-8B projection where they fit.
+  int chosen = 0;
+  for (int c : {4, 8, 16}) {
+    if (c == 16 && a.M > 1) continue;
+    if (steps % c != 0 || steps / c > 16) continue;
+    chosen = c;
+    break;
+  }
+  if (chosen == 0) return false;
+  const int nw = int(steps / chosen);
+  if (16 * a.G / 4 > int64_t(nw) * 64) return false;  // one scale piece per thread
+  *err = a.act == kDtBf16 ? launch_oneshot<ActBf16>(a, chosen, nw, stream)
+                          : launch_oneshot<ActF16>(a, chosen, nw, stream);
+  return true;
+}
+
+// Small M: the streaming kernel, when the step geometry fits and x[M, K] fits in LDS.
+bool try_stream(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
+  if (a.M > 16) return false;
+  const int step_k = a.fmt == kNibble ? 128 : 64;
+  if (a.group % step_k != 0 || a.K % step_k != 0 || a.ldq % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
+  const int64_t steps = a.K / step_k;
+  if (steps >= 65536 || (a.N + 15) / 16 > 0x7FFFFFFF) return false;
+  // 32-bit buffer offsets.
+  if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
+  const int ntt = stream_ntt(a);
+  const size_t lds = a.fmt == kNibble ? StreamGeom<kNibble>::lds_bytes(a.M, steps, a.G, ntt)
+                                      : StreamGeom<kByte>::lds_bytes(a.M, steps, a.G, ntt);
+  if (lds > kStreamLds) return false;
+  // Waves per workgroup: 4, or 8 when the staged activations need the extra threads (they
+  // are loaded in one batch of kStageBatch 16-byte pieces per thread). Several workgroups
+  // share a CU.
+  const int64_t pieces = a.M * a.K / 8;
+  const int64_t meta_pieces = (int64_t(ntt) * 16 * a.G + 3) / 4;
+  int nw = 0;
+  for (int cand : {4, 8}) {
+    if (steps % cand == 0 && pieces <= int64_t(kStageBatch) * cand * 64 &&
+        meta_pieces <= int64_t(kMetaBatch) * cand * 64) {
+      nw = cand;
+      break;
+    }
+  }
+  if (nw == 0) return false;
+  // Ring depth: Q steps per wave ahead (4 or 2, dividing the wave's step count).
+  const int64_t my_steps = steps / nw;
+  const int q = my_steps % 4 == 0 ? 4 : (my_steps % 2 == 0 ? 2 : 0);
+  if (q == 0) return false;
+  const uint32_t per_group = uint32_t(a.group / step_k);
+  const uint32_t magic = per_group == 1 ? 0u
+      : uint32_t((uint64_t(1) << 32) / per_group + ((uint64_t(1) << 32) % per_group != 0));
+  if (a.act == kDtBf16) {
+    *err = a.fmt == kNibble ? launch_stream<ActBf16, kNibble>(a, nw, int(steps), q, magic, stream)
+                            : launch_stream<ActBf16, kByte>(a, nw, int(steps), q, magic, stream);
+  } else {
+    *err = a.fmt == kNibble ? launch_stream<ActF16, kNibble>(a, nw, int(steps), q, magic, stream)
+                            : launch_stream<ActF16, kByte>(a, nw, int(steps), q, magic, stream);
+  }
+  return true;
+}
+
+hipError_t launch_skinny(const LinearArgs& a, hipStream_t stream, bool* fits) {
   *fits = false;
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
   if (a.M < 1 || a.M > 64) return hipSuccess;
@@ -367,6 +947,21 @@ hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* f
   *fits = true;
   if (a.act == kDtBf16) return launch_act<ActBf16>(a, cb, magic, stream);
   return launch_act<ActF16>(a, cb, magic, stream);
+}
+
+
+}  // namespace
+
+hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* fits) {
+  *fits = false;
+  if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
+  if (a.M < 1 || a.M > 64) return hipSuccess;
+  hipError_t err = hipSuccess;
+  if (try_oneshot(a, stream, &err) || try_stream(a, stream, &err)) {
+    *fits = true;
+    return err;
+  }
+  return launch_skinny(a, stream, fits);
 }
 
 }  // namespace llmopt
