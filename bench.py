@@ -1,20 +1,29 @@
 #!/usr/bin/env python3
-"""W4A16 QuantLinear on one MI355X: decode GB/s (headline), prefill TFLOP/s (sweep).
+"""W4A16 QuantLinear on one MI355X: decode GB/s (headline) and prefill TFLOP/s.
 
-One step = one Llama-3-8B decoder layer's four quantized projections at batch 1
-(decode): qkv (K 4096, N 6144), o (4096, 4096), gate_up (4096, 28672) and down
-(14336, 4096), 4-bit asymmetric round-to-nearest with group 128 (the reference's
-packed layout), bf16 activations ~N(0, 1), weights ~N(0, 0.02). Steps cycle through
-several distinct layer copies (at least 512 MB of packed weights) so the 256 MB
-Infinity Cache cannot hold them: every step streams its weights from HBM, like a real
-decode walking through a model's layers. Inputs are resident in HBM before timing.
+Workload (one step): one Llama-3-8B decoder layer's four quantized projections at batch 1
+(decode) -- qkv (K 4096, N 6144), o (4096, 4096), gate_up (4096, 28672), down (14336, 4096) --
+with 4-bit asymmetric round-to-nearest weights, group 128, in the reference's packed layout
+(two codes per byte, fp32 scales and zeros per group); bf16 activations ~N(0, 1), weights
+~N(0, 0.02), all synthetic and seeded. Steps cycle through enough distinct layer copies
+(>= 512 MiB of packed weights) that the 256 MB Infinity Cache cannot hold them: every step
+streams its weights from HBM, like a decode walking through a model's layers. Inputs are
+resident in HBM before timing; each step is one HIP graph of the four launches.
 
-value       = algorithmic bytes of all timed steps / timed seconds
-              bytes per call = N*K/2 + 4*N*G*2 + 2*M*K + 2*M*N  (G = K/128)
-roofline    = the dominant kernel (gate_up decode GEMV): its algorithmic bytes per
-              launch / its mean launch time from HIP events on the launch stream
-cpu_baseline= the reference's host sequence (dequantize once, cache, F.linear in bf16)
-              timed on this host's cores for a bounded sample of the same steps
+value          algorithmic bytes of all timed steps / timed seconds, where one call moves
+               N*K/2 (codes) + 4*N*G*2 (scales, zeros; G = K/128) + 2*M*K + 2*M*N bytes
+roofline       the dominant kernel (gate_up): its algorithmic bytes / its mean time per launch,
+               from HIP events around replays of a graph of back-to-back launches (rotating
+               over the copies) on the replay stream -- so it includes the inter-kernel gap;
+               `traffic` = HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (each
+               scaled by what it reads for a plain copy of known size), when recorded
+prefill        gate_up at M = 8192 through the MFMA prefill kernel, TFLOP/s vs dense bf16 peak
+cpu_baseline   the reference's host sequence (dequantize once, cache the dense bf16 weight,
+               F.linear) on this host's cores, for a bounded number of the same decode steps
+
+Modes: default prints the JSON line. `--pmc-workload` runs only the dominant kernel and a
+256 MiB copy (for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`); `--traffic-from DIR`
+turns two such rocprofv3 CSV outputs into profiles/traffic_decode_gate_up_m1.json.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
 """
@@ -22,6 +31,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
 import statistics
@@ -40,6 +50,8 @@ BF16_PEAK_TFLOPS = 2500.0
 PROJECTIONS = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
 GROUP = 128
 MIN_ROTATION_BYTES = 512 * 2**20
+TRAFFIC_FILE = REPO / "profiles" / "traffic_decode_gate_up_m1.json"
+COPY_BYTES = 256 * 2**20
 
 
 def algorithmic_bytes(m: int, n: int, k: int, bits: int = 4, group: int = GROUP, asym: bool = True) -> int:
@@ -51,18 +63,21 @@ def algorithmic_bytes(m: int, n: int, k: int, bits: int = 4, group: int = GROUP,
 def parse_args() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--steps", type=int, default=400)
+    p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--m", type=int, default=1, help="tokens per decode step")
-    p.add_argument("--kernel-launches", type=int, default=100, help="timed launches of the dominant kernel")
-    p.add_argument("--sweep", action="store_true", help="also time every projection at M in {1,8,32,64,256,2048,8192}")
+    p.add_argument("--kernel-launches", type=int, default=60, help="timed launches of the dominant kernel")
+    p.add_argument("--sweep", action="store_true", help="also time every projection at M in {1..8192}")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--pmc-workload", action="store_true", help="only the dominant kernel + a copy")
+    p.add_argument("--traffic-from", type=str, default=None, help="rocprofv3 --pmc output dir")
     return p.parse_args()
 
 
 def build_layers(torch, count: int, m: int):
-    """`count` distinct copies of the four quantized projections plus their inputs/outputs."""
+    """`count` distinct copies of the four quantized projections plus their inputs."""
     from llmopt.quantization import QuantizedTensor, RoundToNearestQuantizer
 
     dev = torch.device("cuda:0")
@@ -85,12 +100,43 @@ def build_layers(torch, count: int, m: int):
     return base, layers, xs
 
 
+def kernel_launch_times(torch, launch, count: int, replays: int = 7) -> list[float]:
+    """Per-launch times (us) of `count` back-to-back launches captured in one HIP graph and
+    replayed `replays` times, each replay bracketed by HIP events on the replay stream. The
+    figure includes the few-microsecond gap the GPU leaves between two dependent kernels."""
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        launch(0)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            for i in range(count):
+                launch(i)
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    g.replay()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(replays):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(cur)
+        g.replay()
+        e.record(cur)
+        torch.cuda.synchronize()
+        out.append(s.elapsed_time(e) * 1e3 / count)
+    return out
+
+
 def main() -> int:
     args = parse_args()
+    if args.traffic_from:
+        return traffic_summary(Path(args.traffic_from))
     if args.gpus != 1:
         print(
-            "bench.py measures one GPU: this build has no multi-GPU path (the kernels run on one "
-            "device; see DESIGN.md for how the projections would shard). Run with --gpus 1.",
+            "bench.py measures one GPU: the quantized-linear kernels run on one device and this "
+            "build has no multi-GPU path (DESIGN.md describes how the projections would shard). "
+            "Run with --gpus 1.",
             file=sys.stderr,
         )
         return 2
@@ -105,22 +151,46 @@ def main() -> int:
     layer_bytes = sum(algorithmic_bytes(0, n, k) for _, n, k in PROJECTIONS)
     copies = max(2, -(-MIN_ROTATION_BYTES // layer_bytes))
     base, layers, xs = build_layers(torch, copies, args.m)
-    outs = {name: torch.empty(args.m, n, dtype=bf16, device="cuda:0") for name, n, _ in PROJECTIONS}
-    step_bytes = sum(algorithmic_bytes(args.m, n, k) for _, n, k in PROJECTIONS)
+    flush_src = torch.empty(COPY_BYTES // 2, dtype=bf16, device="cuda:0")
+    flush_dst = torch.empty_like(flush_src)
+
+    def flush():
+        flush_dst.copy_(flush_src)
+
+    name, n, k = PROJECTIONS[2]  # gate_up: the dominant kernel
+
+    def launch_gate_up(i):
+        ops.quant_linear(xs[name], layers[i % copies][name], None, bf16)
+
+    if args.pmc_workload:
+        for i in range(3):
+            launch_gate_up(i)
+            flush()
+        torch.cuda.synchronize()
+        for i in range(args.kernel_launches):
+            flush()
+            launch_gate_up(i)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_workload": "gate_up decode", "M": args.m, "launches": args.kernel_launches,
+                          "copy_bytes": COPY_BYTES, "algorithmic_bytes": algorithmic_bytes(args.m, n, k)}))
+        return 0
+
+    outs = {p: torch.empty(args.m, pn, dtype=bf16, device="cuda:0") for p, pn, _ in PROJECTIONS}
+    step_bytes = sum(algorithmic_bytes(args.m, pn, pk) for _, pn, pk in PROJECTIONS)
 
     # One HIP graph per layer copy: the four launches of a step, replayed back to back.
     stream = torch.cuda.Stream()
     graphs = []
     with torch.cuda.stream(stream):
         for layer in layers:  # eager warm-up before capture
-            for name, _, _ in PROJECTIONS:
-                ops.quant_linear(xs[name], layer[name], None, bf16)
+            for p, _, _ in PROJECTIONS:
+                ops.quant_linear(xs[p], layer[p], None, bf16)
         torch.cuda.synchronize()
         for layer in layers:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
-                for name, _, _ in PROJECTIONS:
-                    outs[name] = ops.quant_linear(xs[name], layer[name], None, bf16)
+                for p, _, _ in PROJECTIONS:
+                    outs[p] = ops.quant_linear(xs[p], layer[p], None, bf16)
             graphs.append(g)
     torch.cuda.synchronize()
 
@@ -129,9 +199,9 @@ def main() -> int:
     for i in range(args.warmup):
         graphs[i % copies].replay()
     torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    cur = torch.cuda.current_stream()
     start.record(cur)
     for i in range(args.steps):
         graphs[i % copies].replay()
@@ -140,34 +210,26 @@ def main() -> int:
     total_ms = start.elapsed_time(end)
     ms_per_step = total_ms / args.steps
     value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
+    print(f"# timed {args.steps} steps: {ms_per_step * 1e3:.2f} us/step, {value:.0f} GB/s",
+          file=sys.stderr, flush=True)
 
-    # Dominant kernel: gate_up at M, one event pair per launch, rotating over the copies.
-    name, n, k = PROJECTIONS[2]
-    x = xs[name]
-    times = []
-    for i in range(args.kernel_launches + 10):
-        s_ev = torch.cuda.Event(enable_timing=True)
-        e_ev = torch.cuda.Event(enable_timing=True)
-        s_ev.record(cur)
-        ops.quant_linear(x, layers[i % copies][name], None, bf16)
-        e_ev.record(cur)
-        if i >= 10:
-            times.append((s_ev, e_ev))
-    torch.cuda.synchronize()
-    kernel_us = statistics.mean(s.elapsed_time(e) * 1e3 for s, e in times)
+    times = kernel_launch_times(torch, launch_gate_up, 4 * copies)
+    kernel_us = statistics.mean(times)
     kernel_bytes = algorithmic_bytes(args.m, n, k)
     achieved = kernel_bytes / (kernel_us * 1e-6) / 1e9
     roofline = {
         "bound": "hbm",
-        "kernel": f"qlinear_decode gate_up M={args.m} (K 4096, N 28672)",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": _measured_traffic(f"gate_up_m{args.m}"),
+        "traffic": _measured_traffic(args.m),
+        "kernel": f"quantized-linear decode, gate_up M={args.m} (K 4096, N 28672, W4 g128 asym)",
         "algorithmic_bytes": kernel_bytes,
         "mean_launch_us": round(kernel_us, 3),
+        "median_launch_us": round(statistics.median(times), 3),
     }
+    print(f"# gate_up kernel: mean {kernel_us:.2f} us, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
 
     result = {
         "metric": METRIC,
@@ -194,6 +256,8 @@ def main() -> int:
         },
         "roofline": roofline,
     }
+    if not args.no_prefill:
+        result["prefill"] = prefill(torch, ops, layers, copies)
     if args.sweep:
         result["sweep"] = sweep(torch, ops, layers, copies)
     if not args.no_cpu:
@@ -202,38 +266,46 @@ def main() -> int:
     return 0
 
 
-def _measured_traffic(key: str):
-    """HBM bytes per launch measured with rocprofv3 counters, if recorded in profiles/."""
-    path = REPO / "profiles" / "traffic.json"
-    if not path.exists():
+def _measured_traffic(m: int):
+    """HBM bytes per launch of the dominant kernel, from rocprofv3 counters, if recorded."""
+    if not TRAFFIC_FILE.exists() or m != 1:
         return None
     try:
-        return json.loads(path.read_text()).get(key)
+        return json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         return None
 
 
+def prefill(torch, ops, layers, copies):
+    """gate_up at M = 8192 (prefill kernel), per-launch time of back-to-back launches."""
+    name, n, k = PROJECTIONS[2]
+    m = 8192
+    x = torch.randn(m, k, device="cuda:0").to(torch.bfloat16)
+    ops.quant_linear(x, layers[0][name], None, torch.bfloat16)
+    times = kernel_launch_times(
+        torch, lambda i: ops.quant_linear(x, layers[i % copies][name], None, torch.bfloat16), copies, 3
+    )
+    us = statistics.mean(times)
+    tflops = 2 * m * n * k / (us * 1e-6) / 1e12
+    print(f"# prefill gate_up M={m}: {us:.1f} us, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    return {"kernel": f"quantized-linear prefill, gate_up M={m} (K 4096, N 28672)", "mean_launch_us": round(us, 2),
+            "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "bound": "mfma"}
+
+
 def sweep(torch, ops, layers, copies):
-    """Per-projection kernel times (HIP events) for decode and prefill batch sizes."""
+    """Per-projection kernel times for decode and prefill batch sizes."""
     bf16 = torch.bfloat16
-    cur = torch.cuda.current_stream()
     rows = []
     for m in (1, 8, 32, 64, 256, 2048, 8192):
         for name, n, k in PROJECTIONS:
             x = torch.randn(m, k, device="cuda:0").to(bf16)
-            reps = 20 if m <= 2048 else 5
-            for i in range(3):
-                ops.quant_linear(x, layers[i % copies][name], None, bf16)
-            pairs = []
-            for i in range(reps):
-                s_ev = torch.cuda.Event(enable_timing=True)
-                e_ev = torch.cuda.Event(enable_timing=True)
-                s_ev.record(cur)
-                ops.quant_linear(x, layers[i % copies][name], None, bf16)
-                e_ev.record(cur)
-                pairs.append((s_ev, e_ev))
-            torch.cuda.synchronize()
-            us = statistics.median(s.elapsed_time(e) * 1e3 for s, e in pairs)
+            ops.quant_linear(x, layers[0][name], None, bf16)
+            reps = 4 * copies if m <= 2048 else copies
+            times = kernel_launch_times(
+                torch, lambda i: ops.quant_linear(x, layers[i % copies][name], None, bf16), reps, 3
+            )
+            us = statistics.median(times)
             gbs = algorithmic_bytes(m, n, k) / (us * 1e-6) / 1e9
             tflops = 2 * m * n * k / (us * 1e-6) / 1e12
             rows.append({
@@ -290,6 +362,60 @@ def cpu_baseline(torch, base, m: int, seconds: float):
         "cold_value": round(step_bytes / cold_s / 1e9, 3),
         "torch": torch.__version__,
     }
+
+
+def _counter_per_dispatch(csv_path: Path, counter: str):
+    """Mean value of `counter` per dispatch for the gate_up decode kernel and for the copy."""
+    kern, copy = [], []
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != counter:
+                continue
+            name = row["Kernel_Name"]
+            value = float(row["Counter_Value"])
+            grid = int(row["Grid_Size"])
+            if "decode_oneshot_kernel" in name or "decode_stream_kernel" in name:
+                kern.append(value)
+            elif "copy" in name.lower() and grid > 0:
+                copy.append(value)
+    # Keep the flush copies -- the most frequent copy size of the run, one before every launch --
+    # not the copies that set up the weights.
+    groups: dict[int, list[float]] = {}
+    for v in copy:
+        if v >= 1024:
+            groups.setdefault(round(v / 1024), []).append(v)
+    flushes = max(groups.values(), key=len) if groups else []
+    return kern, flushes
+
+
+def traffic_summary(pmc_dir: Path) -> int:
+    """HBM bytes per launch of the dominant kernel from FETCH_SIZE and WRITE_SIZE runs."""
+    fetch_csv = next(pmc_dir.glob("**/fetch*counter_collection.csv"))
+    write_csv = next(pmc_dir.glob("**/write*counter_collection.csv"))
+    kf, cf = _counter_per_dispatch(fetch_csv, "FETCH_SIZE")
+    kw, cw = _counter_per_dispatch(write_csv, "WRITE_SIZE")
+    # The copy moves COPY_BYTES in and COPY_BYTES out: its counters (KiB) give the scale factor.
+    copy_fetch = statistics.median(cf) * 1024
+    copy_write = statistics.median(cw) * 1024
+    f_scale = COPY_BYTES / copy_fetch
+    w_scale = COPY_BYTES / copy_write
+    kfetch = statistics.median(kf) * 1024 * f_scale
+    kwrite = statistics.median(kw) * 1024 * w_scale
+    out = {
+        "kernel": "quantized-linear decode, gate_up M=1",
+        "fetch_bytes_per_launch": round(kfetch),
+        "write_bytes_per_launch": round(kwrite),
+        "hbm_bytes_per_launch": round(kfetch + kwrite),
+        "algorithmic_bytes": algorithmic_bytes(1, 28672, 4096),
+        "fetch_scale": round(f_scale, 4),
+        "write_scale": round(w_scale, 4),
+        "copy_bytes": COPY_BYTES,
+        "samples": {"kernel_fetch": len(kf), "kernel_write": len(kw), "copy_fetch": len(cf), "copy_write": len(cw)},
+    }
+    TRAFFIC_FILE.parent.mkdir(exist_ok=True)
+    TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+    return 0
 
 
 if __name__ == "__main__":
