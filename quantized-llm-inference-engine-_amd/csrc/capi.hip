@@ -153,7 +153,8 @@ int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const v
       if (M <= 64) {
         err = llmopt::launch_linear_decode(a, s, &fits);
       } else {
-        err = llmopt::launch_linear_prefill(a, s, &fits);
+        err = llmopt::launch_linear_gemm(a, s, &fits);
+        if (!fits) err = llmopt::launch_linear_prefill(a, s, &fits);
       }
       if (!fits) err = llmopt::launch_linear_generic(a, s);
       break;
@@ -165,7 +166,8 @@ int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const v
       if (!fits) return fail(LLMOPT_ERR_UNSUPPORTED, "decode kernel does not take these arguments");
       break;
     case LLMOPT_ALGO_PREFILL:
-      err = llmopt::launch_linear_prefill(a, s, &fits);
+      err = llmopt::launch_linear_gemm(a, s, &fits);
+      if (!fits) err = llmopt::launch_linear_prefill(a, s, &fits);
       if (!fits) return fail(LLMOPT_ERR_UNSUPPORTED, "prefill kernel does not take these arguments");
       break;
     default:

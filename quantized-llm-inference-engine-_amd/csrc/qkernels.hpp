@@ -36,5 +36,6 @@ hipError_t launch_linear_generic(const LinearArgs& a, hipStream_t stream);
 // dtype is outside what the kernel handles.
 hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* fits);
 hipError_t launch_linear_prefill(const LinearArgs& a, hipStream_t stream, bool* fits);
+hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fits);
 
 }  // namespace llmopt
