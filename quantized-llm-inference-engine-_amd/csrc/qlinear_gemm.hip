@@ -1,42 +1,51 @@
-// Prefill-regime quantized linear, second generation: a 256 x 256 MFMA GEMM whose packed
-// weight tiles are dequantized into LDS while the previous tile is being multiplied.
+// Prefill-regime quantized linear: an MFMA GEMM whose weight operand never touches LDS.
 //
 // Replaces QuantLinear.forward (src/llmopt/quantization/quant_linear.py:93-113) for long
 // batches: y = x @ dequant(qweight)^T + bias, where the reference first expands the whole
 // weight to a dense compute-dtype matrix (quantizers.py:204-239) and then calls F.linear.
 //
-// Shape of the computation. The kernel computes the transposed tile D = W x^T, so that the
-// MFMA output gives each lane four consecutive output features of one token (one 8-byte
-// store). A workgroup owns 256 output features x 256 tokens and walks K in 64-wide stages.
-// Eight waves (two per SIMD) split the tile 2 (features) x 4 (tokens); each wave owns
-// 128 x 64 = 4 x 2 tiles of v_mfma_f32_32x32x16_{bf16,f16}.
+// The kernel computes the transposed tile D = W x^T with v_mfma_f32_32x32x16_{bf16,f16}: the
+// A operand of that instruction gives lane l row l % 32 and eight consecutive k of half l / 32,
+// which is exactly one 32-bit word of packed 4-bit codes. Each wave therefore loads its own
+// weight rows straight from HBM (one 16-byte load per 32-row tile per 64-wide k stage),
+// dequantizes them in registers with the reference's arithmetic -- fp32 (q - z), then * s,
+// each rounded once, then a round-to-nearest-even cast -- and feeds them to the MFMAs. Only
+// the activations go through LDS, so an MFMA costs half a kilobyte of LDS reads instead of a
+// kilobyte (LDS reads and MFMAs compete on this part), and no weight is dequantized twice.
 //
-// Pipeline, per stage kt:
-//   * MFMAs on LDS buffer kt % 2 (weight rows as A, activation rows as B);
-//   * meanwhile every thread dequantizes its 32 codes of stage kt + 1 -- exactly as the
-//     reference does: fp32 (q - z) * s with one rounding, then a round-to-nearest-even cast --
-//     and stores them, with the activations it loaded one stage earlier, into buffer
-//     (kt + 1) % 2;
-//   * then it issues the loads for later stages: activations of stage kt + 2 and packed codes
-//     (plus scale and zero) of stage kt + 1 + kRing, kept in a small register ring so that HBM
-//     latency is covered by kRing - 1 stages of MFMA work;
-//   * one barrier per stage.
-// LDS rows are 64 elements (128 bytes) with the 16-byte chunk index XOR-swizzled by the row, so
-// the fragment reads of 32 consecutive rows spread over the banks.
-// Workgroup ids are spread evenly over the 8 XCDs and walked in groups of 8 token-tiles per
-// sweep over the feature tiles, so workgroups that run together share tiles in L2.
+// Layout. A workgroup owns 256 output features x (32 * TT) tokens; its four waves (one per
+// SIMD) each take 64 features and every token, i.e. 2 x TT accumulator tiles of 32 x 32.
+// Within a 64-wide stage, lane half h owns codes k = 32h .. 32h + 31 (bytes 16h .. 16h + 15 of
+// the row's 32-byte stage slice) and feeds codes 8s .. 8s + 7 of those to k-slice s; the
+// activation fragment of k-slice s, half h is then the 16-byte chunk 4h + s of the token's
+// 64-element stage row. The MFMA sums over all 16 k of a slice, so this relabelling of k is
+// free; A and B only have to agree on it.
+//
+// Pipeline, per 64-wide stage kt (stages are walked four at a time, so every ring slot and
+// LDS buffer index below is a compile-time constant):
+//   * the activations of stage kt + 2, loaded into registers during stage kt - 1, are stored
+//     to LDS buffer (kt + 2) % 4, swizzled so that 32 consecutive token rows of one 16-byte
+//     chunk hit distinct banks;
+//   * four k-slices of 2 x TT MFMAs read activation fragments from buffer kt % 4 and weight
+//     fragments dequantized from a four-stage register ring of packed codes; every k-slice
+//     prepares the fragments of the next one, the last k-slice those of stage kt + 1, whose
+//     buffer is already complete -- so no MFMA waits on LDS and the barrier costs no refill;
+//   * in k-slice 2 the activation loads of stage kt + 3 are issued; at the end of the stage
+//     the packed codes of stage kt + 4 and, once per group (every one or two stages), the
+//     scales and zeros, then one barrier.
+// Scales and zeros are loaded per lane (each lane owns one weight row of a tile); loading them
+// once per group instead of once per stage matters: each such load touches 32 cache lines.
 #include "qcommon.hpp"
 #include "qkernels.hpp"
 
 namespace llmopt {
 namespace {
 
-constexpr int kBM = 256;  // tokens per workgroup
-constexpr int kBN = 256;  // output features per workgroup
+constexpr int kBN = 256;  // output features per workgroup (4 waves x 64)
 constexpr int kBK = 64;   // K per stage
-constexpr int kThreads = 512;
-constexpr int kRing = 4;  // stages of packed codes in flight per thread (even: see the loop)
-constexpr int kGroupM = 8;
+constexpr int kThreads = 256;
+constexpr int kRing = 4;   // stages of packed codes in flight (= LDS activation buffers)
+constexpr int kGroupM = 4;  // token tiles per sweep over the feature tiles
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -66,24 +75,45 @@ struct Mfma32x<ActF16> {
   }
 };
 
-// Byte offset (within a [rows][64] bf16 buffer) of 16-byte chunk `c` of row `r`. A row is half
-// of the 64 banks; XOR-ing the chunk with (r / 2) % 8 gives 16 consecutive rows 16 distinct
-// 4-bank groups, so the 16 lanes that a 16-byte LDS access serves together never collide,
-// both for the fragment reads (16 rows, one chunk) and for the stores (8 rows, two halves).
+// Byte offset (within a [rows][64] buffer of 16-bit values) of 16-byte chunk `c` of row `r`.
+// A row is half of the 64 banks; XOR-ing the chunk with (r / 2) % 8 gives 16 consecutive rows
+// 16 distinct 4-bank groups, so the 16 lanes that a 16-byte LDS access serves together never
+// collide, both for the fragment reads (consecutive rows, one chunk) and for the stores
+// (8 rows, all chunks).
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
-
-
+// Eight packed codes (one 32-bit word) -> the A fragment of one k-slice: four words holding
+// bf16/fp16 pairs (k, k + 1). The nibble mask comes from a kernel argument (its extra bits are
+// always zero), so the compiler cannot tell that only four bits per byte survive and converts
+// each code with one v_cvt_f32_ubyte{0..3}.
 template <class Act>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t nib_mask, float z, float s) {
+  const uint32_t lo = word & nib_mask;         // codes 0, 2, 4, 6
+  const uint32_t hi = (word >> 4) & nib_mask;  // codes 1, 3, 5, 7
+  u32x4 out;
+  out.x = Mfma32x<Act>::pack(dequant_exact(float(lo & 0xFFu), z, s), dequant_exact(float(hi & 0xFFu), z, s));
+  out.y = Mfma32x<Act>::pack(dequant_exact(float((lo >> 8) & 0xFFu), z, s),
+                             dequant_exact(float((hi >> 8) & 0xFFu), z, s));
+  out.z = Mfma32x<Act>::pack(dequant_exact(float((lo >> 16) & 0xFFu), z, s),
+                             dequant_exact(float((hi >> 16) & 0xFFu), z, s));
+  out.w = Mfma32x<Act>::pack(dequant_exact(float(lo >> 24), z, s), dequant_exact(float(hi >> 24), z, s));
+  return out;
+}
+
+template <class Act, int TT, int GP>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
     qlinear_gemm_kernel(const LinearArgs a, int tiles_m, int tiles_n, uint32_t group_magic) {
   using Raw = typename Act::raw;
-  // Two LDS stage buffers as separate arrays: the compiler can then see that the stores of
-  // stage kt + 1 and the fragment reads of stage kt never alias, and interleave them.
-  // Each holds the dequantized weight tile [kBN][64] followed by the activation tile [kBM][64].
-  constexpr int kStage = (kBN + kBM) * kBK * 2;
-  __shared__ __attribute__((aligned(16))) uint8_t sbuf0[kStage];
-  __shared__ __attribute__((aligned(16))) uint8_t sbuf1[kStage];
+  constexpr int kBM = 32 * TT;          // tokens per workgroup
+  constexpr int kXStage = kBM * kBK * 2;  // bytes of one activation stage
+  constexpr int kXPer = kBM * 8 / kThreads;  // 16-byte activation chunks per thread per stage
+  // Three activation stage buffers as separate arrays, so that the compiler can see that the
+  // stores of stage kt + 2 and the fragment reads of stages kt and kt + 1 never alias.
+  __shared__ __attribute__((aligned(16))) uint8_t xs0[kXStage];
+  __shared__ __attribute__((aligned(16))) uint8_t xs1[kXStage];
+  __shared__ __attribute__((aligned(16))) uint8_t xs2[kXStage];
+  __shared__ __attribute__((aligned(16))) uint8_t xs3[kXStage];
+  auto xbuf = [&](int i) -> uint8_t* { return i == 0 ? xs0 : i == 1 ? xs1 : i == 2 ? xs2 : xs3; };
 
   // ---- tile order: even split over the XCDs, then kGroupM token-tiles per feature sweep ----
   int bid = blockIdx.x;
@@ -99,155 +129,163 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wn = wave >> 2;  // 0..1: 128 features
-  const int wm = wave & 3;   // 0..3: 64 tokens
+  const int wave = tid >> 6;  // 0..3: 64 features each
+  const int frow = lane & 31;
+  const int half = lane >> 5;
 
-  // ---- per-thread load assignments ----
-  // Packed codes: row tid/2, 16 bytes (32 codes) at half tid%2 of the stage's 32 bytes.
-  const int w_row = tid >> 1;
-  const int w_half = tid & 1;
-  int64_t wn_row = n0 + w_row;
-  wn_row = wn_row < a.N ? wn_row : a.N - 1;
+  // ---- weight rows of this lane: n0 + 64 wave + 32 i + frow, bytes 16 half .. of a stage ----
   const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
-  const uint32_t wq_off = uint32_t(wn_row * a.ldq + w_half * 16);
   const bool asym = !a.symmetric;
   const uint32_t meta_bytes = uint32_t(a.N * a.G * 4);
   const auto ms = make_rsrc(a.scales, meta_bytes);
   const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_bytes);
-  const uint32_t meta_off = uint32_t(wn_row * a.G * 4);
-  const float z_const = a.zero_const;
-  // Activations: 4 chunks of 16 bytes; chunk e = tid + 512 i -> row tid/8 + 64 i, chunk tid%8.
-  // The swizzle depends on row/2 mod 8, which the + 64 i leaves alone, so the LDS
-  // destinations are one offset plus constants.
-  const auto xr = make_rsrc(a.x, uint32_t(a.M * a.ldx * 2));
-  uint32_t xoff[4];
+  uint32_t wq_off[2], meta_off[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int64_t m = m0 + (tid >> 3) + 64 * i;
+  for (int i = 0; i < 2; ++i) {
+    int64_t n = n0 + 64 * wave + 32 * i + frow;
+    n = n < a.N ? n : a.N - 1;  // rows past N repeat row N-1; their outputs are never stored
+    wq_off[i] = uint32_t(n * a.ldq + half * 16);
+    meta_off[i] = uint32_t(n * a.G * 4);
+  }
+  const float z_const = a.zero_const;
+  const int ktiles = int(a.K / kBK);
+
+  // Packed codes: ring slot u holds stage kt0 + u. Scales and zeros are loaded once per GP
+  // stages (GP = 2 when a group spans a multiple of two stages, else 1) into meta slot u / GP.
+  // GP stops at 2: the first k-slice of stage kt + 1 is dequantized during stage kt, so a meta
+  // slot must be refilled a stage before its first use, which needs at least two slots.
+  static_assert(GP == 1 || GP == 2, "metadata period of one or two stages");
+  u32x4 wring[kRing][2];
+  float sring[kRing][2], zring[kRing][2];
+  auto load_codes = [&](int slot, int kt) {
+    const int ktc = kt < ktiles ? kt : ktiles - 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) wring[slot][i] = buf_load16(wq, wq_off[i], uint32_t(ktc) * 32);
+  };
+  auto load_meta = [&](int slot, int kt) {
+    const int ktc = kt < ktiles ? kt : ktiles - 1;
+    // The group index can differ between the two halves of a wave (group 32), so it goes in
+    // the per-lane offset; a lane-varying scalar offset would turn each load into a loop.
+    const uint32_t g4 = div_small(uint32_t(ktc * kBK + half * 32), group_magic) * 4;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      sring[slot][i] = buf_load_f32(ms, meta_off[i] + g4, 0);
+      zring[slot][i] = buf_load_f32(mz, meta_off[i] + g4, 0);
+    }
+  };
+
+  // ---- activations: chunk e = tid + 256 i -> token row tid / 8 + 32 i, chunk tid % 8 ----
+  // The swizzle depends on row / 2 mod 8, which + 32 i leaves alone, so the LDS destinations
+  // are one offset plus constants.
+  const auto xr = make_rsrc(a.x, uint32_t(a.M * a.ldx * 2));
+  uint32_t xoff[kXPer];
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    int64_t m = m0 + (tid >> 3) + 32 * i;
     m = m < a.M ? m : a.M - 1;  // rows past M repeat row M-1; their outputs are never stored
     xoff[i] = uint32_t((m * a.ldx + 8 * (tid & 7)) * 2);
   }
-  const int xdst = kBN * 128 + swz(tid >> 3, tid & 7);
-
-  u32x4 wring[kRing];
-  float sring[kRing], zring[kRing];
-  auto load_w = [&](int slot, int kt) {
-    const int ktc = kt < (int)(a.K / kBK) ? kt : (int)(a.K / kBK) - 1;
-    wring[slot] = buf_load16(wq, wq_off, uint32_t(ktc) * 32);
-    // The group index differs between the two threads of a row (w_half), so it goes in the
-    // per-lane offset; a lane-varying scalar offset would turn each load into a loop.
-    const uint32_t g = div_small(uint32_t(ktc * kBK + w_half * 32), group_magic);
-    sring[slot] = buf_load_f32(ms, meta_off + g * 4, 0);
-    zring[slot] = buf_load_f32(mz, meta_off + g * 4, 0);
-  };
-  u32x4 xreg[4];
+  const int xdst = swz(tid >> 3, tid & 7);
+  u32x4 xreg[kXPer];
   auto load_x = [&](int kt) {
-    const int ktc = kt < (int)(a.K / kBK) ? kt : (int)(a.K / kBK) - 1;
+    const int ktc = kt < ktiles ? kt : ktiles - 1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xreg[i] = buf_load16(xr, xoff[i], uint32_t(ktc) * (kBK * 2));
-  };
-  // Dequantize ring slot -> 32 bf16/fp16 weights -> four 16-byte chunks of the W buffer, with
-  // the reference's arithmetic: fp32 (q - z), then * s, each rounded once, then a round-to-
-  // nearest-even cast (bit-exact for any zero point). The nibble mask comes from a kernel
-  // argument (its extra bits are always zero), so the compiler cannot tell that only four bits
-  // per byte survive and converts each code with one v_cvt_f32_ubyte{0..3}: 31 VALU per 8
-  // codes, with nothing (such as an asm barrier) that would stop the scheduler from spreading
-  // them between the MFMAs.
-  const uint32_t nib_mask = 0x0F0F0F0Fu | uint32_t(uint64_t(a.ldq) >> 48);
-  auto stash_w = [&](int slot, uint8_t* buf) {
-    const float s = sring[slot];
-    const float z = asym ? zring[slot] : z_const;
-    const uint32_t words[4] = {wring[slot].x, wring[slot].y, wring[slot].z, wring[slot].w};
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t lo = words[d] & nib_mask;         // codes 0, 2, 4, 6 of this word
-      const uint32_t hi = (words[d] >> 4) & nib_mask;  // codes 1, 3, 5, 7
-      u32x4 out;
-      out.x = Mfma32x<Act>::pack(dequant_exact(float(lo & 0xFFu), z, s),
-                                 dequant_exact(float(hi & 0xFFu), z, s));
-      out.y = Mfma32x<Act>::pack(dequant_exact(float((lo >> 8) & 0xFFu), z, s),
-                                 dequant_exact(float((hi >> 8) & 0xFFu), z, s));
-      out.z = Mfma32x<Act>::pack(dequant_exact(float((lo >> 16) & 0xFFu), z, s),
-                                 dequant_exact(float((hi >> 16) & 0xFFu), z, s));
-      out.w = Mfma32x<Act>::pack(dequant_exact(float(lo >> 24), z, s),
-                                 dequant_exact(float(hi >> 24), z, s));
-      *reinterpret_cast<u32x4*>(buf + swz(w_row, w_half * 4 + d)) = out;
-    }
+    for (int i = 0; i < kXPer; ++i) xreg[i] = buf_load16(xr, xoff[i], uint32_t(ktc) * (kBK * 2));
   };
   auto stash_x = [&](uint8_t* buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(buf + xdst + 64 * 128 * i) = xreg[i];
+    for (int i = 0; i < kXPer; ++i) *reinterpret_cast<u32x4*>(buf + xdst + 32 * 128 * i) = xreg[i];
   };
 
-  const int ktiles = int(a.K / kBK);
-  // ---- prologue ----
-#pragma unroll
-  for (int r = 0; r < kRing; ++r) load_w(r, r);
+  const uint32_t nib_mask = 0x0F0F0F0Fu | uint32_t(uint64_t(a.ldq) >> 48);
+
+  // ---- prologue: activations of stages 0 and 1 in LDS, stage 2 in registers, codes and
+  //      metadata of stages 0 .. 3 in flight, fragments of stage 0, k-slice 0 ready ----
   load_x(0);
-  stash_w(0, sbuf0);
-  stash_x(sbuf0);
+  stash_x(xs0);
   load_x(1);
-  load_w(0, kRing);  // slot 0 is free again
+  stash_x(xs1);
+  load_x(2);
+#pragma unroll
+  for (int r = 0; r < kRing; ++r) load_codes(r, r);
+#pragma unroll
+  for (int r = 0; r < kRing / GP; ++r) load_meta(r, r * GP);
   __syncthreads();
 
-  f32x16 acc[4][2];
+  f32x16 acc[2][TT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TT; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const int frag_row = lane & 31;
-  const int frag_half = lane >> 5;
-  // The ring slot holding stage kt + 1 is (kt + 1) % kRing; stages are walked kRing at a time
-  // so that every slot index and the buffer parity are constants. The main loop has no
-  // conditional stage: a loop-back path that skipped stages would make the compiler wait for
-  // every load in flight at the top of the loop.
+  auto read_b = [&](const uint8_t* buf, int ks, u32x4* bf) {
+#pragma unroll
+    for (int j = 0; j < TT; ++j)
+      bf[j] = *reinterpret_cast<const u32x4*>(buf + swz(32 * j + frow, 4 * half + ks));
+  };
+  auto dequant_a = [&](int u, int ks, u32x4* af) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const u32x4 q = wring[u][i];
+      const uint32_t w = ks == 0 ? q.x : ks == 1 ? q.y : ks == 2 ? q.z : q.w;
+      af[i] = dequant8<Act>(w, nib_mask, asym ? zring[u / GP][i] : z_const, sring[u / GP][i]);
+    }
+  };
+  u32x4 af[2], bf[TT];
+  read_b(xs0, 0, bf);
+  dequant_a(0, 0, af);
+
+  // Stage kt uses LDS buffer kt % 4 and ring slot kt % 4; stages are walked four at a time so
+  // that both are constants. The main loop has no conditional stage: a loop-back path that
+  // skipped stages would make the compiler wait for every load in flight at the top of the
+  // loop. Each k-slice prepares the fragments of the next one (the last k-slice those of the
+  // next stage, whose activations were stored a stage earlier), so no MFMA waits for LDS.
+  // Buffer (kt + 2) % 4, stored during stage kt, was last read during stage kt - 2 (and its
+  // first fragments during kt - 3): the barrier that ends stage kt - 1 orders the two.
+  static_assert(kRing == 4, "the stage loop assumes a four-deep ring");
   auto stage = [&](const int u, const int kt) {
-    // kt - u is a multiple of kRing (even), so kt & 1 == u & 1 is a compile-time constant.
-    uint8_t* cur = (u & 1) ? sbuf1 : sbuf0;
-    uint8_t* nxt = (u & 1) ? sbuf0 : sbuf1;
-    const uint8_t* wb = cur;
-    const uint8_t* xb = cur + kBN * 128;
-    // Stage kt + 1 into the other buffer (the last stage re-stages the clamped last stage,
-    // which nothing reads) -- independent of the MFMAs below, so the scheduler can
-    // interleave the two.
-    stash_w((u + 1) % kRing, nxt);
-    stash_x(nxt);
+    const uint8_t* cur = xbuf(u);
+    const uint8_t* nxt = xbuf((u + 1) % 4);
+    stash_x(xbuf((u + 2) % 4));  // stage kt + 2 (past the end: a clamped stage nobody reads)
 #pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      u32x4 af[4], bf[2];
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      // The activation registers were stored to LDS during k-slices 0 and 1; refill them here,
+      // so that at the next stage's stores only the later code loads are still in flight.
+      if (ks == 2) load_x(kt + 3);
+      u32x4 an[2], bn[TT];
+      if (ks < kBK / 16 - 1) {
+        read_b(cur, ks + 1, bn);
+        dequant_a(u, ks + 1, an);
+      } else {
+        read_b(nxt, 0, bn);
+        dequant_a((u + 1) % 4, 0, an);
+      }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const u32x4*>(wb + swz(wn * 128 + 32 * i + frag_row, 2 * s + frag_half));
+      for (int j = 0; j < TT; ++j)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *reinterpret_cast<const u32x4*>(xb + swz(wm * 64 + 32 * j + frag_row, 2 * s + frag_half));
+        for (int i = 0; i < 2; ++i) acc[i][j] = Mfma32x<Act>::run(af[i], bf[j], acc[i][j]);
+      // Per pair of MFMAs: eight dequantization VALU ops and one fragment read; the
+      // activation stores go with the first two k-slices.
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int p = 0; p < TT; ++p) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        if (ks < 2 && (p & 1)) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS store
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = Mfma32x<Act>::run(af[i], bf[j], acc[i][j]);
+      for (int j = 0; j < TT; ++j) bf[j] = bn[j];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = an[i];
     }
-    // Issue order: the first k-slice's fragments, then per MFMA a few dequantization VALU
-    // ops, spreading the fragment reads and the LDS stores of the next stage between them.
-    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // 6 LDS reads
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS store
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS reads
-    }
-    load_x(kt + 2);
-    load_w((u + 1) % kRing, kt + 1 + kRing);
+    load_codes(u, kt + kRing);
+    // Meta slot u / GP was last read for stage kt (its last k-slices were dequantized above).
+    if (u % GP == GP - 1) load_meta(u / GP, kt + 1 + kRing - GP);
     __syncthreads();
   };
   int kt0 = 0;
@@ -265,14 +303,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   Raw* y = static_cast<Raw*>(a.y);
   const bool vec = (a.ldy % 4 == 0) && (reinterpret_cast<uintptr_t>(a.y) % 8 == 0);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t m = m0 + wm * 64 + 32 * j + (lane & 31);
+  for (int j = 0; j < TT; ++j) {
+    const int64_t m = m0 + 32 * j + frow;
     if (m >= a.M) continue;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int64_t n = n0 + wn * 128 + 32 * i + 8 * q + 4 * (lane >> 5);
+        const int64_t n = n0 + 64 * wave + 32 * i + 8 * q + 4 * half;
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -295,32 +333,39 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   }
 }
 
+template <class Act, int TT>
+void launch_tt(const LinearArgs& a, hipStream_t stream, uint32_t magic) {
+  const bool gp2 = a.group % 128 == 0;
+  const int64_t tm = (a.M + 32 * TT - 1) / (32 * TT);
+  const int64_t tn = (a.N + kBN - 1) / kBN;
+  const dim3 grid(unsigned(tm * tn)), block(kThreads);
+  if (gp2)
+    hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2>), grid, block, 0, stream, a, int(tm), int(tn), magic);
+  else
+    hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1>), grid, block, 0, stream, a, int(tm), int(tn), magic);
+}
+
 }  // namespace
 
 hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fits) {
   *fits = false;
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
   if (a.fmt != kNibble || a.M < 1) return hipSuccess;
-  // A thread's 32 codes of a stage lie in one group; 16-byte aligned rows and activations.
+  // A lane's 32 codes of a stage lie in one group; 16-byte aligned rows and activations.
   if (a.K % kBK != 0 || a.K / kBK >= 65536 || a.group % 32 != 0) return hipSuccess;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return hipSuccess;
   if (a.ldx % 8 != 0 || reinterpret_cast<uintptr_t>(a.x) % 16 != 0) return hipSuccess;
   if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return hipSuccess;
   if (a.M * a.ldx * 2 >= (int64_t(1) << 31)) return hipSuccess;
-  const int64_t tm = (a.M + kBM - 1) / kBM;
-  const int64_t tn = (a.N + kBN - 1) / kBN;
-  if (tm * tn > 0x7FFFFFFF) return hipSuccess;
+  if ((a.M + 255) / 256 * ((a.N + kBN - 1) / kBN) > 0x7FFFFFFF) return hipSuccess;
   const uint32_t g = uint32_t(a.group);
   const uint32_t magic =
       g == 1 ? 0u : uint32_t((uint64_t(1) << 32) / g + ((uint64_t(1) << 32) % g != 0));
   *fits = true;
-  if (a.act == kDtBf16) {
-    hipLaunchKernelGGL(qlinear_gemm_kernel<ActBf16>, dim3(unsigned(tm * tn)), dim3(kThreads), 0,
-                       stream, a, int(tm), int(tn), magic);
-  } else {
-    hipLaunchKernelGGL(qlinear_gemm_kernel<ActF16>, dim3(unsigned(tm * tn)), dim3(kThreads), 0,
-                       stream, a, int(tm), int(tn), magic);
-  }
+  if (a.act == kDtBf16)
+    launch_tt<ActBf16, 8>(a, stream, magic);
+  else
+    launch_tt<ActF16, 8>(a, stream, magic);
   return hipGetLastError();
 }
 

@@ -150,6 +150,9 @@ SMALL_SHAPES = [  # (N, K, group)
     (64, 176, 16),  # tiny-model down_proj: 88-byte packed rows
     (200, 512, 128),  # N not a multiple of any tile
     (96, 384, 64),
+    (64, 448, 32),  # 7 k-stages of 64 (a three-stage tail), two groups per stage
+    (80, 768, 256),  # a group spanning four k-stages
+    (64, 1024, 512),
 ]
 
 
