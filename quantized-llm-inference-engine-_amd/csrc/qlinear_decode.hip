@@ -742,6 +742,207 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
   }
 }
 
+
+// ---- multi-tile kernel (M <= 64, 2/4-bit codes, group a multiple of 128) ---------------------
+//
+// One workgroup owns NT tiles of 16 output features and all of K; its NW waves split K into
+// contiguous ranges of whole 128-code steps, and their partial sums meet in LDS at the end in
+// a fixed wave order. Lane (col, kq) = (lane % 16, lane / 16), per step of 128 codes:
+// * codes: 16 bytes of row n0 + 16t + col at byte 64*step + 16*kq, for each tile t, i.e. codes
+//   k = 32kq .. 32kq + 31 of the step; MFMA j (of four) takes the 8 codes of word j. One 16-byte
+//   load per lane streams 16 rows x 64 bytes per tile -- half cache lines, fully used;
+// * activations: the A operand of MFMA j for token row 16mb + col is then x[32kq + 8j ..+ 8] of
+//   the step -- 64 contiguous bytes per lane and step, read with four 16-byte loads from L2
+//   (the whole x[M, K] is a few hundred KB and stays there) straight into the MFMA layout. A
+//   token block is shared by all NT tiles, so a larger NT cuts the activation traffic per code;
+// * scales and zeros of the workgroup's 16*NT rows are staged in LDS once, with coalesced
+//   16-byte loads (per-lane loads of a scale per row and step would touch as many cache lines
+//   as the codes themselves).
+// Codes and activations stream through a register ring of D steps: each slot is refilled with
+// the step D ahead as soon as it has been consumed, unconditionally (past the end: the last
+// step again), so the loads form one static sequence under the in-order completion counter.
+// Arithmetic as in the kernels above: OFF + q operands (one v_and_or_b32 per code pair), one
+// MFMA per token block against a ones operand for sum_k x_k, and per step and tile
+//     tot += s * (sum_k (OFF + q_k) x_k - (OFF + z) * sum_k x_k).
+constexpr int kMtMetaPer = 2;  // 16-byte metadata pieces per thread of the multi-tile kernel
+
+template <class Act, int NT, int MB, int D, int NW, int WPE>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+    decode_mt_kernel(const LinearArgs a, int ns, uint32_t group_magic) {
+  using Raw = typename Act::raw;
+  extern __shared__ u32x4 lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;
+  const int kq = lane >> 4;
+  const int64_t n0 = int64_t(blockIdx.x) * (16 * NT);
+  const bool asym = !a.symmetric;
+  const int G = int(a.G);
+  // LDS metadata: one (scale, OFF + zero) pair per row and group; rows of G + 2 pairs keep
+  // 16-byte alignment and put the 16 rows a k-quarter reads on distinct banks.
+  const int mstride = G + 2;
+  f32x2* const sz_lds = reinterpret_cast<f32x2*>(lds);
+
+  // ---- issue the loads: the workgroup's scales and zeros (rows n0 .. n0 + 16NT - 1, all G
+  //      groups, one contiguous run of the [N, G] tensors), then the first D ring slots; only
+  //      then wait for the metadata and stage it in LDS ----
+  const uint32_t meta_bytes = uint32_t(a.N * a.G * 4);
+  const auto ms = make_rsrc(a.scales, meta_bytes);
+  const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_bytes);
+  const int pieces = 16 * NT * G / 4;  // G % 4 == 0; at most kMtMetaPer per thread (host check)
+  const uint32_t mbase = uint32_t(n0 * a.G * 4);
+  u32x4 sv[kMtMetaPer], zv[kMtMetaPer];
+#pragma unroll
+  for (int e = 0; e < kMtMetaPer; ++e) {
+    const int p = tid + e * NW * 64;
+    const uint32_t off = mbase + uint32_t(p < pieces ? p : 0) * 16;  // past the tensors: zeros
+    sv[e] = buf_load16(ms, off, 0);
+    zv[e] = buf_load16(mz, off, 0);
+  }
+
+  const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
+  uint32_t qoff[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    int64_t n = n0 + 16 * t + col;
+    n = n < a.N ? n : a.N - 1;  // rows past N repeat row N-1; their sums are never stored
+    qoff[t] = uint32_t(n * a.ldq + 16 * kq);
+  }
+  const uint32_t xbytes = uint32_t(a.M * a.ldx * 2);
+  const auto xr = make_rsrc(a.x, xbytes);
+  uint32_t xoff[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int64_t m = 16 * mb + col;
+    // Token rows past M read past the end of x: the buffer returns zeros.
+    xoff[mb] = m < a.M ? uint32_t(m * a.ldx * 2 + 64 * kq) : xbytes;
+  }
+  const int s_begin = wave * ns;
+
+  u32x4 cw[D][NT];
+  u32x4 cx[D][MB][4];
+  auto load = [&](int slot, int i) {
+    const int step = s_begin + (i < ns ? i : ns - 1);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) cw[slot][t] = buf_load16(wq, qoff[t], uint32_t(step) * 64);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cx[slot][mb][j] = buf_load16(xr, xoff[mb] + 16 * j, uint32_t(step) * 256);
+  };
+#pragma unroll
+  for (int r = 0; r < D; ++r) load(r, r);
+
+  const float z_shift = Act::kNibbleOffset;
+  const float z_const = a.zero_const + z_shift;
+#pragma unroll
+  for (int e = 0; e < kMtMetaPer; ++e) {
+    const int p = tid + e * NW * 64;
+    if (p < pieces) {
+      const int row = (p * 4) / G;
+      const int g = p * 4 - row * G;
+      const f32x4 sf = __builtin_bit_cast(f32x4, sv[e]);
+      const f32x4 zf = __builtin_bit_cast(f32x4, zv[e]);
+      // Symmetric codes use the constant offset, so the arithmetic below never branches.
+      f32x4 lo, hi;
+      lo[0] = sf[0]; lo[1] = asym ? zf[0] + z_shift : z_const;
+      lo[2] = sf[1]; lo[3] = asym ? zf[1] + z_shift : z_const;
+      hi[0] = sf[2]; hi[1] = asym ? zf[2] + z_shift : z_const;
+      hi[2] = sf[3]; hi[3] = asym ? zf[3] + z_shift : z_const;
+      *reinterpret_cast<f32x4*>(sz_lds + row * mstride + g) = lo;
+      *reinterpret_cast<f32x4*>(sz_lds + row * mstride + g + 2) = hi;
+    }
+  }
+  __syncthreads();  // metadata staged
+
+  const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
+  const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+
+  f32x4 tot[NT][MB];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) tot[t][mb] = zero4;
+
+  auto compute = [&](int slot, int i) {
+    const int step = s_begin + i;
+    const int g = int(div_small(uint32_t(step), group_magic));
+    f32x2 sz[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) sz[t] = sz_lds[(16 * t + col) * mstride + g];
+    u32x4 xa[MB][4];
+    f32x4 xs[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xa[mb][j] = arrange<Act, kNibble>(cx[slot][mb][j]);
+      xs[mb] = Mfma16<Act>::run(xa[mb][0], ones, zero4);
+#pragma unroll
+      for (int j = 1; j < 4; ++j) xs[mb] = Mfma16<Act>::run(xa[mb][j], ones, xs[mb]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const float sc = sz[t][0];
+      const float zc = sz[t][1];
+      const u32x4 q = cw[slot][t];
+      const u32x4 b[4] = {nib.operand(q.x), nib.operand(q.y), nib.operand(q.z), nib.operand(q.w)};
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        f32x4 acc = Mfma16<Act>::run(xa[mb][0], b[0], zero4);
+#pragma unroll
+        for (int j = 1; j < 4; ++j) acc = Mfma16<Act>::run(xa[mb][j], b[j], acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          tot[t][mb][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[mb][r], acc[r]), tot[t][mb][r]);
+      }
+    }
+  };
+
+  // D steps at a time, so that every ring slot index is a constant. The refills are
+  // unconditional, so the loads form one static sequence whatever ns is; only the arithmetic
+  // of the steps past the end is skipped. (A second, tail copy of the loop body would give
+  // the register allocator two shapes of the ring to reconcile, which it does by spilling.)
+  for (int i0 = 0; i0 < ns; i0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      if (i0 + u < ns) compute(u, i0 + u);
+      load(u, i0 + u + D);
+    }
+  }
+
+  // ---- fixed-order reduction over the waves: red[wave][t][mb][r][lane] ----
+  __syncthreads();  // every wave is done with the metadata
+  float* red = reinterpret_cast<float*>(lds);
+  constexpr int kElems = NT * MB * 4 * 64;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave * kElems + ((t * MB + mb) * 4 + r) * 64 + lane] = tot[t][mb][r];
+  __syncthreads();
+  const Raw* bias = static_cast<const Raw*>(a.bias);
+  Raw* y = static_cast<Raw*>(a.y);
+  for (int e = tid; e < kElems; e += NW * 64) {
+    const int ln = e & 63;
+    const int r = (e >> 6) & 3;
+    const int tm = e >> 8;
+    const int t = tm / MB;
+    const int mb = tm - t * MB;
+    const int64_t m = 16 * mb + 4 * (ln >> 4) + r;
+    const int64_t n = n0 + 16 * t + (ln & 15);
+    if (m < a.M && n < a.N) {
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) v += red[w * kElems + e];
+      if (bias) v += Act::load(bias[n]);
+      y[m * a.ldy + n] = Act::store(v);
+    }
+  }
+}
+
 // ---- dispatch ----------------------------------------------------------------------------------
 
 template <class Act, int FMT, int CB, int MB, int NT, int NW>
@@ -911,6 +1112,82 @@ bool try_stream(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   return true;
 }
 
+
+// ---- multi-tile kernel dispatch ----
+
+struct MtConfig {
+  int nt, mb, d, nw;
+};
+
+template <class Act, int NT, int MB, int D, int NW, int WPE>
+hipError_t launch_mt_cfg(const LinearArgs& a, int steps, uint32_t magic, hipStream_t stream) {
+  const int64_t blocks = (a.N + 16 * NT - 1) / (16 * NT);
+  const size_t meta = size_t(16) * NT * (a.G + 2) * 8;
+  const size_t red = size_t(NW) * NT * MB * 4 * 64 * 4;
+  const size_t lds = meta > red ? meta : red;
+  auto kern = decode_mt_kernel<Act, NT, MB, D, NW, WPE>;
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(NW * 64), lds, stream, a, steps / NW, magic);
+  return hipGetLastError();
+}
+
+// The instantiated configurations; `pick_mt` chooses among them.
+template <class Act>
+hipError_t launch_mt(const LinearArgs& a, MtConfig c, int steps, uint32_t magic, hipStream_t stream) {
+#define LLMOPT_MT(NT, MB, D, NW, WPE) \
+  if (c.nt == NT && c.mb == MB && c.d == D && c.nw == NW) return launch_mt_cfg<Act, NT, MB, D, NW, WPE>(a, steps, magic, stream);
+  LLMOPT_MT(8, 1, 2, 8, 2)
+  LLMOPT_MT(2, 1, 4, 8, 2)
+  LLMOPT_MT(1, 1, 4, 8, 4)
+  LLMOPT_MT(4, 2, 2, 4, 2)
+  LLMOPT_MT(2, 4, 2, 8, 2)
+#undef LLMOPT_MT
+  return hipErrorInvalidValue;
+}
+
+// Configuration by token blocks MB = ceil(M / 16) (3 -> 4) and output tiles, as measured on
+// MI355X over the Llama-3-8B projections: more feature tiles per workgroup share each
+// activation load across more rows, fewer give the grid more workgroups.
+// Returns nt = 0 when an older kernel is faster (M <= 16 with long rows: the streaming kernel).
+MtConfig pick_mt(const LinearArgs& a, int64_t steps) {
+  const int64_t tiles = (a.N + 15) / 16;
+  if (a.M <= 16) {
+    if (steps > 64) return MtConfig{0, 1, 0, 0};
+    if (tiles >= 1024) return MtConfig{8, 1, 2, 8};
+    if (tiles >= 384) return MtConfig{2, 1, 4, 8};
+    return MtConfig{1, 1, 4, 8};
+  }
+  if (a.M <= 32) return MtConfig{4, 2, 2, 4};
+  return MtConfig{2, 4, 2, 8};
+}
+
+// M <= 64, 2/4-bit codes, groups of a multiple of 128 codes: the multi-tile kernel.
+bool try_mt(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
+  if (a.fmt != kNibble || a.M < 1 || a.M > 64) return false;
+  if (a.group % 128 != 0 || a.K % 128 != 0 || a.G % 4 != 0) return false;
+  if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
+  if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
+  if (a.M * a.ldx * 2 >= (int64_t(1) << 31) || a.K * 2 >= (int64_t(1) << 31)) return false;
+  if ((a.N + 15) / 16 > 0x7FFFFFFF) return false;
+  const int64_t steps = a.K / 128;
+  const MtConfig c = pick_mt(a, steps);
+  if (c.nt == 0 || steps % c.nw != 0) return false;
+  // The metadata block of the workgroup must fit in LDS, and its loads in two per thread.
+  if (size_t(16) * c.nt * (a.G + 2) * 8 > 160 * 1024) return false;
+  if (int64_t(16) * c.nt * a.G / 4 > int64_t(kMtMetaPer) * c.nw * 64) return false;
+  const uint32_t per_group = uint32_t(a.group / 128);
+  const uint32_t magic = per_group == 1 ? 0u
+      : uint32_t((uint64_t(1) << 32) / per_group + ((uint64_t(1) << 32) % per_group != 0));
+  *err = a.act == kDtBf16 ? launch_mt<ActBf16>(a, c, int(steps), magic, stream)
+                          : launch_mt<ActF16>(a, c, int(steps), magic, stream);
+  return true;
+}
+
 hipError_t launch_skinny(const LinearArgs& a, hipStream_t stream, bool* fits) {
   *fits = false;
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
@@ -957,7 +1234,7 @@ hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* f
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
   if (a.M < 1 || a.M > 64) return hipSuccess;
   hipError_t err = hipSuccess;
-  if (try_oneshot(a, stream, &err) || try_stream(a, stream, &err)) {
+  if (try_oneshot(a, stream, &err) || try_mt(a, stream, &err) || try_stream(a, stream, &err)) {
     *fits = true;
     return err;
   }

@@ -153,6 +153,8 @@ SMALL_SHAPES = [  # (N, K, group)
     (64, 448, 32),  # 7 k-stages of 64 (a three-stage tail), two groups per stage
     (80, 768, 256),  # a group spanning four k-stages
     (64, 1024, 512),
+    (80, 1024, 128),  # eight 128-code steps: the multi-tile decode kernel
+    (48, 2048, 256),
 ]
 
 
