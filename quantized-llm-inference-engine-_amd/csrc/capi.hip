@@ -111,15 +111,18 @@ int llmopt_q_dequant(const void* qweight, int64_t ldq, const float* scales, cons
                     "dequant launch");
 }
 
-size_t llmopt_q_linear_workspace(int64_t, int64_t, int64_t, int, int) { return 0; }
+size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
+  // Only the prefill GEMM (M > 64, 2/4-bit codes) splits K; the decode kernels reduce in LDS.
+  if (M <= 64 || N <= 0 || K <= 0 || (bits != 2 && bits != 4)) return 0;
+  const int64_t g = group_size <= 0 ? K : group_size;
+  return llmopt::gemm_workspace_bytes(M, N, K, g);
+}
 
 int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
                        int64_t ldq, const float* scales, const float* zeros, const void* bias,
                        void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
                        int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
                        void* stream, int algo) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (!valid_dtype(act_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", act_dtype);
   if (M < 0) return fail(LLMOPT_ERR_INVALID_ARG, "negative M=%lld", (long long)M);
   llmopt::LinearArgs a{};
@@ -138,6 +141,8 @@ int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const v
   a.ldy = ldy;
   a.M = M;
   a.act = act_dtype;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace ? workspace_bytes : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (K == 0) {

@@ -24,6 +24,8 @@ struct LinearArgs {
   int symmetric;
   int signed_codes;
   float zero_const;     // code offset used when symmetric
+  void* workspace;      // caller-owned device scratch (split-K partial sums), may be null
+  size_t workspace_bytes;
 };
 
 // Each launcher returns hipSuccess or the launch error; `why` is set when the arguments do not
@@ -37,5 +39,7 @@ hipError_t launch_linear_generic(const LinearArgs& a, hipStream_t stream);
 hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* fits);
 hipError_t launch_linear_prefill(const LinearArgs& a, hipStream_t stream, bool* fits);
 hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fits);
+// Workspace the prefill GEMM's split-K plan uses for these sizes (0 when it does not split).
+size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 
 }  // namespace llmopt

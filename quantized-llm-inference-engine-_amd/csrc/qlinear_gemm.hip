@@ -100,14 +100,15 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t nib_mask, floa
   return out;
 }
 
-template <class Act, int TT, int GP>
+template <class Act, int TT, int GP, bool SPLIT>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-    qlinear_gemm_kernel(const LinearArgs a, int tiles_m, int tiles_n, uint32_t group_magic) {
+    qlinear_gemm_kernel(const LinearArgs a, int tiles_m, int tiles_n, uint32_t group_magic,
+                        int splits, float* partials) {
   using Raw = typename Act::raw;
   constexpr int kBM = 32 * TT;          // tokens per workgroup
   constexpr int kXStage = kBM * kBK * 2;  // bytes of one activation stage
   constexpr int kXPer = kBM * 8 / kThreads;  // 16-byte activation chunks per thread per stage
-  // Three activation stage buffers as separate arrays, so that the compiler can see that the
+  // Four activation stage buffers as separate arrays, so that the compiler can see that the
   // stores of stage kt + 2 and the fragment reads of stages kt and kt + 1 never alias.
   __shared__ __attribute__((aligned(16))) uint8_t xs0[kXStage];
   __shared__ __attribute__((aligned(16))) uint8_t xs1[kXStage];
@@ -115,15 +116,19 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   __shared__ __attribute__((aligned(16))) uint8_t xs3[kXStage];
   auto xbuf = [&](int i) -> uint8_t* { return i == 0 ? xs0 : i == 1 ? xs1 : i == 2 ? xs2 : xs3; };
 
-  // ---- tile order: even split over the XCDs, then kGroupM token-tiles per feature sweep ----
+  // ---- tile order: even split over the XCDs; K splits outermost, then kGroupM token-tiles
+  //      per sweep over the feature tiles ----
   int bid = blockIdx.x;
   const int nblk = gridDim.x;
   if (nblk % 8 == 0) bid = (bid % 8) * (nblk / 8) + bid / 8;
+  const int ntiles = tiles_m * tiles_n;
+  const int split = bid / ntiles;
+  const int tile = bid - split * ntiles;
   const int per_group = kGroupM * tiles_n;
-  const int first_m = (bid / per_group) * kGroupM;
+  const int first_m = (tile / per_group) * kGroupM;
   const int rows_in_group = min(tiles_m - first_m, kGroupM);
-  const int tm = first_m + (bid % per_group) % rows_in_group;
-  const int tn = (bid % per_group) / rows_in_group;
+  const int tm = first_m + (tile % per_group) % rows_in_group;
+  const int tn = (tile % per_group) / rows_in_group;
   const int64_t m0 = int64_t(tm) * kBM;
   const int64_t n0 = int64_t(tn) * kBN;
 
@@ -148,7 +153,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
     meta_off[i] = uint32_t(n * a.G * 4);
   }
   const float z_const = a.zero_const;
-  const int ktiles = int(a.K / kBK);
+  // This workgroup's stages: split `split` of the K range, cut at whole metadata periods so
+  // that a period never straddles two splits.
+  const int units = int(a.K / kBK) / GP;
+  const int kt_base = (split * units / splits) * GP;
+  const int ktiles = ((split + 1) * units / splits) * GP - kt_base;
 
   // Packed codes: ring slot u holds stage kt0 + u. Scales and zeros are loaded once per GP
   // stages (GP = 2 when a group spans a multiple of two stages, else 1) into meta slot u / GP.
@@ -158,12 +167,12 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   u32x4 wring[kRing][2];
   float sring[kRing][2], zring[kRing][2];
   auto load_codes = [&](int slot, int kt) {
-    const int ktc = kt < ktiles ? kt : ktiles - 1;
+    const int ktc = kt_base + (kt < ktiles ? kt : ktiles - 1);
 #pragma unroll
     for (int i = 0; i < 2; ++i) wring[slot][i] = buf_load16(wq, wq_off[i], uint32_t(ktc) * 32);
   };
   auto load_meta = [&](int slot, int kt) {
-    const int ktc = kt < ktiles ? kt : ktiles - 1;
+    const int ktc = kt_base + (kt < ktiles ? kt : ktiles - 1);
     // The group index can differ between the two halves of a wave (group 32), so it goes in
     // the per-lane offset; a lane-varying scalar offset would turn each load into a loop.
     const uint32_t g4 = div_small(uint32_t(ktc * kBK + half * 32), group_magic) * 4;
@@ -188,7 +197,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   const int xdst = swz(tid >> 3, tid & 7);
   u32x4 xreg[kXPer];
   auto load_x = [&](int kt) {
-    const int ktc = kt < ktiles ? kt : ktiles - 1;
+    const int ktc = kt_base + (kt < ktiles ? kt : ktiles - 1);
 #pragma unroll
     for (int i = 0; i < kXPer; ++i) xreg[i] = buf_load16(xr, xoff[i], uint32_t(ktc) * (kBK * 2));
   };
@@ -311,10 +320,25 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t n = n0 + 64 * wave + 32 * i + 8 * q + 4 * half;
+        if (SPLIT) {
+          // Split K: fp32 partial sums into partials[split][m][n]; the reduction kernel that
+          // follows on the stream adds the splits in order and applies the bias.
+          float* dst = partials + (size_t(split) * a.M + m) * a.N + n;
+          if (n + 3 < a.N && a.N % 4 == 0) {
+            *reinterpret_cast<f32x4*>(dst) =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n + r < a.N) dst[r] = acc[i][j][4 * q + r];
+          }
+          continue;
+        }
+        const f32x4 t = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          v[r] = acc[i][j][4 * q + r];
+          v[r] = t[r];
           if (bias && n + r < a.N) v[r] += Act::load(bias[n + r]);
         }
         Raw* dst = y + m * a.ldy + n;
@@ -333,19 +357,133 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   }
 }
 
+// y[m, n] = bias[n] + sum over splits, in split order, of partials[split][m][n]: four columns
+// per thread. Deterministic: the order of the additions never depends on timing.
+template <class Act>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const LinearArgs a, const float* partials, int splits) {
+  using Raw = typename Act::raw;
+  const int64_t n4 = (a.N + 3) / 4;
+  const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= a.M * n4) return;
+  const int64_t m = e / n4;
+  const int64_t n = (e - m * n4) * 4;
+  const size_t plane = size_t(a.M) * a.N;
+  const Raw* bias = static_cast<const Raw*>(a.bias);
+  Raw* y = static_cast<Raw*>(a.y) + m * a.ldy;
+  const float* p = partials + size_t(m) * a.N + n;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (n + 3 < a.N && a.N % 4 == 0) {
+    for (int s = 0; s < splits; ++s) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(p + s * plane);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = s == 0 ? t[r] : v[r] + t[r];
+    }
+  } else {
+    for (int s = 0; s < splits; ++s)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < a.N) v[r] = s == 0 ? p[s * plane + r] : v[r] + p[s * plane + r];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (n + r >= a.N) break;
+    float o = v[r];
+    if (bias) o += Act::load(bias[n + r]);
+    y[n + r] = Act::store(o);
+  }
+}
+
+// ---- launch plan: token-tile height (32 * TT) and K splits ----------------------------------
+//
+// A 256 x 256 tile is the most efficient per MFMA, but a short or narrow GEMM gives too few of
+// them for 256 CUs (one workgroup per CU). Smaller token tiles raise the workgroup count at a
+// higher dequantization cost per MFMA; K splits raise it at the cost of storing and re-reading
+// fp32 partial sums that a second kernel adds up. The plan minimizes a simple time model:
+// rounds of 256 workgroups x stages per workgroup x time per stage, plus the partial-sum
+// traffic of a split, with per-stage times measured on MI355X.
+struct GemmPlan {
+  int tt = 0;      // 0: the GEMM does not take these sizes
+  int splits = 1;
+  int64_t tiles_m = 0, tiles_n = 0;
+  size_t partial_bytes = 0;
+  size_t workspace() const { return splits > 1 ? partial_bytes : 0; }
+};
+
+GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t group) {
+  GemmPlan best;
+  if (M < 1 || N < 1 || K % kBK != 0 || group % 32 != 0) return best;
+  const int gp = group % 128 == 0 ? 2 : 1;
+  const int64_t units = K / kBK / gp;
+  const double stage_us[9] = {0, 0, 0.95, 0, 1.35, 0, 0, 0, 2.1};
+  double best_t = 1e30;
+  for (int tt : {8, 4, 2}) {
+    const int64_t tm = (M + 32 * tt - 1) / (32 * tt);
+    const int64_t tn = (N + kBN - 1) / kBN;
+    if (tm * tn > 0x7FFFFFFF / 8) continue;
+    for (int sp = 1; sp <= 8; ++sp) {
+      if (sp > units || (tt == 8 && sp > 1)) break;  // the 256-token tile never splits
+      const int64_t wgs = tm * tn * sp;
+      const int64_t rounds = (wgs + 255) / 256;
+      const double stages = double((units + sp - 1) / sp * gp);
+      // Split: write and re-read sp fp32 planes of M x N at ~4 TB/s, plus one more launch.
+      const double red = sp > 1 ? 2.0 * sp * double(M) * double(N) * 4.0 / 4e6 + 3.0 : 0.0;
+      const double t = double(rounds) * stages * stage_us[tt] + red;
+      if (t < best_t * 0.97) {
+        best_t = t;
+        best.tt = tt;
+        best.splits = sp;
+        best.tiles_m = tm;
+        best.tiles_n = tn;
+      }
+    }
+  }
+  if (best.tt) {
+    best.partial_bytes = size_t(best.splits) * size_t(M) * size_t(N) * 4;
+  }
+  return best;
+}
+
 template <class Act, int TT>
-void launch_tt(const LinearArgs& a, hipStream_t stream, uint32_t magic) {
-  const bool gp2 = a.group % 128 == 0;
-  const int64_t tm = (a.M + 32 * TT - 1) / (32 * TT);
-  const int64_t tn = (a.N + kBN - 1) / kBN;
-  const dim3 grid(unsigned(tm * tn)), block(kThreads);
-  if (gp2)
-    hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2>), grid, block, 0, stream, a, int(tm), int(tn), magic);
-  else
-    hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1>), grid, block, 0, stream, a, int(tm), int(tn), magic);
+void launch_tt(const LinearArgs& a, const GemmPlan& plan, int splits, hipStream_t stream, uint32_t magic) {
+  float* partials = splits > 1 ? static_cast<float*>(a.workspace) : nullptr;
+  const int ntiles = int(plan.tiles_m * plan.tiles_n);
+  const dim3 grid(unsigned(ntiles * splits)), block(kThreads);
+  // The split epilogue is a separate instantiation: its extra live values would push the
+  // 256-token tile's main loop into spills.
+  constexpr bool kCanSplit = TT < 8;
+  const int tm = int(plan.tiles_m), tn = int(plan.tiles_n);
+  if (kCanSplit && splits > 1) {
+    if (a.group % 128 == 0)
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, kCanSplit>), grid, block, 0, stream, a, tm, tn,
+                         magic, splits, partials);
+    else
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, kCanSplit>), grid, block, 0, stream, a, tm, tn,
+                         magic, splits, partials);
+    const int64_t threads = a.M * ((a.N + 3) / 4);
+    hipLaunchKernelGGL(splitk_reduce_kernel<Act>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
+                       a, partials, splits);
+  } else {
+    if (a.group % 128 == 0)
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, false>), grid, block, 0, stream, a, tm, tn, magic, 1,
+                         partials);
+    else
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, false>), grid, block, 0, stream, a, tm, tn, magic, 1,
+                         partials);
+  }
+}
+
+template <class Act>
+void launch_act(const LinearArgs& a, const GemmPlan& plan, int splits, hipStream_t stream, uint32_t magic) {
+  if (plan.tt == 8) launch_tt<Act, 8>(a, plan, splits, stream, magic);
+  else if (plan.tt == 4) launch_tt<Act, 4>(a, plan, splits, stream, magic);
+  else launch_tt<Act, 2>(a, plan, splits, stream, magic);
 }
 
 }  // namespace
+
+size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
+  return plan_gemm(M, N, K, group).workspace();
+}
 
 hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fits) {
   *fits = false;
@@ -357,15 +495,21 @@ hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fit
   if (a.ldx % 8 != 0 || reinterpret_cast<uintptr_t>(a.x) % 16 != 0) return hipSuccess;
   if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return hipSuccess;
   if (a.M * a.ldx * 2 >= (int64_t(1) << 31)) return hipSuccess;
-  if ((a.M + 255) / 256 * ((a.N + kBN - 1) / kBN) > 0x7FFFFFFF) return hipSuccess;
+  const GemmPlan plan = plan_gemm(a.M, a.N, a.K, a.group);
+  if (plan.tt == 0) return hipSuccess;
+  // Without a large enough workspace the plan runs unsplit (same tiles, one workgroup per tile).
+  int splits = plan.splits;
+  if (splits > 1 && (a.workspace == nullptr || a.workspace_bytes < plan.workspace() ||
+                     reinterpret_cast<uintptr_t>(a.workspace) % 16 != 0))
+    splits = 1;
   const uint32_t g = uint32_t(a.group);
   const uint32_t magic =
       g == 1 ? 0u : uint32_t((uint64_t(1) << 32) / g + ((uint64_t(1) << 32) % g != 0));
   *fits = true;
   if (a.act == kDtBf16)
-    launch_tt<ActBf16, 8>(a, stream, magic);
+    launch_act<ActBf16>(a, plan, splits, stream, magic);
   else
-    launch_tt<ActF16, 8>(a, stream, magic);
+    launch_act<ActF16>(a, plan, splits, stream, magic);
   return hipGetLastError();
 }
 

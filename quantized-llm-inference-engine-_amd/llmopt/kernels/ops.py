@@ -177,6 +177,10 @@ def quant_linear(
         if bias is not None:
             bias = bias.contiguous()
         lib = load_library()
+        # Scratch for split-K partial sums (only some prefill shapes use it); it comes from
+        # torch's caching allocator, so repeated calls reuse the same block.
+        ws_bytes = int(lib.llmopt_q_linear_workspace(m, rows, cols, int(qt.bits), group))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
         call(
             lib.llmopt_q_linear_ex(
                 x2.data_ptr(),
@@ -196,8 +200,8 @@ def quant_linear(
                 group,
                 int(bool(qt.symmetric)),
                 int(signed),
-                None,
-                0,
+                ws.data_ptr() if ws is not None else None,
+                ws_bytes,
                 _stream_handle(x.device),
                 int(algo),
             ),
