@@ -49,6 +49,7 @@ constexpr int kGroupM = 4;  // token tiles per sweep over the feature tiles
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned char uc4 __attribute__((ext_vector_type(4)));
 
 template <class Act>
 struct Mfma32x;
@@ -88,15 +89,15 @@ __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >>
 // each code with one v_cvt_f32_ubyte{0..3}.
 template <class Act>
 __device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t nib_mask, float z, float s) {
-  const uint32_t lo = word & nib_mask;         // codes 0, 2, 4, 6
-  const uint32_t hi = (word >> 4) & nib_mask;  // codes 1, 3, 5, 7
+  // Byte lanes of a vector (rather than shifts and masks) make every code one
+  // v_cvt_f32_ubyte{0..3}; a shift-and-mask of byte 2 becomes v_bfe_u32 plus a conversion.
+  const uc4 lo = __builtin_bit_cast(uc4, word & nib_mask);         // codes 0, 2, 4, 6
+  const uc4 hi = __builtin_bit_cast(uc4, (word >> 4) & nib_mask);  // codes 1, 3, 5, 7
   u32x4 out;
-  out.x = Mfma32x<Act>::pack(dequant_exact(float(lo & 0xFFu), z, s), dequant_exact(float(hi & 0xFFu), z, s));
-  out.y = Mfma32x<Act>::pack(dequant_exact(float((lo >> 8) & 0xFFu), z, s),
-                             dequant_exact(float((hi >> 8) & 0xFFu), z, s));
-  out.z = Mfma32x<Act>::pack(dequant_exact(float((lo >> 16) & 0xFFu), z, s),
-                             dequant_exact(float((hi >> 16) & 0xFFu), z, s));
-  out.w = Mfma32x<Act>::pack(dequant_exact(float(lo >> 24), z, s), dequant_exact(float(hi >> 24), z, s));
+  out.x = Mfma32x<Act>::pack(dequant_exact(float(lo.x), z, s), dequant_exact(float(hi.x), z, s));
+  out.y = Mfma32x<Act>::pack(dequant_exact(float(lo.y), z, s), dequant_exact(float(hi.y), z, s));
+  out.z = Mfma32x<Act>::pack(dequant_exact(float(lo.z), z, s), dequant_exact(float(hi.z), z, s));
+  out.w = Mfma32x<Act>::pack(dequant_exact(float(lo.w), z, s), dequant_exact(float(hi.w), z, s));
   return out;
 }
 
