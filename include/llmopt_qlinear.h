@@ -111,6 +111,30 @@ int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const v
                        int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
                        void* stream, int algo);
 
+/*
+ * Bytes of workspace llmopt_q_linear_swiglu may use for these sizes (N = fused rows),
+ * assuming 16-byte aligned, contiguous tensors (0 if none).
+ */
+size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size);
+
+/*
+ * The gated activation of the reference's MLP, silu(gate(x)) * up(x), from one quantized
+ * weight holding both projections. Replaces the gate_proj / up_proj / silu / multiply part of
+ * SwiGLUMLP.forward (src/llmopt/model/layers.py:43-44): two F.linear calls and two
+ * elementwise passes over [M, intermediate].
+ * Fused row 8p + r (r < 4) is gate row 4p + r and fused row 8p + 4 + r is up row 4p + r;
+ * scales, zeros and bias follow the same order. N (fused rows) must be a multiple of 8.
+ * y: [M, N/2] act_dtype, row stride ldy. Rounding as the reference's sequence: gate and up
+ * rounded to act_dtype, silu in fp32 on the rounded gate and rounded, the product rounded.
+ * Kernels without the fused activation write the full product into `workspace` first;
+ * when that is too small the call returns LLMOPT_ERR_WORKSPACE and names the size.
+ */
+int llmopt_q_linear_swiglu(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                           int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                           void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                           int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

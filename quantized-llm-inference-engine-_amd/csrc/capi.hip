@@ -76,6 +76,98 @@ int describe_weight(llmopt::LinearArgs& a, const void* qweight, int64_t ldq, con
   return LLMOPT_OK;
 }
 
+
+size_t swiglu_temp_bytes(int64_t M, int64_t N) { return (size_t(M) * size_t(N) * 4 + 255) / 256 * 256; }
+
+// Dispatch shared by llmopt_q_linear_ex and llmopt_q_linear_swiglu. With the SwiGLU epilogue,
+// `y` is [M, N/2]; kernels that cannot apply it themselves write the full [M, N] product into
+// the workspace and a combining kernel finishes.
+int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight, int64_t ldq,
+               const float* scales, const float* zeros, const void* bias, void* y, int64_t N,
+               int64_t ldy, int act_dtype, int bits, int group_size, int symmetric, int signed_codes,
+               void* workspace, size_t workspace_bytes, void* stream, int algo, int epilogue) {
+  if (!valid_dtype(act_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", act_dtype);
+  if (M < 0) return fail(LLMOPT_ERR_INVALID_ARG, "negative M=%lld", (long long)M);
+  llmopt::LinearArgs a{};
+  int rc = describe_weight(a, qweight, ldq, scales, zeros, N, K, bits, group_size, symmetric,
+                           signed_codes);
+  if (rc != LLMOPT_OK) return rc;
+  if (M == 0 || N == 0) return LLMOPT_OK;
+  const int64_t ycols = epilogue == llmopt::kEpiSwiglu ? N / 2 : N;
+  if (ldx < K || ldy < ycols)
+    return fail(LLMOPT_ERR_INVALID_ARG, "row strides ldx=%lld ldy=%lld below K=%lld N=%lld",
+                (long long)ldx, (long long)ldy, (long long)K, (long long)ycols);
+  if (!x || !y) return fail(LLMOPT_ERR_INVALID_ARG, "null activation or output");
+  a.x = x;
+  a.bias = bias;
+  a.y = y;
+  a.ldx = ldx;
+  a.ldy = ldy;
+  a.M = M;
+  a.act = act_dtype;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace ? workspace_bytes : 0;
+  a.epilogue = epilogue;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (K == 0 && epilogue == llmopt::kEpiNone) {
+    // An empty reduction: the reference's F.linear returns the bias (or zeros).
+    a.K = 0;
+    return hip_status(llmopt::launch_linear_generic(a, s), "linear launch");
+  }
+
+  bool fits = false;
+  hipError_t err = hipSuccess;
+  if (epilogue != llmopt::kEpiNone) {
+    // Kernels with the fused epilogue first.
+    if (K > 0 && algo == LLMOPT_ALGO_AUTO) {
+      if (M <= 64)
+        err = llmopt::launch_linear_decode(a, s, &fits);
+      else
+        err = llmopt::launch_linear_gemm(a, s, &fits);
+      if (fits) return hip_status(err, "linear launch");
+    }
+    // Then the plain product into the workspace, and the combining kernel.
+    const size_t temp = swiglu_temp_bytes(M, N);
+    if (!workspace || workspace_bytes < temp || reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+      return fail(LLMOPT_ERR_WORKSPACE, "this shape needs a workspace of at least %zu bytes",
+                  temp + llmopt_q_linear_workspace(M, N, K, bits, group_size));
+    void* t = workspace;
+    rc = run_linear(x, M, K, ldx, qweight, ldq, scales, zeros, bias, t, N, N, act_dtype, bits,
+                    group_size, symmetric, signed_codes, static_cast<uint8_t*>(workspace) + temp,
+                    workspace_bytes - temp, stream, algo, llmopt::kEpiNone);
+    if (rc != LLMOPT_OK) return rc;
+    return hip_status(llmopt::launch_swiglu_combine(t, N, y, ldy, M, N, act_dtype, s), "swiglu launch");
+  }
+
+  switch (algo) {
+    case LLMOPT_ALGO_AUTO:
+      if (M <= 64) {
+        err = llmopt::launch_linear_decode(a, s, &fits);
+      } else {
+        err = llmopt::launch_linear_gemm(a, s, &fits);
+        if (!fits) err = llmopt::launch_linear_prefill(a, s, &fits);
+      }
+      if (!fits) err = llmopt::launch_linear_generic(a, s);
+      break;
+    case LLMOPT_ALGO_GENERIC:
+      err = llmopt::launch_linear_generic(a, s);
+      break;
+    case LLMOPT_ALGO_DECODE:
+      err = llmopt::launch_linear_decode(a, s, &fits);
+      if (!fits) return fail(LLMOPT_ERR_UNSUPPORTED, "decode kernel does not take these arguments");
+      break;
+    case LLMOPT_ALGO_PREFILL:
+      err = llmopt::launch_linear_gemm(a, s, &fits);
+      if (!fits) err = llmopt::launch_linear_prefill(a, s, &fits);
+      if (!fits) return fail(LLMOPT_ERR_UNSUPPORTED, "prefill kernel does not take these arguments");
+      break;
+    default:
+      return fail(LLMOPT_ERR_INVALID_ARG, "unknown algo %d", algo);
+  }
+  return hip_status(err, "linear launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -123,62 +215,33 @@ int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const v
                        void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
                        int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
                        void* stream, int algo) {
-  if (!valid_dtype(act_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", act_dtype);
-  if (M < 0) return fail(LLMOPT_ERR_INVALID_ARG, "negative M=%lld", (long long)M);
-  llmopt::LinearArgs a{};
-  int rc = describe_weight(a, qweight, ldq, scales, zeros, N, K, bits, group_size, symmetric,
-                           signed_codes);
-  if (rc != LLMOPT_OK) return rc;
-  if (M == 0 || N == 0) return LLMOPT_OK;
-  if (ldx < K || ldy < N)
-    return fail(LLMOPT_ERR_INVALID_ARG, "row strides ldx=%lld ldy=%lld below K=%lld N=%lld",
-                (long long)ldx, (long long)ldy, (long long)K, (long long)N);
-  if (!x || !y) return fail(LLMOPT_ERR_INVALID_ARG, "null activation or output");
-  a.x = x;
-  a.bias = bias;
-  a.y = y;
-  a.ldx = ldx;
-  a.ldy = ldy;
-  a.M = M;
-  a.act = act_dtype;
-  a.workspace = workspace;
-  a.workspace_bytes = workspace ? workspace_bytes : 0;
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  return run_linear(x, M, K, ldx, qweight, ldq, scales, zeros, bias, y, N, ldy, act_dtype, bits,
+                    group_size, symmetric, signed_codes, workspace, workspace_bytes, stream, algo,
+                    llmopt::kEpiNone);
+}
 
-  if (K == 0) {
-    // An empty reduction: the reference's F.linear returns the bias (or zeros).
-    a.K = 0;
-    return hip_status(llmopt::launch_linear_generic(a, s), "linear launch");
-  }
+size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const int64_t g = group_size <= 0 ? K : group_size;
+  const bool nibble = bits == 2 || bits == 4;
+  // Sizes whose kernels apply the activation themselves (assuming aligned, contiguous tensors).
+  if (nibble && M <= 64 && g % 128 == 0 && K % 128 == 0 && (K / g) % 4 == 0 && (M <= 4 || K <= 8192))
+    return 0;
+  if (nibble && M > 64 && g % 32 == 0 && K % 64 == 0) return llmopt::gemm_workspace_bytes(M, N, K, g);
+  // Otherwise: the full [M, N] output in fp32-sized slots, then the combining kernel.
+  return swiglu_temp_bytes(M, N) + llmopt_q_linear_workspace(M, N, K, bits, group_size);
+}
 
-  bool fits = false;
-  hipError_t err = hipSuccess;
-  switch (algo) {
-    case LLMOPT_ALGO_AUTO:
-      if (M <= 64) {
-        err = llmopt::launch_linear_decode(a, s, &fits);
-      } else {
-        err = llmopt::launch_linear_gemm(a, s, &fits);
-        if (!fits) err = llmopt::launch_linear_prefill(a, s, &fits);
-      }
-      if (!fits) err = llmopt::launch_linear_generic(a, s);
-      break;
-    case LLMOPT_ALGO_GENERIC:
-      err = llmopt::launch_linear_generic(a, s);
-      break;
-    case LLMOPT_ALGO_DECODE:
-      err = llmopt::launch_linear_decode(a, s, &fits);
-      if (!fits) return fail(LLMOPT_ERR_UNSUPPORTED, "decode kernel does not take these arguments");
-      break;
-    case LLMOPT_ALGO_PREFILL:
-      err = llmopt::launch_linear_gemm(a, s, &fits);
-      if (!fits) err = llmopt::launch_linear_prefill(a, s, &fits);
-      if (!fits) return fail(LLMOPT_ERR_UNSUPPORTED, "prefill kernel does not take these arguments");
-      break;
-    default:
-      return fail(LLMOPT_ERR_INVALID_ARG, "unknown algo %d", algo);
-  }
-  return hip_status(err, "linear launch");
+int llmopt_q_linear_swiglu(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                           int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                           void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                           int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (N % 8 != 0)
+    return fail(LLMOPT_ERR_INVALID_ARG, "fused gate/up rows N=%lld are not a multiple of 8", (long long)N);
+  return run_linear(x, M, K, ldx, qweight, ldq, scales, zeros, bias, y, N, ldy, act_dtype, bits,
+                    group_size, symmetric, signed_codes, workspace, workspace_bytes, stream,
+                    LLMOPT_ALGO_AUTO, llmopt::kEpiSwiglu);
 }
 
 int llmopt_q_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,

@@ -74,6 +74,18 @@ struct ActBf16 {
   __device__ static raw store(float f) { return f32_to_bf16_rne(f); }
 };
 
+// The gated activation of the reference's MLP, silu(gate(x)) * up(x) (layers.py:44), with its
+// roundings: gate and up are linear outputs in the compute dtype, silu runs in fp32 on the
+// rounded gate and is rounded, and the product of the two rounded values is rounded by the
+// caller's store.
+template <class Act>
+__device__ __forceinline__ float swiglu(float g, float u) {
+  const float gr = Act::load(Act::store(g));
+  const float ur = Act::load(Act::store(u));
+  const float s = Act::load(Act::store(gr / (1.0f + expf(-gr))));
+  return s * ur;
+}
+
 // ---- code access -----------------------------------------------------------------------------
 
 // Numeric value of code k of one weight row, exactly as the reference reads it:

@@ -26,7 +26,12 @@ struct LinearArgs {
   float zero_const;     // code offset used when symmetric
   void* workspace;      // caller-owned device scratch (split-K partial sums), may be null
   size_t workspace_bytes;
+  // kEpiSwiglu: the weight rows are gate and up projections interleaved in blocks of four
+  // (fused rows 8p .. 8p+3 = gate features 4p .. 4p+3, rows 8p+4 .. 8p+7 = up features
+  // 4p .. 4p+3) and y[m, 4p + r] = silu(gate) * up; y then has N / 2 columns.
+  int epilogue;
 };
+enum : int { kEpiNone = 0, kEpiSwiglu = 1 };
 
 // Each launcher returns hipSuccess or the launch error; `why` is set when the arguments do not
 // fit the kernel (then hipErrorInvalidValue is returned and nothing is launched).
@@ -39,6 +44,10 @@ hipError_t launch_linear_generic(const LinearArgs& a, hipStream_t stream);
 hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* fits);
 hipError_t launch_linear_prefill(const LinearArgs& a, hipStream_t stream, bool* fits);
 hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fits);
+// y[m, 4p + r] = silu(t[m, 8p + r]) * t[m, 8p + 4 + r] for a full fused output t [M, N]
+// (row stride ldt) in the activation dtype: the path for kernels without the fused epilogue.
+hipError_t launch_swiglu_combine(const void* t, int64_t ldt, void* y, int64_t ldy, int64_t M, int64_t N,
+                                 int act, hipStream_t stream);
 // Workspace the prefill GEMM's split-K plan uses for these sizes (0 when it does not split).
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 

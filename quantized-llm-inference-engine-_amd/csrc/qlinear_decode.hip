@@ -737,7 +737,14 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
     const int64_t nn = tile * 16 + c;
     if (nn < a.N) {
       if (a.bias) v += Act::load(static_cast<const Raw*>(a.bias)[nn]);
-      static_cast<Raw*>(a.y)[m * a.ldy + nn] = Act::store(v);
+      if (a.epilogue == kEpiSwiglu) {
+        // Gate rows 8p .. 8p+3 and up rows 8p+4 .. 8p+7 sit four lanes apart (N % 8 == 0).
+        const float up = __shfl_xor(v, 4, 64);
+        if ((c & 4) == 0)
+          static_cast<Raw*>(a.y)[m * a.ldy + (nn >> 3) * 4 + (c & 3)] = Act::store(swiglu<Act>(v, up));
+      } else {
+        static_cast<Raw*>(a.y)[m * a.ldy + nn] = Act::store(v);
+      }
     }
   }
 }
@@ -938,7 +945,13 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WP
 #pragma unroll
       for (int w = 0; w < NW; ++w) v += red[w * kElems + e];
       if (bias) v += Act::load(bias[n]);
-      y[m * a.ldy + n] = Act::store(v);
+      if (a.epilogue == kEpiSwiglu) {
+        // Gate rows 8p .. 8p+3 and up rows 8p+4 .. 8p+7 sit four lanes apart (N % 8 == 0).
+        const float up = __shfl_xor(v, 4, 64);
+        if ((n & 4) == 0) y[m * a.ldy + (n >> 3) * 4 + (n & 3)] = Act::store(swiglu<Act>(v, up));
+      } else {
+        y[m * a.ldy + n] = Act::store(v);
+      }
     }
   }
 }
@@ -1042,6 +1055,7 @@ hipError_t launch_oneshot(const LinearArgs& a, int c, int nw, hipStream_t stream
 // M <= 4, 2/4-bit codes, group 128: the one-shot kernel.
 bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.fmt != kNibble || a.M > 4 || a.group != 128 || a.K % 128 != 0 || a.G % 4 != 0) return false;
+  if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
   if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
@@ -1068,7 +1082,7 @@ bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
 
 // Small M: the streaming kernel, when the step geometry fits and x[M, K] fits in LDS.
 bool try_stream(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
-  if (a.M > 16) return false;
+  if (a.M > 16 || a.epilogue != kEpiNone) return false;
   const int step_k = a.fmt == kNibble ? 128 : 64;
   if (a.group % step_k != 0 || a.K % step_k != 0 || a.ldq % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
@@ -1168,6 +1182,7 @@ MtConfig pick_mt(const LinearArgs& a, int64_t steps) {
 // M <= 64, 2/4-bit codes, groups of a multiple of 128 codes: the multi-tile kernel.
 bool try_mt(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.fmt != kNibble || a.M < 1 || a.M > 64) return false;
+  if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
   if (a.group % 128 != 0 || a.K % 128 != 0 || a.G % 4 != 0) return false;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
@@ -1191,6 +1206,7 @@ bool try_mt(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
 hipError_t launch_skinny(const LinearArgs& a, hipStream_t stream, bool* fits) {
   *fits = false;
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
+  if (a.epilogue != kEpiNone) return hipSuccess;
   if (a.M < 1 || a.M > 64) return hipSuccess;
   // Bytes per lane per chunk: the widest that a group and the row alignment allow.
   int cb = 0;

@@ -342,6 +342,28 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
           v[r] = t[r];
           if (bias && n + r < a.N) v[r] += Act::load(bias[n + r]);
         }
+        if (a.epilogue == kEpiSwiglu) {
+          // Fused rows 8p .. 8p+3 (gate) are in this lane's half 0, rows 8p+4 .. 8p+7 (up) in
+          // the lane 32 above (N % 8 == 0): output features 4p .. 4p+3.
+          float up[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) up[r] = __shfl_xor(v[r], 32, 64);
+          if (half == 0 && n < a.N) {
+            Raw* dst = y + m * a.ldy + (n >> 1);
+            u32x2 pk;
+            pk.x = uint32_t(Act::store(swiglu<Act>(v[0], up[0]))) | (uint32_t(Act::store(swiglu<Act>(v[1], up[1]))) << 16);
+            pk.y = uint32_t(Act::store(swiglu<Act>(v[2], up[2]))) | (uint32_t(Act::store(swiglu<Act>(v[3], up[3]))) << 16);
+            if ((a.ldy % 4 == 0) && (reinterpret_cast<uintptr_t>(a.y) % 8 == 0)) {
+              *reinterpret_cast<u32x2*>(dst) = pk;
+            } else {
+              dst[0] = Raw(pk.x & 0xFFFFu);
+              dst[1] = Raw(pk.x >> 16);
+              dst[2] = Raw(pk.y & 0xFFFFu);
+              dst[3] = Raw(pk.y >> 16);
+            }
+          }
+          continue;
+        }
         Raw* dst = y + m * a.ldy + n;
         if (vec && n + 3 < a.N) {
           u32x2 pk;
@@ -363,6 +385,35 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
 template <class Act>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(const LinearArgs a, const float* partials, int splits) {
   using Raw = typename Act::raw;
+  if (a.epilogue == kEpiSwiglu) {
+    // One thread per output feature group of four: fused columns 8p .. 8p+7 (N % 8 == 0).
+    const int64_t p8 = a.N / 8;
+    const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= a.M * p8) return;
+    const int64_t m = e / p8;
+    const int64_t n = (e - m * p8) * 8;
+    const size_t plane = size_t(a.M) * a.N;
+    const float* p = partials + size_t(m) * a.N + n;
+    float g[4], u[4];
+    for (int s = 0; s < splits; ++s) {
+      const f32x4 tg = *reinterpret_cast<const f32x4*>(p + s * plane);
+      const f32x4 tu = *reinterpret_cast<const f32x4*>(p + s * plane + 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        g[r] = s == 0 ? tg[r] : g[r] + tg[r];
+        u[r] = s == 0 ? tu[r] : u[r] + tu[r];
+      }
+    }
+    const Raw* bias = static_cast<const Raw*>(a.bias);
+    Raw* y = static_cast<Raw*>(a.y) + m * a.ldy + n / 2;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float gb = bias ? g[r] + Act::load(bias[n + r]) : g[r];
+      const float ub = bias ? u[r] + Act::load(bias[n + 4 + r]) : u[r];
+      y[r] = Act::store(swiglu<Act>(gb, ub));
+    }
+    return;
+  }
   const int64_t n4 = (a.N + 3) / 4;
   const int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (e >= a.M * n4) return;
@@ -460,7 +511,7 @@ void launch_tt(const LinearArgs& a, const GemmPlan& plan, int splits, hipStream_
     else
       hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, kCanSplit>), grid, block, 0, stream, a, tm, tn,
                          magic, splits, partials);
-    const int64_t threads = a.M * ((a.N + 3) / 4);
+    const int64_t threads = a.epilogue == kEpiSwiglu ? a.M * (a.N / 8) : a.M * ((a.N + 3) / 4);
     hipLaunchKernelGGL(splitk_reduce_kernel<Act>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
                        a, partials, splits);
   } else {
@@ -496,6 +547,7 @@ hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fit
   if (a.ldx % 8 != 0 || reinterpret_cast<uintptr_t>(a.x) % 16 != 0) return hipSuccess;
   if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return hipSuccess;
   if (a.M * a.ldx * 2 >= (int64_t(1) << 31)) return hipSuccess;
+  if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return hipSuccess;
   const GemmPlan plan = plan_gemm(a.M, a.N, a.K, a.group);
   if (plan.tt == 0) return hipSuccess;
   // Without a large enough workspace the plan runs unsplit (same tiles, one workgroup per tile).

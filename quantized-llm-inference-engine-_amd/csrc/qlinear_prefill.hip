@@ -267,7 +267,7 @@ hipError_t launch_fmt(const LinearArgs& a, uint32_t magic, hipStream_t stream) {
 hipError_t launch_linear_prefill(const LinearArgs& a, hipStream_t stream, bool* fits) {
   *fits = false;
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
-  if (a.M < 1) return hipSuccess;
+  if (a.M < 1 || a.epilogue != kEpiNone) return hipSuccess;
   const int piece_k = a.fmt == kNibble ? 32 : 16;
   if (a.K % kBK != 0 || a.K >= 65536 || a.group % piece_k != 0) return hipSuccess;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return hipSuccess;

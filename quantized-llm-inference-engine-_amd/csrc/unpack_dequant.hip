@@ -124,4 +124,36 @@ hipError_t launch_dequant(const LinearArgs& a, void* out, int out_dtype, hipStre
   return hipGetLastError();
 }
 
+namespace {
+template <class Act>
+__global__ void __launch_bounds__(256) swiglu_combine_kernel(const typename Act::raw* t, int64_t ldt,
+                                                             typename Act::raw* y, int64_t ldy, int64_t M,
+                                                             int64_t I) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= M * I) return;
+  const int64_t m = i / I;
+  const int64_t f = i - m * I;
+  const int64_t col = (f >> 2) * 8 + (f & 3);  // gate; the matching up column is col + 4
+  y[m * ldy + f] = Act::store(swiglu<Act>(Act::load(t[m * ldt + col]), Act::load(t[m * ldt + col + 4])));
+}
+}  // namespace
+
+hipError_t launch_swiglu_combine(const void* t, int64_t ldt, void* y, int64_t ldy, int64_t M, int64_t N,
+                                 int act, hipStream_t stream) {
+  const int64_t I = N / 2;
+  const int64_t total = M * I;
+  if (total == 0) return hipSuccess;
+  const dim3 grid(unsigned((total + 255) / 256)), block(256);
+  if (act == kDtBf16)
+    hipLaunchKernelGGL(swiglu_combine_kernel<ActBf16>, grid, block, 0, stream,
+                       static_cast<const uint16_t*>(t), ldt, static_cast<uint16_t*>(y), ldy, M, I);
+  else if (act == kDtF16)
+    hipLaunchKernelGGL(swiglu_combine_kernel<ActF16>, grid, block, 0, stream,
+                       static_cast<const uint16_t*>(t), ldt, static_cast<uint16_t*>(y), ldy, M, I);
+  else
+    hipLaunchKernelGGL(swiglu_combine_kernel<ActF32>, grid, block, 0, stream, static_cast<const float*>(t),
+                       ldt, static_cast<float*>(y), ldy, M, I);
+  return hipGetLastError();
+}
+
 }  // namespace llmopt

@@ -51,6 +51,12 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _i64, _p, _p, _p, _int, _i64, _i64, _int, _int, _int, _int, _p],
     ),
     "llmopt_q_linear_workspace": (_size, [_i64, _i64, _i64, _int, _int]),
+    "llmopt_q_linear_swiglu_workspace": (_size, [_i64, _i64, _i64, _int, _int]),
+    "llmopt_q_linear_swiglu": (
+        _int,
+        [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _int, _int, _int, _int, _int,
+         _p, _size, _p],
+    ),
     "llmopt_q_linear": (
         _int,
         [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _int, _int, _int, _int, _int,

@@ -18,7 +18,7 @@ import torch
 
 from llmopt.kernels._lib import ALGO_AUTO, DTYPE_CODES, call, load_library
 
-__all__ = ["dequantize", "quant_linear", "unpack_nibbles"]
+__all__ = ["dequantize", "quant_linear", "quant_linear_swiglu", "unpack_nibbles"]
 
 
 def _stream_handle(device: torch.device) -> int:
@@ -208,3 +208,72 @@ def quant_linear(
             "llmopt_q_linear",
         )
     return y.reshape(*lead_shape, rows)
+
+
+ERR_WORKSPACE = -4
+
+
+def quant_linear_swiglu(
+    x: torch.Tensor,
+    qt,  # noqa: ANN001 - QuantizedTensor with gate and up rows interleaved in blocks of four
+    bias: torch.Tensor | None,
+    compute_dtype: torch.dtype,
+) -> torch.Tensor:
+    """``silu(x @ gate^T) * (x @ up^T)`` from one fused weight, without the [M, 2I] product.
+
+    ``qt`` holds ``2I`` rows: fused row ``8p + r`` is gate row ``4p + r`` and ``8p + 4 + r`` is
+    up row ``4p + r`` (``r < 4``); ``bias`` (if any) follows the same order. Returns ``[..., I]``.
+    """
+    if x.dtype != compute_dtype:
+        raise RuntimeError(
+            f"expected m1 and m2 to have the same dtype, but got: {x.dtype} != {compute_dtype}"
+        )
+    if compute_dtype not in DTYPE_CODES:
+        raise TypeError(f"compute_dtype {compute_dtype} is not supported by the HIP kernels")
+    if bias is not None and bias.dtype != compute_dtype:
+        raise RuntimeError(
+            f"self and mat2 must have the same dtype, but got {bias.dtype} and {compute_dtype}"
+        )
+    _same_device(x, qt.qweight, qt.scales, bias)
+    qweight, ldq, scales, zeros, rows, cols, group, signed = _weight_args(qt, x.device)
+    if rows % 8:
+        raise ValueError(f"fused gate/up weight needs a multiple of 8 rows, got {rows}")
+    if x.dim() == 0 or x.shape[-1] != cols:
+        lead = x.numel() // x.shape[-1] if x.dim() and x.shape[-1] else 0
+        raise RuntimeError(
+            f"mat1 and mat2 shapes cannot be multiplied ({lead}x{x.shape[-1] if x.dim() else 0} "
+            f"and {cols}x{rows})"
+        )
+    lead_shape = x.shape[:-1]
+    x2 = x.reshape(-1, cols)
+    if cols and x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    ldx = x2.stride(0) if m > 1 else cols
+    out = rows // 2
+    y = torch.empty(m, out, dtype=compute_dtype, device=x.device)
+    if m and rows:
+        if bias is not None:
+            bias = bias.contiguous()
+        lib = load_library()
+        ws_bytes = int(lib.llmopt_q_linear_swiglu_workspace(m, rows, cols, int(qt.bits), group))
+        for _attempt in range(2):
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+            rc = lib.llmopt_q_linear_swiglu(
+                x2.data_ptr(), m, cols, max(ldx, cols), qweight.data_ptr(), ldq, scales.data_ptr(),
+                zeros.data_ptr() if zeros is not None else None,
+                bias.data_ptr() if bias is not None else None,
+                y.data_ptr(), rows, out, DTYPE_CODES[compute_dtype], int(qt.bits), group,
+                int(bool(qt.symmetric)), int(signed), ws.data_ptr() if ws is not None else None,
+                ws_bytes, _stream_handle(x.device),
+            )
+            if rc != ERR_WORKSPACE:
+                break
+            # A kernel without the fused activation ran into a short workspace (an unusual
+            # alignment): give it room for the full product and try once more.
+            ws_bytes = (m * rows * 4 + 255) // 256 * 256 + int(
+                lib.llmopt_q_linear_workspace(m, rows, cols, int(qt.bits), group)
+            )
+        call(rc, "llmopt_q_linear_swiglu")
+    return y.reshape(*lead_shape, out)
+

@@ -1,6 +1,7 @@
 """Weight quantization: RTN, GPTQ, packed storage and ``QuantLinear``.
 
-Exports the same names as the reference's ``src/llmopt/quantization/__init__.py:30-49``.
+Exports the same names as the reference's ``src/llmopt/quantization/__init__.py:30-49``, plus
+the fused projections of :mod:`llmopt.quantization.fused` (which have no counterpart there).
 """
 
 from __future__ import annotations
@@ -11,6 +12,7 @@ from llmopt.quantization.calibration import (
     HessianCollector,
     apply_quantization,
 )
+from llmopt.quantization.fused import FusedQuantLinear, QuantSwiGLU, concat_rows, interleave_gate_up
 from llmopt.quantization.quant_linear import (
     QuantLinear,
     QuantLinearConfig,
@@ -33,17 +35,21 @@ from llmopt.quantization.quantizers import (
 __all__ = [
     "CalibrationHarness",
     "CalibrationResult",
+    "FusedQuantLinear",
     "GPTQQuantizer",
     "HessianCollector",
     "QuantLinear",
     "QuantLinearConfig",
+    "QuantSwiGLU",
     "QuantizedTensor",
     "Quantizer",
     "RoundToNearestQuantizer",
     "apply_quantization",
     "build_quantizer",
     "choose_qparams",
+    "concat_rows",
     "dequantize",
+    "interleave_gate_up",
     "pack_int4",
     "quantize_model_",
     "quantize_to_codes",

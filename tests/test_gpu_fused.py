@@ -1,0 +1,147 @@
+"""Parity of the fused projections on the GPU, through the C ABI.
+
+* ``llmopt_q_linear_swiglu`` (gate and up rows interleaved in blocks of four) against the
+  reference's sequence on the CPU: oracle dequantization cast to the compute dtype,
+  ``F.linear`` for gate and for up, then ``silu(gate) * up`` in the compute dtype
+  (``src/llmopt/model/layers.py:44``): max|y - y_ref| / max|y_ref| <= 2e-2 (bf16/fp16): the
+  output is the product of two GEMM outputs, gate and up, each held to the 1e-2 bound of a
+  single quantized linear, so the product's bound is their sum (seen: 1.2e-2). The
+  shapes cover the kernels with the activation in their epilogue (one-shot and multi-tile
+  decode, the prefill GEMM unsplit and split) and the workspace path for the others (8-bit
+  codes, groups of 64).
+* ``FusedQuantLinear``: each part of one launch equals the separate ``QuantLinear``.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from llmopt.kernels import ops
+from llmopt.quantization import (
+    FusedQuantLinear,
+    QuantLinear,
+    QuantSwiGLU,
+    QuantizedTensor,
+    RoundToNearestQuantizer,
+    dequantize,
+    interleave_gate_up,
+)
+from oracle import quant_oracle as qo
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+NP_NAMES = {torch.float16: "float16", torch.bfloat16: "bfloat16"}
+SWIGLU_TOL = 2e-2
+
+
+def _host_qt(rows, cols, bits, group, symmetric, seed):
+    gen = torch.Generator().manual_seed(seed)
+    w = torch.randn(rows, cols, generator=gen) * 0.02
+    return RoundToNearestQuantizer(bits, group, symmetric).quantize(w)
+
+
+def _to_device(qt):
+    return QuantizedTensor(qt.qweight.to(DEV), qt.scales.to(DEV), qt.zeros.to(DEV), qt.bits,
+                           qt.group_size, qt.symmetric, qt.shape)
+
+
+def _oracle_dense(qt):
+    return qo.dequantize(qt.qweight.numpy(), qt.scales.numpy(), qt.zeros.numpy(), qt.bits,
+                         qt.group_size, qt.symmetric, qt.shape)
+
+
+def _rel_err(y, ref):
+    y, ref = y.detach().float().cpu(), ref.detach().float().cpu()
+    d = float(ref.abs().max())
+    return float((y - ref).abs().max()) / (d if d > 0 else 1.0)
+
+
+def _ref_linear(x, dense32, dtype, bias=None):
+    w = torch.from_numpy(qo.round_to_dtype(dense32, NP_NAMES[dtype])).to(dtype)
+    return qo.reference_linear(x, w, bias)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bits,symmetric,group", [(4, False, 128), (4, True, 128), (2, False, 256),
+                                                   (4, False, 64), (8, False, 128)])
+@pytest.mark.parametrize("inter,k", [(64, 1024), (96, 512)])
+@pytest.mark.parametrize("m", [1, 3, 8, 33, 64, 200, 300])
+def test_swiglu_small_shapes(dtype, bits, symmetric, group, inter, k, m):
+    gate = _host_qt(inter, k, bits, group, symmetric, seed=inter + k + bits)
+    up = _host_qt(inter, k, bits, group, symmetric, seed=inter + k + bits + 1)
+    fused = _to_device(interleave_gate_up(gate, up))
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(dtype)
+    y = ops.quant_linear_swiglu(x.to(DEV), fused, None, dtype)
+    g = _ref_linear(x, _oracle_dense(gate), dtype)
+    u = _ref_linear(x, _oracle_dense(up), dtype)
+    ref = torch.nn.functional.silu(g) * u
+    assert y.shape == (m, inter) and y.dtype == dtype
+    assert _rel_err(y, ref) <= SWIGLU_TOL, (dtype, bits, symmetric, group, inter, k, m)
+
+
+def test_swiglu_bias_and_leading_dims():
+    dtype = torch.bfloat16
+    gen = torch.Generator().manual_seed(7)
+    lin_g, lin_u = nn.Linear(512, 64), nn.Linear(512, 64)
+    with torch.no_grad():
+        for lin in (lin_g, lin_u):
+            lin.weight.copy_(torch.randn(64, 512, generator=gen) * 0.02)
+            lin.bias.copy_(torch.randn(64, generator=gen) * 0.1)
+    qg = RoundToNearestQuantizer(4, 128, False).quantize(lin_g.weight.detach())
+    qu = RoundToNearestQuantizer(4, 128, False).quantize(lin_u.weight.detach())
+    gate = QuantLinear.from_float(lin_g.to(dtype), qg, compute_dtype=dtype)
+    up = QuantLinear.from_float(lin_u.to(dtype), qu, compute_dtype=dtype)
+    fused_host = QuantSwiGLU(gate, up)
+    fused_dev = QuantSwiGLU(gate, up).to(DEV)
+    for m in (1, 40, 300):
+        x = torch.randn(2, m, 512, generator=gen).to(dtype)
+        ref = fused_host(x)
+        y = fused_dev(x.to(DEV))
+        assert y.shape == (2, m, 64)
+        assert _rel_err(y, ref) <= SWIGLU_TOL, m
+
+
+@pytest.mark.parametrize("m", [1, 8, 64, 2048])
+def test_swiglu_llama_gate_up(m):
+    dtype = torch.bfloat16
+    inter, k = 14336, 4096
+    gate = _to_device(_host_qt(inter, k, 4, 128, False, seed=1))
+    up = _to_device(_host_qt(inter, k, 4, 128, False, seed=2))
+    fused = interleave_gate_up(gate, up)
+    x = torch.randn(m, k, device=DEV).to(dtype)
+    y = ops.quant_linear_swiglu(x, fused, None, dtype)
+    # GPU fp32 reference over the bit-exact dequantized weights (dequantize is checked
+    # bit-exact against the oracle elsewhere), rounded like the reference's sequence.
+    g = (x.float() @ dequantize(gate, dtype).float().t().contiguous()).to(dtype)
+    u = (x.float() @ dequantize(up, dtype).float().t().contiguous()).to(dtype)
+    ref = torch.nn.functional.silu(g.float()).to(dtype).float() * u.float()
+    assert _rel_err(y, ref) <= SWIGLU_TOL
+
+
+@pytest.mark.parametrize("m", [1, 5, 64, 300])
+def test_fused_qkv_matches_separate(m):
+    dtype = torch.bfloat16
+    gen = torch.Generator().manual_seed(m)
+    parts = []
+    for i, n in enumerate((128, 32, 32)):
+        lin = nn.Linear(1024, n, bias=False)
+        with torch.no_grad():
+            lin.weight.copy_(torch.randn(n, 1024, generator=gen) * 0.02)
+        qt = RoundToNearestQuantizer(4, 128, False).quantize(lin.weight.detach())
+        parts.append(QuantLinear.from_float(lin.to(dtype), qt, compute_dtype=dtype).to(DEV))
+    fused = FusedQuantLinear(parts)
+    x = torch.randn(m, 1024, generator=gen).to(dtype).to(DEV)
+    outs = fused(x)
+    for o, p in zip(outs, parts):
+        assert o.shape == (m, p.out_features)
+        assert _rel_err(o, p(x)) <= 1e-2
+
+
+def test_swiglu_rejects_bad_row_count():
+    qt = _to_device(_host_qt(12, 256, 4, 128, False, seed=3))
+    with pytest.raises(ValueError):
+        ops.quant_linear_swiglu(torch.randn(2, 256, device=DEV).to(torch.bfloat16), qt, None, torch.bfloat16)
