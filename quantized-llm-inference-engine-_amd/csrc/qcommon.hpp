@@ -77,12 +77,13 @@ struct ActBf16 {
 // The gated activation of the reference's MLP, silu(gate(x)) * up(x) (layers.py:44), with its
 // roundings: gate and up are linear outputs in the compute dtype, silu runs in fp32 on the
 // rounded gate and is rounded, and the product of the two rounded values is rounded by the
-// caller's store.
+// caller's store. The exponential is the hardware one (a few fp32 ulps), which the rounding
+// to bf16/fp16 that follows hides.
 template <class Act>
 __device__ __forceinline__ float swiglu(float g, float u) {
   const float gr = Act::load(Act::store(g));
   const float ur = Act::load(Act::store(u));
-  const float s = Act::load(Act::store(gr / (1.0f + expf(-gr))));
+  const float s = Act::load(Act::store(gr / (1.0f + __expf(-gr))));
   return s * ur;
 }
 

@@ -101,7 +101,9 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t nib_mask, floa
   return out;
 }
 
-template <class Act, int TT, int GP, bool SPLIT>
+// EPI is the output epilogue (kEpiNone or kEpiSwiglu), a template parameter so that the plain
+// kernel's register allocation is not shaped by the fused activation's extra live values.
+template <class Act, int TT, int GP, bool SPLIT, int EPI>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
     qlinear_gemm_kernel(const LinearArgs a, int tiles_m, int tiles_n, uint32_t group_magic,
                         int splits, float* partials) {
@@ -342,26 +344,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
           v[r] = t[r];
           if (bias && n + r < a.N) v[r] += Act::load(bias[n + r]);
         }
-        if (a.epilogue == kEpiSwiglu) {
-          // Fused rows 8p .. 8p+3 (gate) are in this lane's half 0, rows 8p+4 .. 8p+7 (up) in
-          // the lane 32 above (N % 8 == 0): output features 4p .. 4p+3.
-          float up[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) up[r] = __shfl_xor(v[r], 32, 64);
-          if (half == 0 && n < a.N) {
-            Raw* dst = y + m * a.ldy + (n >> 1);
-            u32x2 pk;
-            pk.x = uint32_t(Act::store(swiglu<Act>(v[0], up[0]))) | (uint32_t(Act::store(swiglu<Act>(v[1], up[1]))) << 16);
-            pk.y = uint32_t(Act::store(swiglu<Act>(v[2], up[2]))) | (uint32_t(Act::store(swiglu<Act>(v[3], up[3]))) << 16);
-            if ((a.ldy % 4 == 0) && (reinterpret_cast<uintptr_t>(a.y) % 8 == 0)) {
-              *reinterpret_cast<u32x2*>(dst) = pk;
-            } else {
-              dst[0] = Raw(pk.x & 0xFFFFu);
-              dst[1] = Raw(pk.x >> 16);
-              dst[2] = Raw(pk.y & 0xFFFFu);
-              dst[3] = Raw(pk.y >> 16);
-            }
-          }
+        if (EPI == kEpiSwiglu) {
+          // Rounded gate / up values go to this wave's LDS tile [token][64 fused rows]; the
+          // activation is applied below.
+          Raw* tile = reinterpret_cast<Raw*>(xbuf(wave)) + (32 * j + frow) * 64 + 32 * i + 8 * q + 4 * half;
+          u32x2 pk;
+          pk.x = uint32_t(Act::store(v[0])) | (uint32_t(Act::store(v[1])) << 16);
+          pk.y = uint32_t(Act::store(v[2])) | (uint32_t(Act::store(v[3])) << 16);
+          *reinterpret_cast<u32x2*>(tile) = pk;
           continue;
         }
         Raw* dst = y + m * a.ldy + n;
@@ -376,6 +366,24 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
             if (n + r < a.N) dst[r] = Act::store(v[r]);
         }
       }
+    }
+  }
+
+  if (EPI == kEpiSwiglu) {
+    // Each wave owns 64 fused rows = 8 gate/up blocks = 32 output features of 32 * TT tokens.
+    // Lanes take consecutive output features of one token, so stores are 64-byte runs.
+    const Raw* tile = reinterpret_cast<const Raw*>(xbuf(wave));
+    const int64_t out0 = (n0 + 64 * wave) / 2;
+    for (int e = lane; e < 32 * TT * 32; e += 64) {
+      const int t = e >> 5;
+      const int o = e & 31;
+      const int64_t m = m0 + t;
+      const int64_t f = out0 + o;
+      if (m >= a.M || 2 * f >= a.N) continue;
+      const int g = (o >> 2) * 8 + (o & 3);
+      const float gv = Act::load(tile[t * 64 + g]);
+      const float uv = Act::load(tile[t * 64 + g + 4]);
+      y[m * a.ldy + f] = Act::store(swiglu<Act>(gv, uv));
     }
   }
 }
@@ -501,26 +509,35 @@ void launch_tt(const LinearArgs& a, const GemmPlan& plan, int splits, hipStream_
   const int ntiles = int(plan.tiles_m * plan.tiles_n);
   const dim3 grid(unsigned(ntiles * splits)), block(kThreads);
   // The split epilogue is a separate instantiation: its extra live values would push the
-  // 256-token tile's main loop into spills.
+  // 256-token tile's main loop into spills. (Split results get the activation, if any, from
+  // the reduction kernel.)
   constexpr bool kCanSplit = TT < 8;
   const int tm = int(plan.tiles_m), tn = int(plan.tiles_n);
+  const bool gp2 = a.group % 128 == 0;
   if (kCanSplit && splits > 1) {
-    if (a.group % 128 == 0)
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, kCanSplit>), grid, block, 0, stream, a, tm, tn,
-                         magic, splits, partials);
+    if (gp2)
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, kCanSplit, kEpiNone>), grid, block, 0, stream, a, tm,
+                         tn, magic, splits, partials);
     else
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, kCanSplit>), grid, block, 0, stream, a, tm, tn,
-                         magic, splits, partials);
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, kCanSplit, kEpiNone>), grid, block, 0, stream, a, tm,
+                         tn, magic, splits, partials);
     const int64_t threads = a.epilogue == kEpiSwiglu ? a.M * (a.N / 8) : a.M * ((a.N + 3) / 4);
     hipLaunchKernelGGL(splitk_reduce_kernel<Act>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
                        a, partials, splits);
-  } else {
-    if (a.group % 128 == 0)
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, false>), grid, block, 0, stream, a, tm, tn, magic, 1,
-                         partials);
+  } else if (a.epilogue == kEpiSwiglu) {
+    if (gp2)
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, false, kEpiSwiglu>), grid, block, 0, stream, a, tm, tn,
+                         magic, 1, partials);
     else
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, false>), grid, block, 0, stream, a, tm, tn, magic, 1,
-                         partials);
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, false, kEpiSwiglu>), grid, block, 0, stream, a, tm, tn,
+                         magic, 1, partials);
+  } else {
+    if (gp2)
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, false, kEpiNone>), grid, block, 0, stream, a, tm, tn,
+                         magic, 1, partials);
+    else
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, false, kEpiNone>), grid, block, 0, stream, a, tm, tn,
+                         magic, 1, partials);
   }
 }
 
