@@ -1,7 +1,8 @@
 """Weight quantization: RTN, GPTQ, packed storage and ``QuantLinear``.
 
 Exports the same names as the reference's ``src/llmopt/quantization/__init__.py:30-49``, plus
-the fused projections of :mod:`llmopt.quantization.fused` (which have no counterpart there).
+the fused projections of :mod:`llmopt.quantization.fused` and the packed checkpoint of
+:mod:`llmopt.quantization.checkpoint` (which have no counterpart there).
 """
 
 from __future__ import annotations
@@ -12,6 +13,7 @@ from llmopt.quantization.calibration import (
     HessianCollector,
     apply_quantization,
 )
+from llmopt.quantization.checkpoint import is_quantized_checkpoint, load_quantized_, save_quantized
 from llmopt.quantization.fused import FusedQuantLinear, QuantSwiGLU, concat_rows, interleave_gate_up
 from llmopt.quantization.quant_linear import (
     QuantLinear,
@@ -50,9 +52,12 @@ __all__ = [
     "concat_rows",
     "dequantize",
     "interleave_gate_up",
+    "is_quantized_checkpoint",
+    "load_quantized_",
     "pack_int4",
     "quantize_model_",
     "quantize_to_codes",
     "replace_linear_modules",
+    "save_quantized",
     "unpack_int4",
 ]
