@@ -204,10 +204,10 @@ int llmopt_q_dequant(const void* qweight, int64_t ldq, const float* scales, cons
 }
 
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
-  // Only the prefill GEMM (M > 64, 2/4-bit codes) splits K; the decode kernels reduce in LDS.
-  if (M <= 64 || N <= 0 || K <= 0 || (bits != 2 && bits != 4)) return 0;
+  // Only the prefill GEMM (M > 64) splits K; the decode kernels reduce in LDS.
+  if (M <= 64 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
   const int64_t g = group_size <= 0 ? K : group_size;
-  return llmopt::gemm_workspace_bytes(M, N, K, g);
+  return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
 }
 
 int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
@@ -227,7 +227,8 @@ size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bit
   // Sizes whose kernels apply the activation themselves (assuming aligned, contiguous tensors).
   if (nibble && M <= 64 && g % 128 == 0 && K % 128 == 0 && (K / g) % 4 == 0 && (M <= 4 || K <= 8192))
     return 0;
-  if (nibble && M > 64 && g % 32 == 0 && K % 64 == 0) return llmopt::gemm_workspace_bytes(M, N, K, g);
+  if (M > 64 && bits >= 1 && bits <= 8 && g % 32 == 0 && K % 64 == 0)
+    return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
   // Otherwise: the full [M, N] output in fp32-sized slots, then the combining kernel.
   return swiglu_temp_bytes(M, N) + llmopt_q_linear_workspace(M, N, K, bits, group_size);
 }

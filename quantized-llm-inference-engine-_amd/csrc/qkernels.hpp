@@ -49,6 +49,6 @@ hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fit
 hipError_t launch_swiglu_combine(const void* t, int64_t ldt, void* y, int64_t ldy, int64_t M, int64_t N,
                                  int act, hipStream_t stream);
 // Workspace the prefill GEMM's split-K plan uses for these sizes (0 when it does not split).
-size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
+size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int fmt);
 
 }  // namespace llmopt

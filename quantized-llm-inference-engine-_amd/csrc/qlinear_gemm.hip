@@ -101,12 +101,28 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t nib_mask, floa
   return out;
 }
 
+// Eight byte codes (two 32-bit words) -> the A fragment of one k-slice. Signed 8-bit codes
+// arrive with their sign bit flipped (q + 128) and the offset folded into z, which is exact.
+template <class Act>
+__device__ __forceinline__ u32x4 dequant8_bytes(uint32_t w0, uint32_t w1, float z, float s) {
+  const uc4 b0 = __builtin_bit_cast(uc4, w0);
+  const uc4 b1 = __builtin_bit_cast(uc4, w1);
+  u32x4 out;
+  out.x = Mfma32x<Act>::pack(dequant_exact(float(b0.x), z, s), dequant_exact(float(b0.y), z, s));
+  out.y = Mfma32x<Act>::pack(dequant_exact(float(b0.z), z, s), dequant_exact(float(b0.w), z, s));
+  out.z = Mfma32x<Act>::pack(dequant_exact(float(b1.x), z, s), dequant_exact(float(b1.y), z, s));
+  out.w = Mfma32x<Act>::pack(dequant_exact(float(b1.z), z, s), dequant_exact(float(b1.w), z, s));
+  return out;
+}
+
 // EPI is the output epilogue (kEpiNone or kEpiSwiglu), a template parameter so that the plain
 // kernel's register allocation is not shaped by the fused activation's extra live values.
-template <class Act, int TT, int GP, bool SPLIT, int EPI>
+// FMT is the code storage: kNibble (two codes per byte, widths 1-7) or kByte (8-bit codes).
+template <class Act, int TT, int GP, bool SPLIT, int EPI, int FMT>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
     qlinear_gemm_kernel(const LinearArgs a, int tiles_m, int tiles_n, uint32_t group_magic,
                         int splits, float* partials) {
+  constexpr int kCB = FMT == kNibble ? 1 : 2;  // 16-byte code loads per tile and stage
   using Raw = typename Act::raw;
   constexpr int kBM = 32 * TT;          // tokens per workgroup
   constexpr int kXStage = kBM * kBK * 2;  // bytes of one activation stage
@@ -152,7 +168,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   for (int i = 0; i < 2; ++i) {
     int64_t n = n0 + 64 * wave + 32 * i + frow;
     n = n < a.N ? n : a.N - 1;  // rows past N repeat row N-1; their outputs are never stored
-    wq_off[i] = uint32_t(n * a.ldq + half * 16);
+    wq_off[i] = uint32_t(n * a.ldq + half * 16 * kCB);
     meta_off[i] = uint32_t(n * a.G * 4);
   }
   const float z_const = a.zero_const;
@@ -167,12 +183,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   // GP stops at 2: the first k-slice of stage kt + 1 is dequantized during stage kt, so a meta
   // slot must be refilled a stage before its first use, which needs at least two slots.
   static_assert(GP == 1 || GP == 2, "metadata period of one or two stages");
-  u32x4 wring[kRing][2];
+  u32x4 wring[kRing][2][kCB];
   float sring[kRing][2], zring[kRing][2];
   auto load_codes = [&](int slot, int kt) {
     const int ktc = kt_base + (kt < ktiles ? kt : ktiles - 1);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) wring[slot][i] = buf_load16(wq, wq_off[i], uint32_t(ktc) * 32);
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int c = 0; c < kCB; ++c) wring[slot][i][c] = buf_load16(wq, wq_off[i] + 16 * c, uint32_t(ktc) * 32 * kCB);
   };
   auto load_meta = [&](int slot, int kt) {
     const int ktc = kt_base + (kt < ktiles ? kt : ktiles - 1);
@@ -210,6 +228,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   };
 
   const uint32_t nib_mask = 0x0F0F0F0Fu | uint32_t(uint64_t(a.ldq) >> 48);
+  const bool flipped = FMT == kByte && a.signed_codes;
+  const uint32_t flip = flipped ? 0x80808080u : 0u;
+  const float z_flip = flipped ? 128.0f : 0.0f;
 
   // ---- prologue: activations of stages 0 and 1 in LDS, stage 2 in registers, codes and
   //      metadata of stages 0 .. 3 in flight, fragments of stage 0, k-slice 0 ready ----
@@ -237,12 +258,19 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
     for (int j = 0; j < TT; ++j)
       bf[j] = *reinterpret_cast<const u32x4*>(buf + swz(32 * j + frow, 4 * half + ks));
   };
+  auto word = [](const u32x4& q, int w) { return w == 0 ? q.x : w == 1 ? q.y : w == 2 ? q.z : q.w; };
   auto dequant_a = [&](int u, int ks, u32x4* af) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const u32x4 q = wring[u][i];
-      const uint32_t w = ks == 0 ? q.x : ks == 1 ? q.y : ks == 2 ? q.z : q.w;
-      af[i] = dequant8<Act>(w, nib_mask, asym ? zring[u / GP][i] : z_const, sring[u / GP][i]);
+      const float z = (asym ? zring[u / GP][i] : z_const) + z_flip;
+      if constexpr (FMT == kNibble) {
+        af[i] = dequant8<Act>(word(wring[u][i][0], ks), nib_mask, z, sring[u / GP][i]);
+      } else {
+        // Codes 8ks .. 8ks + 7 of the lane's 32: words 2ks and 2ks + 1 of its 32 bytes.
+        const u32x4 q = wring[u][i][ks >> 1];
+        af[i] = dequant8_bytes<Act>(word(q, (2 * ks) & 3) ^ flip, word(q, (2 * ks + 1) & 3) ^ flip, z,
+                                    sring[u / GP][i]);
+      }
     }
   };
   u32x4 af[2], bf[TT];
@@ -469,7 +497,7 @@ struct GemmPlan {
   size_t workspace() const { return splits > 1 ? partial_bytes : 0; }
 };
 
-GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t group) {
+GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t group, int fmt) {
   GemmPlan best;
   if (M < 1 || N < 1 || K % kBK != 0 || group % 32 != 0) return best;
   const int gp = group % 128 == 0 ? 2 : 1;
@@ -477,6 +505,7 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t group) {
   const double stage_us[9] = {0, 0, 0.95, 0, 1.35, 0, 0, 0, 2.1};
   double best_t = 1e30;
   for (int tt : {8, 4, 2}) {
+    if (fmt == kByte && tt == 8) continue;  // the byte-code ring does not fit the 256-token tile
     const int64_t tm = (M + 32 * tt - 1) / (32 * tt);
     const int64_t tn = (N + kBN - 1) / kBN;
     if (tm * tn > 0x7FFFFFFF / 8) continue;
@@ -503,7 +532,7 @@ GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t group) {
   return best;
 }
 
-template <class Act, int TT>
+template <class Act, int TT, int FMT>
 void launch_tt(const LinearArgs& a, const GemmPlan& plan, int splits, hipStream_t stream, uint32_t magic) {
   float* partials = splits > 1 ? static_cast<float*>(a.workspace) : nullptr;
   const int ntiles = int(plan.tiles_m * plan.tiles_n);
@@ -516,48 +545,53 @@ void launch_tt(const LinearArgs& a, const GemmPlan& plan, int splits, hipStream_
   const bool gp2 = a.group % 128 == 0;
   if (kCanSplit && splits > 1) {
     if (gp2)
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, kCanSplit, kEpiNone>), grid, block, 0, stream, a, tm,
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, kCanSplit, kEpiNone, FMT>), grid, block, 0, stream, a, tm,
                          tn, magic, splits, partials);
     else
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, kCanSplit, kEpiNone>), grid, block, 0, stream, a, tm,
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, kCanSplit, kEpiNone, FMT>), grid, block, 0, stream, a, tm,
                          tn, magic, splits, partials);
     const int64_t threads = a.epilogue == kEpiSwiglu ? a.M * (a.N / 8) : a.M * ((a.N + 3) / 4);
     hipLaunchKernelGGL(splitk_reduce_kernel<Act>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
                        a, partials, splits);
   } else if (a.epilogue == kEpiSwiglu) {
     if (gp2)
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, false, kEpiSwiglu>), grid, block, 0, stream, a, tm, tn,
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, false, kEpiSwiglu, FMT>), grid, block, 0, stream, a, tm, tn,
                          magic, 1, partials);
     else
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, false, kEpiSwiglu>), grid, block, 0, stream, a, tm, tn,
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, false, kEpiSwiglu, FMT>), grid, block, 0, stream, a, tm, tn,
                          magic, 1, partials);
   } else {
     if (gp2)
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, false, kEpiNone>), grid, block, 0, stream, a, tm, tn,
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 2, false, kEpiNone, FMT>), grid, block, 0, stream, a, tm, tn,
                          magic, 1, partials);
     else
-      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, false, kEpiNone>), grid, block, 0, stream, a, tm, tn,
+      hipLaunchKernelGGL((qlinear_gemm_kernel<Act, TT, 1, false, kEpiNone, FMT>), grid, block, 0, stream, a, tm, tn,
                          magic, 1, partials);
   }
 }
 
 template <class Act>
 void launch_act(const LinearArgs& a, const GemmPlan& plan, int splits, hipStream_t stream, uint32_t magic) {
-  if (plan.tt == 8) launch_tt<Act, 8>(a, plan, splits, stream, magic);
-  else if (plan.tt == 4) launch_tt<Act, 4>(a, plan, splits, stream, magic);
-  else launch_tt<Act, 2>(a, plan, splits, stream, magic);
+  if (a.fmt == kByte) {  // byte codes: two code loads per tile and stage; tiles of up to 128 tokens
+    if (plan.tt == 4) launch_tt<Act, 4, kByte>(a, plan, splits, stream, magic);
+    else launch_tt<Act, 2, kByte>(a, plan, splits, stream, magic);
+    return;
+  }
+  if (plan.tt == 8) launch_tt<Act, 8, kNibble>(a, plan, splits, stream, magic);
+  else if (plan.tt == 4) launch_tt<Act, 4, kNibble>(a, plan, splits, stream, magic);
+  else launch_tt<Act, 2, kNibble>(a, plan, splits, stream, magic);
 }
 
 }  // namespace
 
-size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
-  return plan_gemm(M, N, K, group).workspace();
+size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int fmt) {
+  return plan_gemm(M, N, K, group, fmt).workspace();
 }
 
 hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fits) {
   *fits = false;
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
-  if (a.fmt != kNibble || a.M < 1) return hipSuccess;
+  if (a.M < 1) return hipSuccess;
   // A lane's 32 codes of a stage lie in one group; 16-byte aligned rows and activations.
   if (a.K % kBK != 0 || a.K / kBK >= 65536 || a.group % 32 != 0) return hipSuccess;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return hipSuccess;
@@ -565,7 +599,7 @@ hipError_t launch_linear_gemm(const LinearArgs& a, hipStream_t stream, bool* fit
   if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return hipSuccess;
   if (a.M * a.ldx * 2 >= (int64_t(1) << 31)) return hipSuccess;
   if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return hipSuccess;
-  const GemmPlan plan = plan_gemm(a.M, a.N, a.K, a.group);
+  const GemmPlan plan = plan_gemm(a.M, a.N, a.K, a.group, a.fmt);
   if (plan.tt == 0) return hipSuccess;
   // Without a large enough workspace the plan runs unsplit (same tiles, one workgroup per tile).
   int splits = plan.splits;
