@@ -14,18 +14,24 @@ value          algorithmic bytes of all timed steps / timed seconds, where one c
                N*K/2 (codes) + 4*N*G*2 (scales, zeros; G = K/128) + 2*M*K + 2*M*N bytes
 roofline       the dominant kernel (gate_up): its algorithmic bytes / its mean time per launch,
                from HIP events around replays of a graph of back-to-back launches (rotating
-               over the copies) on the replay stream -- so it includes the inter-kernel gap;
+               over >= 512 MiB of gate_up copies) on the replay stream -- so it includes the
+               inter-kernel gap;
                `traffic` = HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (each
                scaled by what it reads for a plain copy of known size), when recorded
 prefill        gate_up at M = 8192 through the MFMA prefill kernel, TFLOP/s vs dense bf16 peak
+dense_comparator  (in roofline and prefill) torch's dense bf16 F.linear on the dequantized
+               weight at the same shape: hipBLASLt's figure for the unquantized layer
 cpu_baseline   the reference's host sequence (dequantize once, cache the dense bf16 weight,
                F.linear) on this host's cores, for a bounded number of the same decode steps
+
+Every single-projection timing (roofline, prefill, --sweep, --bits-sweep) rotates over at least
+512 MiB of that projection's own weight copies.
 
 Modes: default prints the JSON line. `--pmc-workload` runs only the dominant kernel and a
 256 MiB copy (for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`); `--traffic-from DIR`
 turns two such rocprofv3 CSV outputs into profiles/traffic_decode_gate_up_m1.json.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--bits-sweep] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -68,6 +74,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--m", type=int, default=1, help="tokens per decode step")
     p.add_argument("--kernel-launches", type=int, default=60, help="timed launches of the dominant kernel")
     p.add_argument("--sweep", action="store_true", help="also time every projection at M in {1..8192}")
+    p.add_argument("--bits-sweep", action="store_true",
+                   help="also time the down projection at 8/4/2 bits, M in {1, 32, 2048}")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -98,6 +106,24 @@ def build_layers(torch, count: int, m: int):
         layers.append(layer)
     xs = {name: torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16) for name, _, k in PROJECTIONS}
     return base, layers, xs
+
+
+def build_rotations(layers, min_bytes: int = MIN_ROTATION_BYTES):
+    """Per projection, distinct weight copies totalling at least `min_bytes`: the layer copies,
+    plus clones of them. Timing one projection alone over fewer bytes than the 256 MB Infinity
+    Cache would let repeats hit that cache."""
+    from llmopt.quantization import QuantizedTensor
+
+    rot = {}
+    for name, n, k in PROJECTIONS:
+        copies = [layer[name] for layer in layers]
+        need = max(2, -(-min_bytes // algorithmic_bytes(0, n, k)))
+        while len(copies) < need:
+            qt = copies[len(copies) % len(layers)]
+            copies.append(QuantizedTensor(qt.qweight.clone(), qt.scales.clone(), qt.zeros.clone(), qt.bits,
+                                          qt.group_size, qt.symmetric, qt.shape))
+        rot[name] = copies
+    return rot
 
 
 def kernel_launch_times(torch, launch, count: int, replays: int = 7) -> list[float]:
@@ -157,10 +183,12 @@ def main() -> int:
     def flush():
         flush_dst.copy_(flush_src)
 
+    rotations = build_rotations(layers)
     name, n, k = PROJECTIONS[2]  # gate_up: the dominant kernel
+    gate_up_copies = rotations[name]
 
     def launch_gate_up(i):
-        ops.quant_linear(xs[name], layers[i % copies][name], None, bf16)
+        ops.quant_linear(xs[name], gate_up_copies[i % len(gate_up_copies)], None, bf16)
 
     if args.pmc_workload:
         for i in range(3):
@@ -213,7 +241,7 @@ def main() -> int:
     print(f"# timed {args.steps} steps: {ms_per_step * 1e3:.2f} us/step, {value:.0f} GB/s",
           file=sys.stderr, flush=True)
 
-    times = kernel_launch_times(torch, launch_gate_up, 4 * copies)
+    times = kernel_launch_times(torch, launch_gate_up, 3 * len(gate_up_copies))
     kernel_us = statistics.mean(times)
     kernel_bytes = algorithmic_bytes(args.m, n, k)
     achieved = kernel_bytes / (kernel_us * 1e-6) / 1e9
@@ -228,6 +256,8 @@ def main() -> int:
         "algorithmic_bytes": kernel_bytes,
         "mean_launch_us": round(kernel_us, 3),
         "median_launch_us": round(statistics.median(times), 3),
+        "weight_copies": len(gate_up_copies),
+        "dense_comparator": dense_comparator(torch, base[name], args.m),
     }
     print(f"# gate_up kernel: mean {kernel_us:.2f} us, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
 
@@ -256,10 +286,13 @@ def main() -> int:
         },
         "roofline": roofline,
     }
+    result["dequant"] = dequant_rate(torch, ops, rotations)
     if not args.no_prefill:
-        result["prefill"] = prefill(torch, ops, layers, copies)
+        result["prefill"] = prefill(torch, ops, rotations)
     if args.sweep:
-        result["sweep"] = sweep(torch, ops, layers, copies)
+        result["sweep"] = sweep(torch, ops, rotations)
+    if args.bits_sweep:
+        result["bits_sweep"] = bits_sweep(torch, ops)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, base, args.m, args.cpu_seconds)
     print(json.dumps(result), flush=True)
@@ -276,34 +309,113 @@ def _measured_traffic(m: int):
         return None
 
 
-def prefill(torch, ops, layers, copies):
+def prefill(torch, ops, rotations):
     """gate_up at M = 8192 (prefill kernel), per-launch time of back-to-back launches."""
     name, n, k = PROJECTIONS[2]
     m = 8192
+    qts = rotations[name]
     x = torch.randn(m, k, device="cuda:0").to(torch.bfloat16)
-    ops.quant_linear(x, layers[0][name], None, torch.bfloat16)
+    ops.quant_linear(x, qts[0], None, torch.bfloat16)
     times = kernel_launch_times(
-        torch, lambda i: ops.quant_linear(x, layers[i % copies][name], None, torch.bfloat16), copies, 3
+        torch, lambda i: ops.quant_linear(x, qts[i % len(qts)], None, torch.bfloat16), len(qts), 3
     )
     us = statistics.mean(times)
     tflops = 2 * m * n * k / (us * 1e-6) / 1e12
     print(f"# prefill gate_up M={m}: {us:.1f} us, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    dense = dense_comparator(torch, qts[0], m)
     return {"kernel": f"quantized-linear prefill, gate_up M={m} (K 4096, N 28672)", "mean_launch_us": round(us, 2),
             "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "bound": "mfma"}
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "bound": "mfma", "dense_comparator": dense}
 
 
-def sweep(torch, ops, layers, copies):
-    """Per-projection kernel times for decode and prefill batch sizes."""
+def dequant_rate(torch, ops, rotations):
+    """The device dequantize (QuantizedTensor -> dense bf16, bit-exact with the reference) of
+    gate_up: packed codes, scales and zeros read once, the dense weight written once."""
+    name, n, k = PROJECTIONS[2]
+    qts = rotations[name]
+    count = min(len(qts), 8)
+    times = kernel_launch_times(torch, lambda i: ops.dequantize(qts[i % count], torch.bfloat16), count, 3)
+    us = statistics.median(times)
+    moved = algorithmic_bytes(0, n, k) + 2 * n * k
+    gbs = moved / (us * 1e-6) / 1e9
+    print(f"# dequantize gate_up -> bf16: {us:.1f} us, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    return {"kernel": f"dequantize gate_up (N {n}, K {k}) W4 g128 -> bf16", "us": round(us, 2),
+            "bytes": moved, "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def dense_comparator(torch, qt, m: int):
+    """torch's dense bf16 F.linear (hipBLASLt) on the dequantized weight at the same shape: a
+    comparator, not the reference. Rotates over enough weight copies to exceed the 256 MB
+    Infinity Cache (a dense bf16 weight is four times the packed bytes)."""
+    from llmopt.quantization import dequantize
+
+    n, k = qt.shape
+    w = dequantize(qt, torch.bfloat16)
+    copies = max(2, -(-MIN_ROTATION_BYTES // (2 * n * k)))
+    ws = [w] + [w.clone() for _ in range(copies - 1)]
+    x = torch.randn(m, k, device="cuda:0").to(torch.bfloat16)
+    f = torch.nn.functional.linear
+    times = kernel_launch_times(torch, lambda i: f(x, ws[i % copies]), 2 * copies if m <= 64 else copies, 3)
+    us = statistics.median(times)
+    dense_bytes = 2 * n * k + 2 * m * k + 2 * m * n
+    out = {"op": f"F.linear bf16 [{m}, {k}] x [{n}, {k}]^T", "us": round(us, 2),
+           "GB/s": round(dense_bytes / (us * 1e-6) / 1e9, 1),
+           "TFLOP/s": round(2 * m * n * k / (us * 1e-6) / 1e12, 1), "weight_copies": copies}
+    print(f"# dense comparator M={m}: {us:.1f} us, {out['GB/s']:.0f} GB/s, {out['TFLOP/s']:.1f} TFLOP/s",
+          file=sys.stderr, flush=True)
+    del ws, w
+    return out
+
+
+def bits_sweep(torch, ops):
+    """The bit-width sweep on the down projection (K 14336, N 4096): asymmetric RTN, group 128,
+    8-bit (one code per byte), 4-bit and 2-bit (two codes per byte), M in {1, 32, 2048}.
+    A GPTQ-quantized 4-bit weight has the 4-bit RTN layout, so it runs the same kernels."""
+    from llmopt.quantization import QuantizedTensor, RoundToNearestQuantizer
+
+    name, n, k = PROJECTIONS[3]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(4)
+    rows = []
+    for bits in (8, 4, 2):
+        w = torch.randn(n, k, generator=gen, device=dev) * 0.02
+        qt = RoundToNearestQuantizer(bits, GROUP, symmetric=False).quantize(w)
+        del w
+        copies = max(2, -(-MIN_ROTATION_BYTES // qt.qweight.numel()))
+        qts = [QuantizedTensor(qt.qweight.clone(), qt.scales.clone(), qt.zeros.clone(), bits, GROUP, False, qt.shape)
+               for _ in range(copies)]
+        for m in (1, 32, 2048):
+            x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
+            ops.quant_linear(x, qts[0], None, torch.bfloat16)
+            times = kernel_launch_times(
+                torch, lambda i: ops.quant_linear(x, qts[i % copies], None, torch.bfloat16), 2 * copies, 3
+            )
+            us = statistics.median(times)
+            gbs = algorithmic_bytes(m, n, k, bits=bits) / (us * 1e-6) / 1e9
+            tflops = 2 * m * n * k / (us * 1e-6) / 1e12
+            rows.append({"proj": name, "bits": bits, "M": m, "us": round(us, 2), "GB/s": round(gbs, 1),
+                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 3), "TFLOP/s": round(tflops, 2),
+                         "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)})
+            print(f"# bits {name} {bits}-bit M={m:5d} {us:9.2f} us {gbs:8.1f} GB/s {tflops:8.2f} TFLOP/s",
+                  file=sys.stderr, flush=True)
+            del x
+        del qts, qt
+    return rows
+
+
+def sweep(torch, ops, rotations):
+    """Per-projection kernel times for decode and prefill batch sizes, each rotating over at
+    least 512 MiB of that projection's weight copies."""
     bf16 = torch.bfloat16
     rows = []
     for m in (1, 8, 32, 64, 256, 2048, 8192):
         for name, n, k in PROJECTIONS:
+            qts = rotations[name]
             x = torch.randn(m, k, device="cuda:0").to(bf16)
-            ops.quant_linear(x, layers[0][name], None, bf16)
-            reps = 4 * copies if m <= 2048 else copies
+            ops.quant_linear(x, qts[0], None, bf16)
+            reps = 2 * len(qts) if m <= 2048 else min(len(qts), 16)
             times = kernel_launch_times(
-                torch, lambda i: ops.quant_linear(x, layers[i % copies][name], None, bf16), reps, 3
+                torch, lambda i: ops.quant_linear(x, qts[i % len(qts)], None, bf16), reps, 3
             )
             us = statistics.median(times)
             gbs = algorithmic_bytes(m, n, k) / (us * 1e-6) / 1e9

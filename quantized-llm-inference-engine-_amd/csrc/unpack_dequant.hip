@@ -51,7 +51,7 @@ __device__ __forceinline__ void store_elem(void* out, int64_t idx, float v) {
   static_cast<typename Out::raw*>(out)[idx] = Out::store(v);
 }
 
-// Dense weight: each thread produces eight consecutive columns of one row.
+// Dense weight, any geometry: each thread produces eight consecutive columns of one row.
 template <class Out>
 __global__ void __launch_bounds__(256) dequant_kernel(const LinearArgs a, void* out) {
   const int64_t chunks = (a.K + 7) / 8;
@@ -75,6 +75,48 @@ __global__ void __launch_bounds__(256) dequant_kernel(const LinearArgs a, void* 
       const float z = zrow ? zrow[g] : a.zero_const;
       store_elem<Out>(out, n * a.K + k, dequant_exact(q, z, srow[g]));
       ++in_group;
+    }
+  }
+}
+
+// Dense weight, vectorized: rows of whole 8-code chunks (K % 8 == 0, group % 8 == 0, rows of
+// packed codes 4-byte (nibbles) or 8-byte (bytes) aligned). Thread (chunk c, row n) reads the
+// chunk's 4 or 8 code bytes and its group's scale and zero, and writes eight consecutive
+// outputs with 16-byte stores, so a wave moves one contiguous run of each row. Grid: x covers
+// a row's chunks, y strides over rows.
+template <class Out, int FMT>
+__global__ void __launch_bounds__(256) dequant_chunks_kernel(const LinearArgs a, void* out) {
+  using Raw = typename Out::raw;
+  const int64_t chunks = a.K >> 3;
+  const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= chunks) return;
+  const int64_t g = (c * 8) / a.group;
+  for (int64_t n = blockIdx.y; n < a.N; n += gridDim.y) {
+    const uint8_t* row = a.qw + n * a.ldq;
+    float q[8];
+    if constexpr (FMT == kNibble) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(row + c * 4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) q[j] = float((w >> (4 * j)) & 0xFu);
+    } else {
+      const u32x2 w = *reinterpret_cast<const u32x2*>(row + c * 8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t b = ((j < 4 ? w.x : w.y) >> (8 * (j & 3))) & 0xFFu;
+        q[j] = a.signed_codes ? float(int8_t(b)) : float(b);
+      }
+    }
+    const float s = a.scales[n * a.G + g];
+    const float z = a.symmetric ? a.zero_const : a.zeros[n * a.G + g];
+    Raw v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = Out::store(dequant_exact(q[j], z, s));
+    u32x4* dst = reinterpret_cast<u32x4*>(static_cast<Raw*>(out) + n * a.K + c * 8);
+#pragma unroll
+    for (int h = 0; h < int(sizeof(v) / 16); ++h) {
+      u32x4 piece;
+      __builtin_memcpy(&piece, reinterpret_cast<const char*>(v) + 16 * h, 16);
+      dst[h] = piece;
     }
   }
 }
@@ -105,8 +147,32 @@ hipError_t launch_unpack(const uint8_t* packed, uint8_t* codes, int64_t rows, in
   return hipGetLastError();
 }
 
+template <class Out>
+void launch_dequant_chunks(const LinearArgs& a, void* out, hipStream_t stream) {
+  const int64_t chunks = a.K >> 3;
+  const dim3 grid(unsigned((chunks + 255) / 256), unsigned(a.N < 65535 ? a.N : 65535));
+  if (a.fmt == kNibble)
+    hipLaunchKernelGGL((dequant_chunks_kernel<Out, kNibble>), grid, dim3(256), 0, stream, a, out);
+  else
+    hipLaunchKernelGGL((dequant_chunks_kernel<Out, kByte>), grid, dim3(256), 0, stream, a, out);
+}
+
 hipError_t launch_dequant(const LinearArgs& a, void* out, int out_dtype, hipStream_t stream) {
   if (a.N == 0 || a.K == 0) return hipSuccess;
+  const uintptr_t qa = reinterpret_cast<uintptr_t>(a.qw);
+  const int64_t code_align = a.fmt == kNibble ? 4 : 8;
+  const bool chunked = a.K % 8 == 0 && a.group % 8 == 0 && a.ldq % code_align == 0 &&
+                       qa % code_align == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                       (a.K >> 3) <= int64_t(65535) * 256;
+  if (chunked) {
+    switch (out_dtype) {
+      case kDtF32: launch_dequant_chunks<ActF32>(a, out, stream); break;
+      case kDtF16: launch_dequant_chunks<ActF16>(a, out, stream); break;
+      case kDtBf16: launch_dequant_chunks<ActBf16>(a, out, stream); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   const dim3 grid(grid_for(a.N * ((a.K + 7) / 8), 256));
   switch (out_dtype) {
     case kDtF32:

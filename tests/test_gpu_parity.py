@@ -110,7 +110,11 @@ def test_unpack_every_byte_value_and_views():
 
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("symmetric", [False, True])
-@pytest.mark.parametrize("rows,cols,group", [(48, 256, 128), (64, 176, 16), (33, 96, 32), (16, 512, 0)])
+@pytest.mark.parametrize(
+    "rows,cols,group",
+    # 8-code chunks (the vectorized kernel), then K % 8 != 0 and group % 8 != 0 (the generic one)
+    [(48, 256, 128), (64, 176, 16), (33, 96, 32), (16, 512, 0), (8, 100, 10), (16, 96, 12)],
+)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_dequant_bit_exact(bits, symmetric, rows, cols, group, dtype):
     qt = _host_qt(rows, cols, bits, group if group else cols, symmetric, seed=rows + cols + bits)
@@ -119,6 +123,13 @@ def test_dequant_bit_exact(bits, symmetric, rows, cols, group, dtype):
     got = dequantize(_to_device(qt), dtype)
     assert got.dtype == dtype and got.shape == (rows, cols)
     np.testing.assert_array_equal(_bits_of(got), _expected_bits(_oracle_dense(qt), dtype))
+
+
+def test_dequant_more_rows_than_one_grid_dimension():
+    # 70000 rows exceed the 65535 workgroups of one grid dimension: rows are strided.
+    qt = _host_qt(70000, 16, 4, 8, False, seed=11)
+    got = dequantize(_to_device(qt), torch.bfloat16)
+    np.testing.assert_array_equal(_bits_of(got), _expected_bits(_oracle_dense(qt), torch.bfloat16))
 
 
 def test_dequant_extreme_scales_bit_exact():
