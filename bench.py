@@ -287,6 +287,7 @@ def main() -> int:
         "roofline": roofline,
     }
     result["dequant"] = dequant_rate(torch, ops, rotations)
+    result["quantize"] = quantize_rate(torch, ops)
     if not args.no_prefill:
         result["prefill"] = prefill(torch, ops, rotations)
     if args.sweep:
@@ -341,6 +342,41 @@ def dequant_rate(torch, ops, rotations):
     print(f"# dequantize gate_up -> bf16: {us:.1f} us, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
     return {"kernel": f"dequantize gate_up (N {n}, K {k}) W4 g128 -> bf16", "us": round(us, 2),
             "bytes": moved, "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def quantize_rate(torch, ops):
+    """The on-device round-to-nearest quantizer on gate_up (bf16 [28672, 4096] -> W4 g128 asym),
+    beside the reference's torch sequence (choose_qparams, quantize_to_codes, pack_int4) run by
+    torch on the same GPU. Both are bit-exact with the reference; `GB/s` counts the weight read
+    once and codes, scales and zeros written once."""
+    from llmopt.quantization.quantizers import choose_qparams, pack_int4, quantize_to_codes
+
+    name, n, k = PROJECTIONS[2]
+    gen = torch.Generator(device="cuda:0").manual_seed(5)
+    copies = max(2, -(-MIN_ROTATION_BYTES // (2 * n * k)))
+    ws = [(torch.randn(n, k, generator=gen, device="cuda:0") * 0.02).to(torch.bfloat16) for _ in range(copies)]
+    times = kernel_launch_times(torch, lambda i: ops.quantize_rtn(ws[i % copies], 4, GROUP, False), 2 * copies, 3)
+    us = statistics.median(times)
+    moved = 2 * n * k + algorithmic_bytes(0, n, k)
+    gbs = moved / (us * 1e-6) / 1e9
+
+    def torch_sequence(w):
+        scales, zeros = choose_qparams(w, 4, GROUP, False)
+        return pack_int4(quantize_to_codes(w, scales, zeros, 4, GROUP, False)), scales, zeros
+
+    torch_sequence(ws[0])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(copies):
+        torch_sequence(ws[i])
+    torch.cuda.synchronize()
+    torch_us = (time.perf_counter() - t0) * 1e6 / copies
+    print(f"# quantize gate_up bf16 -> W4 g128: {us:.1f} us, {gbs:.0f} GB/s; torch sequence {torch_us:.0f} us",
+          file=sys.stderr, flush=True)
+    del ws
+    return {"kernel": f"round-to-nearest quantize gate_up bf16 (N {n}, K {k}) -> W4 g128 asym", "us": round(us, 2),
+            "bytes": moved, "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "torch_sequence_us": round(torch_us, 1)}
 
 
 def dense_comparator(torch, qt, m: int):

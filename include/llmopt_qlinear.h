@@ -83,6 +83,19 @@ int llmopt_q_dequant(const void* qweight, int64_t ldq, const float* scales, cons
                      int symmetric, int signed_codes, void* stream);
 
 /*
+ * Round-to-nearest quantization of a dense weight into the packed layout, in one pass.
+ * Replaces RoundToNearestQuantizer.quantize (src/llmopt/quantization/quantizers.py:285-305),
+ * i.e. choose_qparams (:100-142), quantize_to_codes (:167-201) and pack_int4 (:83-89),
+ * bit-exact with their fp32 arithmetic on finite weights.
+ * weight: [N, ldw] of w_dtype; bits in {2, 4, 8}; group_size divides K (even below 8 bits).
+ * qweight: [N, ldq] bytes -- uint8 two codes per byte (bits < 8), uint8 (asymmetric 8-bit) or
+ * int8 (symmetric 8-bit); scales, zeros: [N, K/group] fp32 (zeros are 0 when symmetric).
+ */
+int llmopt_q_quantize_rtn(const void* weight, int w_dtype, int64_t ldw, int64_t N, int64_t K, int bits,
+                          int group_size, int symmetric, void* qweight, int64_t ldq, float* scales,
+                          float* zeros, void* stream);
+
+/*
  * Bytes of workspace llmopt_q_linear may use for these sizes (0 if none).
  */
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size);

@@ -203,6 +203,45 @@ int llmopt_q_dequant(const void* qweight, int64_t ldq, const float* scales, cons
                     "dequant launch");
 }
 
+int llmopt_q_quantize_rtn(const void* weight, int w_dtype, int64_t ldw, int64_t N, int64_t K, int bits,
+                          int group_size, int symmetric, void* qweight, int64_t ldq, float* scales,
+                          float* zeros, void* stream) {
+  if (!valid_dtype(w_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", w_dtype);
+  // Quantizer validation (quantizers.py:252-255) and choose_qparams' divisibility check (:123-124).
+  if (bits != 2 && bits != 4 && bits != 8) return fail(LLMOPT_ERR_INVALID_ARG, "unsupported bit width: %d", bits);
+  if (N < 0 || K < 0) return fail(LLMOPT_ERR_INVALID_ARG, "negative shape N=%lld K=%lld", (long long)N, (long long)K);
+  const int64_t group = group_size <= 0 ? K : group_size;
+  if (K > 0 && K % group != 0)
+    return fail(LLMOPT_ERR_INVALID_ARG, "in_features=%lld not divisible by group_size=%lld", (long long)K,
+                (long long)group);
+  if (bits < 8 && group % 2 != 0)  // pack_int4 needs whole bytes (quantizers.py:85-86)
+    return fail(LLMOPT_ERR_INVALID_ARG, "4-bit packing requires an even number of columns");
+  if (ldw < K) return fail(LLMOPT_ERR_INVALID_ARG, "weight row stride %lld < in_features %lld", (long long)ldw,
+                           (long long)K);
+  const int64_t need = bits == 8 ? K : K / 2;
+  if (ldq < need)
+    return fail(LLMOPT_ERR_INVALID_ARG, "packed row of %lld bytes cannot hold %lld columns", (long long)ldq,
+                (long long)K);
+  if (N == 0 || K == 0) return LLMOPT_OK;
+  if (!weight || !qweight || !scales || !zeros) return fail(LLMOPT_ERR_INVALID_ARG, "null pointer argument");
+  if (N * K / 8 >= (int64_t(1) << 38)) return fail(LLMOPT_ERR_UNSUPPORTED, "weight too large for one launch");
+  llmopt::RtnArgs a{};
+  a.w = weight;
+  a.w_dtype = w_dtype;
+  a.ldw = ldw;
+  a.N = N;
+  a.K = K;
+  a.bits = bits;
+  a.group = group;
+  a.G = K / group;
+  a.symmetric = symmetric ? 1 : 0;
+  a.q = static_cast<uint8_t*>(qweight);
+  a.ldq = ldq;
+  a.scales = scales;
+  a.zeros = zeros;
+  return hip_status(llmopt::launch_quantize_rtn(a, static_cast<hipStream_t>(stream)), "quantize launch");
+}
+
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
   // Only the prefill GEMM (M > 64) splits K; the decode kernels reduce in LDS.
   if (M <= 64 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;

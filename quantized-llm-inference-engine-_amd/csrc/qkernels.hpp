@@ -38,6 +38,23 @@ enum : int { kEpiNone = 0, kEpiSwiglu = 1 };
 hipError_t launch_unpack(const uint8_t* packed, uint8_t* codes, int64_t rows, int64_t packed_cols,
                          int64_t columns, hipStream_t stream);
 hipError_t launch_dequant(const LinearArgs& a, void* out, int out_dtype, hipStream_t stream);
+
+// Round-to-nearest quantization of a dense weight into the packed layout.
+struct RtnArgs {
+  const void* w;   // [N, ldw] weight of w_dtype
+  int w_dtype;     // kDtF32 / kDtF16 / kDtBf16
+  int64_t ldw;     // row stride of w, elements
+  int64_t N, K;
+  int bits;        // 2, 4 or 8
+  int64_t group;   // columns per group (divides K; even)
+  int64_t G;       // K / group
+  int symmetric;
+  uint8_t* q;      // [N, ldq] codes: two per byte below 8 bits
+  int64_t ldq;     // row stride of q, bytes
+  float* scales;   // [N, G]
+  float* zeros;    // [N, G] (zeros written even for symmetric grids)
+};
+hipError_t launch_quantize_rtn(const RtnArgs& a, hipStream_t stream);
 hipError_t launch_linear_generic(const LinearArgs& a, hipStream_t stream);
 // Decode and prefill report `fits = false` (and launch nothing) when the shape, alignment or
 // dtype is outside what the kernel handles.

@@ -50,6 +50,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int,
         [_p, _i64, _p, _p, _p, _int, _i64, _i64, _int, _int, _int, _int, _p],
     ),
+    "llmopt_q_quantize_rtn": (
+        _int,
+        [_p, _int, _i64, _i64, _i64, _int, _int, _int, _p, _i64, _p, _p, _p],
+    ),
     "llmopt_q_linear_workspace": (_size, [_i64, _i64, _i64, _int, _int]),
     "llmopt_q_linear_swiglu_workspace": (_size, [_i64, _i64, _i64, _int, _int]),
     "llmopt_q_linear_swiglu": (

@@ -5,7 +5,9 @@ These are the only entry points the quantization layer uses on HIP devices:
 * :func:`unpack_nibbles` replaces ``unpack_int4`` (``quantizers.py:92-97``),
 * :func:`dequantize` replaces ``dequantize`` (``quantizers.py:231-239``),
 * :func:`quant_linear` replaces the dequantize-then-``F.linear`` body of
-  ``QuantLinear.forward`` (``quant_linear.py:93-113``).
+  ``QuantLinear.forward`` (``quant_linear.py:93-113``),
+* :func:`quantize_rtn` replaces ``RoundToNearestQuantizer.quantize``
+  (``quantizers.py:285-305``) in one pass over the weight.
 
 Each wrapper checks what torch would check (dtypes, devices, shapes), passes raw
 device pointers and the current HIP stream to the library, and raises if the
@@ -18,7 +20,7 @@ import torch
 
 from llmopt.kernels._lib import ALGO_AUTO, DTYPE_CODES, call, load_library
 
-__all__ = ["dequantize", "quant_linear", "quant_linear_swiglu", "unpack_nibbles"]
+__all__ = ["dequantize", "quant_linear", "quant_linear_swiglu", "quantize_rtn", "unpack_nibbles"]
 
 
 def _stream_handle(device: torch.device) -> int:
@@ -80,6 +82,48 @@ def _weight_args(qt, device: torch.device):  # noqa: ANN001, ANN202 - QuantizedT
     zeros = None if qt.symmetric else _metadata(qt.zeros, rows, groups, "zeros")
     signed = qweight.dtype == torch.int8
     return qweight, int(qweight.shape[1]), scales, zeros, rows, cols, int(qt.group_size), signed
+
+
+def quantize_rtn(
+    weight: torch.Tensor, bits: int, group_size: int, symmetric: bool
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Round-to-nearest quantization of a HIP weight ``[out, in]``: ``(qweight, scales, zeros)``.
+
+    Bit-exact with ``choose_qparams`` + ``quantize_to_codes`` + ``pack_int4`` on the host
+    (``quantizers.py:83-89,100-142,167-201``): ``qweight`` is ``uint8 [out, in/2]`` below 8 bits,
+    ``uint8``/``int8 [out, in]`` at 8 bits (asymmetric/symmetric); ``scales`` and ``zeros`` are
+    fp32 ``[out, in/group]`` (``zeros`` all 0 when symmetric). float64 weights are rounded to
+    fp32 first, which commutes with the reference's min/max and is what its division sees.
+    """
+    if weight.dim() != 2:
+        raise ValueError(f"expected a 2D weight, got shape {tuple(weight.shape)}")
+    if not weight.is_floating_point():
+        raise TypeError(f"expected a floating-point weight, got {weight.dtype}")
+    if weight.dtype == torch.float64:
+        weight = weight.to(torch.float32)
+    rows, cols = (int(d) for d in weight.shape)
+    group = cols if group_size is None or group_size <= 0 else int(group_size)
+    if cols % group:
+        raise ValueError(f"in_features={cols} not divisible by group_size={group}")
+    w = weight.contiguous()
+    dev = w.device
+    if bits == 8:
+        qweight = torch.empty(rows, cols, dtype=torch.int8 if symmetric else torch.uint8, device=dev)
+    else:
+        qweight = torch.empty(rows, cols // 2, dtype=torch.uint8, device=dev)
+    groups = cols // group if cols else 0
+    scales = torch.empty(rows, groups, dtype=torch.float32, device=dev)
+    zeros = torch.empty(rows, groups, dtype=torch.float32, device=dev)
+    lib = load_library()
+    call(
+        lib.llmopt_q_quantize_rtn(
+            w.data_ptr(), DTYPE_CODES[w.dtype], cols, rows, cols, int(bits), group, int(bool(symmetric)),
+            qweight.data_ptr(), int(qweight.shape[1]), scales.data_ptr(), zeros.data_ptr(),
+            _stream_handle(dev),
+        ),
+        "llmopt_q_quantize_rtn",
+    )
+    return qweight, scales, zeros
 
 
 def unpack_nibbles(packed: torch.Tensor, columns: int) -> torch.Tensor:

@@ -322,6 +322,20 @@ class RoundToNearestQuantizer(Quantizer):
         weight = weight.detach()
         if weight.dim() != 2:
             raise ValueError(f"expected a 2D weight, got {tuple(weight.shape)}")
+        if _on_hip(weight):
+            # One fused pass on the GPU, bit-exact with the sequence below.
+            from llmopt.kernels import ops
+
+            qweight, scales, zeros = ops.quantize_rtn(weight, self.bits, self.group_size, self.symmetric)
+            return QuantizedTensor(
+                qweight=qweight,
+                scales=scales,
+                zeros=zeros,
+                bits=self.bits,
+                group_size=self.group_size,
+                symmetric=self.symmetric,
+                shape=tuple(weight.shape),
+            )
         scales, zeros = choose_qparams(weight, self.bits, self.group_size, self.symmetric)
         codes = quantize_to_codes(weight, scales, zeros, self.bits, self.group_size, self.symmetric)
         return self._finalize(codes, scales, zeros, tuple(weight.shape))

@@ -67,6 +67,18 @@ def test_host_side_validation_reports_errors(lib):
     assert lib.llmopt_q_linear_ex(1, 1, 64, 64, 1, 32, 1, 1, None, 1, 8, 8, 2, 4, 32, 0, 0, None, 0, None, 9) == -1
     # Unpack asked for more columns than the bytes hold.
     assert lib.llmopt_q_unpack(None, None, 2, 4, 9, None) == -1
+    # Quantizer: bad width, group not dividing K, odd group under nibble packing, short rows.
+    q = lib.llmopt_q_quantize_rtn
+    assert q(1, 2, 64, 4, 64, 3, 32, 0, 1, 32, 1, 1, None) == -1
+    assert b"bit width" in lib.llmopt_q_last_error()
+    assert q(1, 2, 64, 4, 64, 4, 48, 0, 1, 32, 1, 1, None) == -1
+    assert b"not divisible" in lib.llmopt_q_last_error()
+    assert q(1, 2, 66, 4, 66, 4, 33, 0, 1, 33, 1, 1, None) == -1
+    assert b"even number of columns" in lib.llmopt_q_last_error()
+    assert q(1, 2, 64, 4, 64, 8, 32, 0, 1, 32, 1, 1, None) == -1
+    assert b"cannot hold" in lib.llmopt_q_last_error()
+    assert q(1, 5, 64, 4, 64, 4, 32, 0, 1, 32, 1, 1, None) == -1  # dtype code
+    assert q(None, 2, 64, 0, 64, 4, 32, 0, None, 32, None, None, None) == 0  # no rows: no-op
     # Empty batches are a no-op that succeeds without touching the device.
     assert lib.llmopt_q_linear(None, 0, 64, 64, 1, 32, 1, 1, None, None, 8, 8, 2, 4, 32, 0, 0, None, 0, None) == 0
 
