@@ -526,13 +526,9 @@ def _counter_per_dispatch(csv_path: Path, counter: str):
                 kern.append(value)
             elif "copy" in name.lower() and grid > 0:
                 copy.append(value)
-    # Keep the flush copies -- the most frequent copy size of the run, one before every launch --
-    # not the copies that set up the weights.
-    groups: dict[int, list[float]] = {}
-    for v in copy:
-        if v >= 1024:
-            groups.setdefault(round(v / 1024), []).append(v)
-    flushes = max(groups.values(), key=len) if groups else []
+    # Keep the flush copies (COPY_BYTES, one before every launch; the counter may see half of
+    # them), not the smaller copies that set up the weight copies.
+    flushes = [v for v in copy if v * 1024 >= COPY_BYTES / 4]
     return kern, flushes
 
 
