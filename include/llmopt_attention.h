@@ -1,0 +1,75 @@
+/*
+ * llmopt_attention.h -- C ABI of the paged KV cache writes and the decode attention in
+ * libllmopt_qlinear.so (gfx950). Same conventions as llmopt_qlinear.h: device pointers owned by
+ * the caller, `stream` a hipStream_t as void*, LLMOPT_OK or a negative LLMOPT_ERR_* code with
+ * the message in llmopt_q_last_error(), dtype codes LLMOPT_DTYPE_*.
+ *
+ * Cache layout (the reference's, src/llmopt/cache/paged_cache.py:152-160): each layer's key and
+ * value caches are [num_blocks, block_size, kv_heads, head_dim], row-major; callers pass the
+ * layer's base pointers. Token t of sequence s lives in block block_ids[s * ldb + t / block_size]
+ * at slot t % block_size. block_ids, token offsets and context lengths are int32.
+ */
+#ifndef LLMOPT_ATTENTION_H_
+#define LLMOPT_ATTENTION_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * One new token per sequence into the cache. Replaces PagedKVCache.write_decode
+ * (src/llmopt/cache/paged_cache.py:246-277). keys/values: [num_seqs, kv_heads, head_dim] of
+ * src_dtype, row stride src_seq_stride elements; converted to cache_dtype with round-to-nearest-
+ * even, as .to(dtype) does. A block id outside [0, num_blocks) writes block 0, as the reference
+ * does; an offset whose block index is outside [0, ldb) writes nothing (the reference raises).
+ */
+int llmopt_kv_write_decode(void* key_cache, void* value_cache, int cache_dtype, int64_t num_blocks,
+                           int64_t block_size, int64_t kv_heads, int64_t head_dim, const int32_t* block_ids,
+                           int64_t ldb, const int32_t* token_offsets, const void* keys, const void* values,
+                           int src_dtype, int64_t src_seq_stride, int64_t num_seqs, void* stream);
+
+/*
+ * q_len new tokens per sequence, from token_offsets[s]. Replaces PagedKVCache.write / _write_one
+ * (src/llmopt/cache/paged_cache.py:187-244): a sequence stops at its first -1 block or at the end
+ * of its table row. keys/values: [num_seqs, q_len, kv_heads, head_dim] with element strides
+ * src_seq_stride (sequence) and src_token_stride (token).
+ */
+int llmopt_kv_write(void* key_cache, void* value_cache, int cache_dtype, int64_t num_blocks, int64_t block_size,
+                    int64_t kv_heads, int64_t head_dim, const int32_t* block_ids, int64_t ldb,
+                    const int32_t* token_offsets, const void* keys, const void* values, int src_dtype,
+                    int64_t src_seq_stride, int64_t src_token_stride, int64_t num_seqs, int64_t q_len,
+                    void* stream);
+
+/*
+ * Bytes of workspace llmopt_paged_attention_decode uses to split the context (0: no split).
+ */
+size_t llmopt_paged_attention_workspace(int64_t num_seqs, int64_t num_heads, int64_t kv_heads, int64_t head_dim,
+                                        int64_t ldb, int64_t block_size);
+
+/*
+ * Decode attention (one query token per sequence) read in place from the paged cache. Replaces
+ * PagedAttention.forward with q_len == 1 (src/llmopt/attention/paged_attention.py:145-182,
+ * 218-290), which gathers the K/V into a padded tensor first (paged_cache.py:279-324).
+ * query: [num_seqs, num_heads, head_dim] of q_dtype, row stride q_seq_stride elements; it is
+ * cast to the cache dtype as the reference does. out: [num_seqs, num_heads, head_dim] of
+ * q_dtype. Query head h reads KV head h / (num_heads / kv_heads). Keys are the tokens
+ * t < context_lens[s] whose block id is >= 0; a sequence without keys gets zeros. softcap > 0
+ * applies tanh(x / softcap) * softcap to the scaled scores. Supported: cache_dtype F16/BF16,
+ * head_dim 64 or 128, num_heads / kv_heads in {1, 2, 4, 8, 16}; otherwise
+ * LLMOPT_ERR_UNSUPPORTED. With less workspace than llmopt_paged_attention_workspace asks for,
+ * the context is not split (correct, slower for few sequences).
+ */
+int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_stride, const void* key_cache,
+                                  const void* value_cache, int cache_dtype, int64_t num_blocks, int64_t block_size,
+                                  int64_t kv_heads, int64_t head_dim, const int32_t* block_ids, int64_t ldb,
+                                  const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
+                                  float softcap, void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLMOPT_ATTENTION_H_ */

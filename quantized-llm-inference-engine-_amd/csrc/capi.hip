@@ -9,6 +9,7 @@
 
 #include <string>
 
+#include "../../include/llmopt_attention.h"
 #include "../../include/llmopt_qlinear.h"
 #include "qcommon.hpp"
 #include "qkernels.hpp"
@@ -292,6 +293,176 @@ int llmopt_q_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void
   return llmopt_q_linear_ex(x, M, K, ldx, qweight, ldq, scales, zeros, bias, y, N, ldy, act_dtype,
                             bits, group_size, symmetric, signed_codes, workspace, workspace_bytes,
                             stream, LLMOPT_ALGO_AUTO);
+}
+
+}  // extern "C"
+
+namespace {
+
+int describe_cache(llmopt::KvWriteArgs& a, void* key_cache, void* value_cache, int cache_dtype, int64_t num_blocks,
+                   int64_t block_size, int64_t kv_heads, int64_t head_dim, const int32_t* block_ids, int64_t ldb) {
+  if (!valid_dtype(cache_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad cache dtype code %d", cache_dtype);
+  if (num_blocks < 1 || block_size < 1 || kv_heads < 1 || head_dim < 1 || ldb < 0)
+    return fail(LLMOPT_ERR_INVALID_ARG, "bad cache geometry: blocks %lld, block_size %lld, kv_heads %lld, "
+                "head_dim %lld, table width %lld", (long long)num_blocks, (long long)block_size, (long long)kv_heads,
+                (long long)head_dim, (long long)ldb);
+  a.key_cache = key_cache;
+  a.value_cache = value_cache;
+  a.cache_dtype = cache_dtype;
+  a.num_blocks = num_blocks;
+  a.block_size = block_size;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.block_ids = block_ids;
+  a.ldb = ldb;
+  return LLMOPT_OK;
+}
+
+// Context splits for decode attention: enough (sequence, KV head, split) waves to cover the
+// chip (about 1024), at least four 16-token tiles per split.
+void plan_decode_splits(int64_t num_seqs, int64_t kv_heads, int64_t ldb, int64_t block_size, int* splits,
+                        int64_t* tiles_per_split) {
+  const int64_t tiles = (ldb * block_size + 15) / 16;
+  const int64_t pairs = num_seqs * kv_heads;
+  const int64_t want = pairs > 0 ? (1024 + pairs - 1) / pairs : 1;
+  int64_t per = want > 0 ? (tiles + want - 1) / want : tiles;
+  if (per < 4) per = 4;
+  if (per < 1) per = 1;
+  int64_t n = tiles > 0 ? (tiles + per - 1) / per : 1;
+  if (n > 1024) {  // keep the merge short
+    n = 1024;
+    per = (tiles + n - 1) / n;
+  }
+  *splits = int(n < 1 ? 1 : n);
+  *tiles_per_split = per;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmopt_kv_write_decode(void* key_cache, void* value_cache, int cache_dtype, int64_t num_blocks,
+                           int64_t block_size, int64_t kv_heads, int64_t head_dim, const int32_t* block_ids,
+                           int64_t ldb, const int32_t* token_offsets, const void* keys, const void* values,
+                           int src_dtype, int64_t src_seq_stride, int64_t num_seqs, void* stream) {
+  llmopt::KvWriteArgs a{};
+  int rc = describe_cache(a, key_cache, value_cache, cache_dtype, num_blocks, block_size, kv_heads, head_dim,
+                          block_ids, ldb);
+  if (rc != LLMOPT_OK) return rc;
+  if (!valid_dtype(src_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", src_dtype);
+  if (num_seqs < 0) return fail(LLMOPT_ERR_INVALID_ARG, "negative sequence count");
+  if (num_seqs == 0) return LLMOPT_OK;
+  if (!key_cache || !value_cache || !block_ids || !token_offsets || !keys || !values)
+    return fail(LLMOPT_ERR_INVALID_ARG, "null pointer argument");
+  a.offsets = token_offsets;
+  a.keys = keys;
+  a.values = values;
+  a.src_dtype = src_dtype;
+  a.src_seq_stride = src_seq_stride;
+  a.src_token_stride = 0;
+  a.num_seqs = num_seqs;
+  return hip_status(llmopt::launch_kv_write(a, 1, true, static_cast<hipStream_t>(stream)), "kv write launch");
+}
+
+int llmopt_kv_write(void* key_cache, void* value_cache, int cache_dtype, int64_t num_blocks, int64_t block_size,
+                    int64_t kv_heads, int64_t head_dim, const int32_t* block_ids, int64_t ldb,
+                    const int32_t* token_offsets, const void* keys, const void* values, int src_dtype,
+                    int64_t src_seq_stride, int64_t src_token_stride, int64_t num_seqs, int64_t q_len,
+                    void* stream) {
+  llmopt::KvWriteArgs a{};
+  int rc = describe_cache(a, key_cache, value_cache, cache_dtype, num_blocks, block_size, kv_heads, head_dim,
+                          block_ids, ldb);
+  if (rc != LLMOPT_OK) return rc;
+  if (!valid_dtype(src_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", src_dtype);
+  if (num_seqs < 0 || q_len < 0) return fail(LLMOPT_ERR_INVALID_ARG, "negative sequence count or q_len");
+  if (num_seqs == 0 || q_len == 0) return LLMOPT_OK;
+  if (q_len > 65535 || num_seqs > 65535)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "q_len %lld x sequences %lld exceed one launch", (long long)q_len,
+                (long long)num_seqs);
+  if (!key_cache || !value_cache || !block_ids || !token_offsets || !keys || !values)
+    return fail(LLMOPT_ERR_INVALID_ARG, "null pointer argument");
+  a.offsets = token_offsets;
+  a.keys = keys;
+  a.values = values;
+  a.src_dtype = src_dtype;
+  a.src_seq_stride = src_seq_stride;
+  a.src_token_stride = src_token_stride;
+  a.num_seqs = num_seqs;
+  return hip_status(llmopt::launch_kv_write(a, q_len, false, static_cast<hipStream_t>(stream)), "kv write launch");
+}
+
+size_t llmopt_paged_attention_workspace(int64_t num_seqs, int64_t num_heads, int64_t kv_heads, int64_t head_dim,
+                                        int64_t ldb, int64_t block_size) {
+  if (num_seqs <= 0 || num_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || ldb <= 0 || block_size <= 0) return 0;
+  int splits = 1;
+  int64_t per = 1;
+  plan_decode_splits(num_seqs, kv_heads, ldb, block_size, &splits, &per);
+  if (splits <= 1) return 0;
+  return size_t(splits) * size_t(num_seqs) * size_t(num_heads) * size_t(head_dim + 1) * sizeof(float);
+}
+
+int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_stride, const void* key_cache,
+                                  const void* value_cache, int cache_dtype, int64_t num_blocks, int64_t block_size,
+                                  int64_t kv_heads, int64_t head_dim, const int32_t* block_ids, int64_t ldb,
+                                  const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
+                                  float softcap, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!valid_dtype(q_dtype) || !valid_dtype(cache_dtype))
+    return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d / %d", q_dtype, cache_dtype);
+  if (num_seqs < 0 || num_heads < 1 || kv_heads < 1 || num_heads % kv_heads != 0)
+    return fail(LLMOPT_ERR_INVALID_ARG, "num_heads %lld must be a positive multiple of kv_heads %lld",
+                (long long)num_heads, (long long)kv_heads);
+  if (num_blocks < 1 || block_size < 1 || ldb < 0 || head_dim < 1)
+    return fail(LLMOPT_ERR_INVALID_ARG, "bad cache geometry");
+  const int64_t group = num_heads / kv_heads;
+  if (cache_dtype == LLMOPT_DTYPE_F32 || (head_dim != 64 && head_dim != 128) ||
+      (group != 1 && group != 2 && group != 4 && group != 8 && group != 16))
+    return fail(LLMOPT_ERR_UNSUPPORTED, "decode attention kernel: cache dtype %d, head_dim %lld, %lld heads per KV "
+                "head", cache_dtype, (long long)head_dim, (long long)group);
+  if (num_blocks * block_size >= (int64_t(1) << 31) || num_seqs > 65535 || kv_heads > 65535)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "cache or batch too large for one launch");
+  if (q_seq_stride < num_heads * head_dim)
+    return fail(LLMOPT_ERR_INVALID_ARG, "query row stride %lld < heads x head_dim", (long long)q_seq_stride);
+  if (num_seqs == 0) return LLMOPT_OK;
+  if (!query || !key_cache || !value_cache || !block_ids || !context_lens || !out)
+    return fail(LLMOPT_ERR_INVALID_ARG, "null pointer argument");
+  if (reinterpret_cast<uintptr_t>(key_cache) % 16 != 0 || reinterpret_cast<uintptr_t>(value_cache) % 16 != 0)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "caches must be 16-byte aligned");
+  llmopt::PagedDecodeArgs a{};
+  a.query = query;
+  a.q_dtype = q_dtype;
+  a.q_seq_stride = q_seq_stride;
+  a.key_cache = key_cache;
+  a.value_cache = value_cache;
+  a.cache_dtype = cache_dtype;
+  a.num_blocks = num_blocks;
+  a.block_size = block_size;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.block_ids = block_ids;
+  a.ldb = ldb;
+  a.context_lens = context_lens;
+  a.num_seqs = num_seqs;
+  a.num_heads = num_heads;
+  a.scale = scale;
+  a.softcap = softcap;
+  a.out = out;
+  a.out_dtype = q_dtype;
+  int splits = 1;
+  int64_t per = 1;
+  plan_decode_splits(num_seqs, kv_heads, ldb, block_size, &splits, &per);
+  const size_t need = llmopt_paged_attention_workspace(num_seqs, num_heads, kv_heads, head_dim, ldb, block_size);
+  if (splits > 1 && (workspace == nullptr || workspace_bytes < need ||
+                     reinterpret_cast<uintptr_t>(workspace) % 16 != 0)) {
+    splits = 1;
+    per = (ldb * block_size + 15) / 16;
+  }
+  a.splits = splits;
+  a.tiles_per_split = per < 1 ? 1 : per;
+  if (splits > 1) {
+    a.part_out = static_cast<float*>(workspace);
+    a.part_lse = a.part_out + size_t(splits) * size_t(num_seqs) * size_t(num_heads) * size_t(head_dim);
+  }
+  return hip_status(llmopt::launch_paged_decode(a, static_cast<hipStream_t>(stream)), "paged attention launch");
 }
 
 }  // extern "C"

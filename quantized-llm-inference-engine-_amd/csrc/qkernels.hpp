@@ -55,6 +55,45 @@ struct RtnArgs {
   float* zeros;    // [N, G] (zeros written even for symmetric grids)
 };
 hipError_t launch_quantize_rtn(const RtnArgs& a, hipStream_t stream);
+
+// Paged KV cache: one layer's caches [num_blocks, block_size, kv_heads, head_dim].
+struct KvWriteArgs {
+  void* key_cache;
+  void* value_cache;
+  int cache_dtype;
+  int64_t num_blocks, block_size, kv_heads, head_dim;
+  const int32_t* block_ids;  // [num_seqs, ldb]
+  int64_t ldb;
+  const int32_t* offsets;    // [num_seqs] first position written
+  const void* keys;          // [num_seqs, (q_len,) kv_heads, head_dim] of src_dtype
+  const void* values;
+  int src_dtype;
+  int64_t src_seq_stride, src_token_stride;  // elements
+  int64_t num_seqs;
+};
+hipError_t launch_kv_write(const KvWriteArgs& a, int64_t q_len, bool decode, hipStream_t stream);
+
+struct PagedDecodeArgs {
+  const void* query;  // [num_seqs, num_heads, head_dim] rows of q_seq_stride elements
+  int q_dtype;
+  int64_t q_seq_stride;
+  const void* key_cache;
+  const void* value_cache;
+  int cache_dtype;
+  int64_t num_blocks, block_size, kv_heads, head_dim;
+  const int32_t* block_ids;
+  int64_t ldb;
+  const int32_t* context_lens;
+  int64_t num_seqs, num_heads;
+  float scale, softcap;
+  void* out;  // [num_seqs, num_heads, head_dim] of out_dtype
+  int out_dtype;
+  float* part_out;  // [splits, num_seqs, num_heads, head_dim]
+  float* part_lse;  // [splits, num_seqs, num_heads]
+  int splits;
+  int64_t tiles_per_split;  // 16-token tiles per split
+};
+hipError_t launch_paged_decode(const PagedDecodeArgs& a, hipStream_t stream);
 hipError_t launch_linear_generic(const LinearArgs& a, hipStream_t stream);
 // Decode and prefill report `fits = false` (and launch nothing) when the shape, alignment or
 // dtype is outside what the kernel handles.

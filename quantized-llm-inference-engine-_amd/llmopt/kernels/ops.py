@@ -7,7 +7,11 @@ These are the only entry points the quantization layer uses on HIP devices:
 * :func:`quant_linear` replaces the dequantize-then-``F.linear`` body of
   ``QuantLinear.forward`` (``quant_linear.py:93-113``),
 * :func:`quantize_rtn` replaces ``RoundToNearestQuantizer.quantize``
-  (``quantizers.py:285-305``) in one pass over the weight.
+  (``quantizers.py:285-305``) in one pass over the weight,
+* :func:`kv_write_decode` / :func:`kv_write` replace ``PagedKVCache.write_decode`` / ``write``
+  (``src/llmopt/cache/paged_cache.py:187-277``),
+* :func:`paged_decode_attention` replaces ``PagedAttention.forward`` for one query token per
+  sequence (``src/llmopt/attention/paged_attention.py:145-290``), reading the cache in place.
 
 Each wrapper checks what torch would check (dtypes, devices, shapes), passes raw
 device pointers and the current HIP stream to the library, and raises if the
@@ -20,7 +24,16 @@ import torch
 
 from llmopt.kernels._lib import ALGO_AUTO, DTYPE_CODES, call, load_library
 
-__all__ = ["dequantize", "quant_linear", "quant_linear_swiglu", "quantize_rtn", "unpack_nibbles"]
+__all__ = [
+    "dequantize",
+    "kv_write",
+    "kv_write_decode",
+    "paged_decode_attention",
+    "quant_linear",
+    "quant_linear_swiglu",
+    "quantize_rtn",
+    "unpack_nibbles",
+]
 
 
 def _stream_handle(device: torch.device) -> int:
@@ -320,4 +333,114 @@ def quant_linear_swiglu(
             )
         call(rc, "llmopt_q_linear_swiglu")
     return y.reshape(*lead_shape, out)
+
+
+# ---- paged KV cache and decode attention -------------------------------------------------------
+
+def _int32(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def _layer_cache(key_cache: torch.Tensor, value_cache: torch.Tensor) -> tuple[int, int, int, int, int]:
+    """Geometry of one layer's caches ``[num_blocks, block_size, kv_heads, head_dim]``."""
+    if key_cache.dim() != 4 or key_cache.shape != value_cache.shape:
+        raise ValueError(f"expected two [blocks, block_size, kv_heads, head_dim] caches, got "
+                         f"{tuple(key_cache.shape)} and {tuple(value_cache.shape)}")
+    if key_cache.dtype != value_cache.dtype or key_cache.dtype not in DTYPE_CODES:
+        raise TypeError(f"unsupported cache dtypes {key_cache.dtype}, {value_cache.dtype}")
+    if not (key_cache.is_contiguous() and value_cache.is_contiguous()):
+        raise ValueError("the caches must be contiguous")
+    nb, bs, kvh, hd = (int(d) for d in key_cache.shape)
+    return nb, bs, kvh, hd, DTYPE_CODES[key_cache.dtype]
+
+
+def kv_write_decode(key_cache, value_cache, block_ids, token_offsets, keys, values) -> None:  # noqa: ANN001
+    """``PagedKVCache.write_decode`` for one layer: ``keys``/``values`` ``[seq, kv_heads, head_dim]``."""
+    nb, bs, kvh, hd, cdt = _layer_cache(key_cache, value_cache)
+    seqs = int(keys.shape[0])
+    if seqs == 0:
+        return
+    dev = key_cache.device
+    if keys.dtype not in DTYPE_CODES:
+        keys, values = keys.to(key_cache.dtype), values.to(key_cache.dtype)
+    k = keys.reshape(seqs, kvh * hd).contiguous()
+    v = values.reshape(seqs, kvh * hd).to(k.dtype).contiguous()
+    table = _int32(block_ids, dev)
+    offsets = _int32(token_offsets, dev)
+    lib = load_library()
+    call(
+        lib.llmopt_kv_write_decode(
+            key_cache.data_ptr(), value_cache.data_ptr(), cdt, nb, bs, kvh, hd, table.data_ptr(),
+            int(table.shape[1]), offsets.data_ptr(), k.data_ptr(), v.data_ptr(), DTYPE_CODES[k.dtype],
+            kvh * hd, seqs, _stream_handle(dev),
+        ),
+        "llmopt_kv_write_decode",
+    )
+
+
+def kv_write(key_cache, value_cache, block_ids, token_offsets, keys, values) -> None:  # noqa: ANN001
+    """``PagedKVCache.write`` for one layer: ``keys``/``values`` ``[seq, q_len, kv_heads, head_dim]``."""
+    nb, bs, kvh, hd, cdt = _layer_cache(key_cache, value_cache)
+    seqs, q_len = int(keys.shape[0]), int(keys.shape[1])
+    if seqs == 0 or q_len == 0:
+        return
+    dev = key_cache.device
+    if keys.dtype not in DTYPE_CODES:
+        keys, values = keys.to(key_cache.dtype), values.to(key_cache.dtype)
+    k = keys.reshape(seqs, q_len, kvh * hd).contiguous()
+    v = values.reshape(seqs, q_len, kvh * hd).to(k.dtype).contiguous()
+    table = _int32(block_ids, dev)
+    offsets = _int32(token_offsets, dev)
+    lib = load_library()
+    call(
+        lib.llmopt_kv_write(
+            key_cache.data_ptr(), value_cache.data_ptr(), cdt, nb, bs, kvh, hd, table.data_ptr(),
+            int(table.shape[1]), offsets.data_ptr(), k.data_ptr(), v.data_ptr(), DTYPE_CODES[k.dtype],
+            q_len * kvh * hd, kvh * hd, seqs, q_len, _stream_handle(dev),
+        ),
+        "llmopt_kv_write",
+    )
+
+
+def paged_decode_attention(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_ids: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    softcap: float = 0.0,
+) -> torch.Tensor:
+    """Decode attention for ``query [seq, heads, head_dim]`` over one layer's paged caches.
+
+    Returns ``[seq, heads, head_dim]`` in the query's dtype. Raises ``NotImplementedError`` for
+    shapes the kernel does not take (fp32 caches, head_dim other than 64/128, more than 16 or a
+    non-power-of-two number of query heads per KV head).
+    """
+    nb, bs, kvh, hd, cdt = _layer_cache(key_cache, value_cache)
+    if query.dim() != 3 or int(query.shape[2]) != hd:
+        raise ValueError(f"query of shape {tuple(query.shape)} does not match head_dim {hd}")
+    if query.dtype not in DTYPE_CODES:
+        raise TypeError(f"unsupported query dtype {query.dtype}")
+    seqs, heads = int(query.shape[0]), int(query.shape[1])
+    dev = key_cache.device
+    q = query.contiguous()
+    out = torch.empty(seqs, heads, hd, dtype=query.dtype, device=dev)
+    if seqs == 0:
+        return out
+    table = _int32(block_ids, dev)
+    lens = _int32(context_lens, dev)
+    ldb = int(table.shape[1])
+    lib = load_library()
+    ws_bytes = lib.llmopt_paged_attention_workspace(seqs, heads, kvh, hd, ldb, bs)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    call(
+        lib.llmopt_paged_attention_decode(
+            q.data_ptr(), DTYPE_CODES[q.dtype], heads * hd, key_cache.data_ptr(), value_cache.data_ptr(), cdt,
+            nb, bs, kvh, hd, table.data_ptr(), ldb, lens.data_ptr(), seqs, heads, float(scale), float(softcap),
+            out.data_ptr(), None if ws is None else ws.data_ptr(), ws_bytes, _stream_handle(dev),
+        ),
+        "llmopt_paged_attention_decode",
+    )
+    return out
 
