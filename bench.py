@@ -21,6 +21,9 @@ roofline       the dominant kernel (gate_up): its algorithmic bytes / its mean t
 prefill        gate_up at M = 8192 through the MFMA prefill kernel, TFLOP/s vs dense bf16 peak
 dense_comparator  (in roofline and prefill) torch's dense bf16 F.linear on the dequantized
                weight at the same shape: hipBLASLt's figure for the unquantized layer
+dequant, quantize, attention  the device dequantize and RTN quantizer on gate_up, and the
+               decode-step paged attention / KV write / last-token vocabulary projection of the
+               end-to-end Llama-3-8B workload (32 sequences, 512-token prompts)
 cpu_baseline   the reference's host sequence (dequantize once, cache the dense bf16 weight,
                F.linear) on this host's cores, for a bounded number of the same decode steps
 
@@ -288,6 +291,7 @@ def main() -> int:
     }
     result["dequant"] = dequant_rate(torch, ops, rotations)
     result["quantize"] = quantize_rate(torch, ops)
+    result["attention"] = attention_rates(torch)
     if not args.no_prefill:
         result["prefill"] = prefill(torch, ops, rotations)
     if args.sweep:
@@ -377,6 +381,75 @@ def quantize_rate(torch, ops):
     return {"kernel": f"round-to-nearest quantize gate_up bf16 (N {n}, K {k}) -> W4 g128 asym", "us": round(us, 2),
             "bytes": moved, "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "torch_sequence_us": round(torch_us, 1)}
+
+
+def attention_rates(torch):
+    """Decode-step attention of the Llama-3-8B end-to-end workload: 32 sequences with 512-640
+    cached tokens (512-token prompts, then up to 128 decoded), 32 query / 8 KV heads of 128,
+    block 16, bf16 cache; one layer per call, rotating over 8 layers' caches (> 512 MiB) as a
+    decode step walks the layers. Also: this step's KV write, the reference's torch sequence for
+    the same attention (gather, matmul, softmax, matmul) on the same GPU, and the vocabulary
+    projection of a 32 x 512-token prefill chunk for all positions vs the last ones only."""
+    from llmopt.attention import PagedAttention, PagedAttentionConfig
+    from llmopt.cache import PagedKVCache
+    from llmopt.logits import last_token_logits
+
+    seqs, heads, kv_heads, head_dim, bs, layers = 32, 32, 8, 128, 16, 8
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(6)
+    ctx = torch.randint(512, 641, (seqs,), generator=gen)
+    width = 41
+    blocks = seqs * width
+    cache = PagedKVCache(layers, blocks, bs, kv_heads, head_dim, dtype=torch.bfloat16, device=dev)
+    cache.key_cache.normal_()
+    cache.value_cache.normal_()
+    table = torch.randperm(blocks, generator=gen).view(seqs, width).to(torch.int32).to(dev)
+    lens = ctx.to(torch.int32).to(dev)
+    q = torch.randn(seqs, heads, 1, head_dim, device=dev).to(torch.bfloat16)
+    attn = PagedAttention(heads, kv_heads, head_dim, config=PagedAttentionConfig(block_size=bs))
+    times = kernel_launch_times(torch, lambda i: attn.forward(q, cache, i % layers, table, lens), 2 * layers, 5)
+    us = statistics.median(times)
+    moved = int(ctx.sum()) * kv_heads * head_dim * 2 * 2 + 2 * q.numel() * 2 + table.numel() * 4
+    gbs = moved / (us * 1e-6) / 1e9
+    torch_attn = PagedAttention(heads, kv_heads, head_dim, config=PagedAttentionConfig(block_size=bs), backend="sdpa")
+    torch_attn.forward(q, cache, 0, table, lens)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(layers):
+        torch_attn.forward(q, cache, i % layers, table, lens)
+    torch.cuda.synchronize()
+    torch_us = (time.perf_counter() - t0) * 1e6 / layers
+    new_k = torch.randn(seqs, kv_heads, head_dim, device=dev).to(torch.bfloat16)
+    offsets = (lens - 1).to(torch.int64)
+    w_times = kernel_launch_times(torch, lambda i: cache.write_decode(i % layers, table, offsets, new_k, new_k),
+                                  2 * layers, 5)
+    print(f"# paged decode attention (32 seqs x 512-640 tokens, 32/8 heads): {us:.1f} us, {gbs:.0f} GB/s; "
+          f"torch sequence {torch_us:.0f} us; KV write {statistics.median(w_times):.1f} us",
+          file=sys.stderr, flush=True)
+    del cache
+
+    # Vocabulary projection of one prefill chunk: every position vs the last ones.
+    hidden_size, vocab, q_len = 4096, 128256, 512
+    head = torch.nn.Linear(hidden_size, vocab, bias=False, device=dev, dtype=torch.bfloat16)
+    hidden = torch.randn(seqs * q_len, hidden_size, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        full = kernel_launch_times(torch, lambda i: head(hidden), 2, 3)
+        last = kernel_launch_times(torch, lambda i: last_token_logits(hidden, head, q_len), 8, 3)
+    full_us, last_us = statistics.median(full), statistics.median(last)
+    print(f"# lm_head over a 32 x 512 prefill chunk: all positions {full_us:.0f} us, last positions {last_us:.0f} us",
+          file=sys.stderr, flush=True)
+    del head, hidden
+    return {
+        "decode_attention": {
+            "workload": "32 seqs x 512-640 cached tokens, 32 query / 8 KV heads x 128, block 16, bf16 cache, "
+                        "one layer per call over 8 layers",
+            "us": round(us, 2), "bytes": moved, "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "torch_sequence_us": round(torch_us, 1),
+        },
+        "kv_write_decode_us": round(statistics.median(w_times), 2),
+        "lm_head_prefill_chunk": {"tokens": seqs * q_len, "all_positions_us": round(full_us, 1),
+                                  "last_positions_us": round(last_us, 1)},
+    }
 
 
 def dense_comparator(torch, qt, m: int):

@@ -418,8 +418,11 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
       (group != 1 && group != 2 && group != 4 && group != 8 && group != 16))
     return fail(LLMOPT_ERR_UNSUPPORTED, "decode attention kernel: cache dtype %d, head_dim %lld, %lld heads per KV "
                 "head", cache_dtype, (long long)head_dim, (long long)group);
-  if (num_blocks * block_size >= (int64_t(1) << 31) || num_seqs > 65535 || kv_heads > 65535)
-    return fail(LLMOPT_ERR_UNSUPPORTED, "cache or batch too large for one launch");
+  if (num_blocks * block_size * kv_heads * head_dim * 2 >= (int64_t(1) << 31) || num_seqs > 65535 ||
+      kv_heads > 65535)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "cache layer (2 GiB at most) or batch too large for one launch");
+  if (ldb >= (int64_t(1) << 31) / (block_size + 16))
+    return fail(LLMOPT_ERR_UNSUPPORTED, "block table row of %lld blocks too long", (long long)ldb);
   if (q_seq_stride < num_heads * head_dim)
     return fail(LLMOPT_ERR_INVALID_ARG, "query row stride %lld < heads x head_dim", (long long)q_seq_stride);
   if (num_seqs == 0) return LLMOPT_OK;

@@ -22,7 +22,8 @@
 //   * online softmax per head in fp32 (running max and sum), masked tokens contribute nothing;
 //   * P V on the VALU with lanes over head dims (HD / 64 dims per lane): each token's V row is one
 //     coalesced 256-byte read per wave, the tile's probabilities come from LDS as broadcasts;
-//   * the next tile's K, V and block ids are in flight while the current one is computed;
+//   * two or three tiles of K and V, and the block ids of as many after them, are in flight
+//     while a tile is computed;
 //   * with several splits each wave writes its normalized partial output and log-sum-exp, and a
 //     merge kernel combines them (the reference's merge_states, paged_attention.py:30-56).
 // Everything is computed in fp32 and rounded once into the query dtype; the reference rounds
@@ -123,8 +124,12 @@ __global__ void __launch_bounds__(64) paged_decode_kernel(const PagedDecodeArgs 
   const int64_t t_begin = split * a.tiles_per_split * 16;
   const int64_t t_end = ctx < t_begin + a.tiles_per_split * 16 ? ctx : t_begin + a.tiles_per_split * 16;
   const int64_t row_stride = a.kv_heads * HD;  // elements between two slots
-  const Raw* const kc = static_cast<const Raw*>(a.key_cache) + kvh * HD;
-  const Raw* const vc = static_cast<const Raw*>(a.value_cache) + kvh * HD;
+  const uint32_t cache_bytes = uint32_t(a.num_blocks * a.block_size * row_stride * int64_t(sizeof(Raw)));
+  const auto krs = make_rsrc(a.key_cache, cache_bytes);
+  const auto vrs = make_rsrc(a.value_cache, cache_bytes);
+  const uint32_t row_bytes = uint32_t(row_stride * int64_t(sizeof(Raw)));
+  const uint32_t head_off = uint32_t(kvh * HD * int64_t(sizeof(Raw)));
+  const uint32_t v_lane_off = uint32_t(kDpl * lane * int(sizeof(Raw)));
   const int32_t* const table = a.block_ids + s * a.ldb;
 
   __shared__ float p_lds[16][GQ < 4 ? 4 : GQ];  // [token][head]
@@ -150,27 +155,39 @@ __global__ void __launch_bounds__(64) paged_decode_kernel(const PagedDecodeArgs 
     }
   }
 
-  // Loads of one tile: lane `col` fetches K of token t0 + col (dims 8kb .. of each 32-dim slice);
-  // every lane fetches its dims of V for all 16 tokens (block ids broadcast through readlane).
-  auto fetch = [&](int64_t t0, u32x4* kf, uint32_t* vf, uint32_t& valid_bits) {
-    const int64_t t = t0 + col;
-    int64_t block = -1;
-    if (t < t_end && t / a.block_size < a.ldb) block = table[t / a.block_size];  // past the row: no key
-    const bool ok = block >= 0 && block < a.num_blocks;
-    const int64_t slot_row = ok ? (block * a.block_size + t % a.block_size) : 0;
+  // Slot row (block * block_size + slot) of token t0 + col, or -1 when that token is not a key.
+  // 32-bit arithmetic: contexts, table widths and slot rows stay below 2^31 (checked on the host).
+  const uint32_t bsz = uint32_t(a.block_size);
+  const uint32_t ldb32 = uint32_t(a.ldb);
+  const uint32_t nblk = uint32_t(a.num_blocks);
+  const uint32_t t_end32 = uint32_t(t_end > 0 ? t_end : 0);
+  auto fetch_row = [&](int64_t t0) -> int32_t {
+    const uint32_t t = uint32_t(t0) + uint32_t(col);
+    const uint32_t bi = t / bsz;
+    int32_t block = -1;
+    if (t < t_end32 && bi < ldb32) block = table[bi];  // past the row: no key
+    const bool ok = block >= 0 && uint32_t(block) < nblk;
+    return ok ? int32_t(uint32_t(block) * bsz + (t - bi * bsz)) : -1;
+  };
+  // K of token t0 + col (dims 8kb .. of each 32-dim slice) and this lane's dims of V for all 16
+  // tokens (slot rows broadcast with readlane, so each V row address is a scalar); masked tokens
+  // read slot row 0. Buffer loads with 32-bit offsets (the host keeps a layer's cache under
+  // 2 GiB), marked to stay in program order so that the ring below keeps them in flight.
+  auto fetch_kv = [&](int32_t row, u32x4* kf, uint32_t* vf, uint32_t& valid_bits) {
+    valid_bits = uint32_t(__builtin_amdgcn_ballot_w64(row >= 0) & 0xFFFFu);
+    const uint32_t r_own = uint32_t(row >= 0 ? row : 0);
 #pragma unroll
     for (int m = 0; m < kNm; ++m)
-      kf[m] = *reinterpret_cast<const u32x4*>(kc + slot_row * row_stride + 32 * m + 8 * kb);
-    valid_bits = uint32_t(__builtin_amdgcn_ballot_w64(ok) & 0xFFFFu);
-    const int32_t row32 = int32_t(slot_row);  // < num_blocks * block_size, checked on the host
+      kf[m] = buf_load16(krs, (r_own * row_bytes) + uint32_t(2 * (32 * m + 8 * kb)), head_off);
+    const int32_t row0 = row >= 0 ? row : 0;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int64_t r = __builtin_amdgcn_readlane(row32, j);
-      const Raw* p = vc + r * row_stride + kDpl * lane;
+      const uint32_t r = uint32_t(__builtin_amdgcn_readlane(row0, j));
       if constexpr (kDpl == 2)
-        vf[j] = *reinterpret_cast<const uint32_t*>(p);
+        vf[j] = __builtin_amdgcn_raw_buffer_load_b32(vrs, v_lane_off, int(r * row_bytes + head_off), kLoadInOrder);
       else
-        vf[j] = uint32_t(*p);
+        vf[j] = uint32_t(__builtin_amdgcn_raw_buffer_load_b16(vrs, v_lane_off, int(r * row_bytes + head_off),
+                                                              kLoadInOrder));
     }
   };
 
@@ -182,14 +199,8 @@ __global__ void __launch_bounds__(64) paged_decode_kernel(const PagedDecodeArgs 
 #pragma unroll
     for (int d = 0; d < kDpl; ++d) o[h][d] = 0.0f;
 
-  u32x4 kf[kNm], kn[kNm];
-  uint32_t vf[16], vn[16];
-  uint32_t bits = 0, bits_n = 0;
-  if (t_begin < t_end) fetch(t_begin, kf, vf, bits);
-  for (int64_t t0 = t_begin; t0 < t_end; t0 += 16) {
-    const bool more = t0 + 16 < t_end;
-    if (more) fetch(t0 + 16, kn, vn, bits_n);
-
+  // One tile: scores on the MFMA, online softmax, P V on the VALU.
+  auto compute = [&](const u32x4* kf, const uint32_t* vf, uint32_t bits) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < kNm; ++m) acc = Mfma16x32<C>::run(kf[m], qf[m], acc);
@@ -250,14 +261,41 @@ __global__ void __launch_bounds__(64) paged_decode_kernel(const PagedDecodeArgs 
       }
     }
     __syncthreads();
-    if (more) {
+  };
+
+  // A ring of kDepth tiles in flight. Slot u holds tile g + u of the current group; after it is
+  // computed it is refilled with tile g + u + kDepth, whose slot rows were loaded kDepth tiles
+  // earlier (rows[u]); the rows for the refill after that are loaded at the same time. The main
+  // loop runs whole groups with unconditional loads (past the last tile they read slot row 0 and
+  // are never used), so the loads keep one static order; the last partial group has no refills.
+  constexpr int kDepth = GQ >= 16 ? 1 : GQ >= 8 ? 2 : 3;  // registers: larger groups keep more accumulators
+  u32x4 kf[kDepth][kNm];
+  uint32_t vf[kDepth][16];
+  uint32_t bits[kDepth];
+  int32_t rows[kDepth];
+  const int64_t n_tiles = t_end > t_begin ? (t_end - t_begin + 15) / 16 : 0;
+  if (n_tiles > 0) {
+    int32_t first[kDepth];
 #pragma unroll
-      for (int m = 0; m < kNm; ++m) kf[m] = kn[m];
+    for (int u = 0; u < kDepth; ++u) first[u] = fetch_row(t_begin + 16 * u);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) vf[j] = vn[j];
-      bits = bits_n;
+    for (int u = 0; u < kDepth; ++u) rows[u] = fetch_row(t_begin + 16 * (u + kDepth));
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) fetch_kv(first[u], kf[u], vf[u], bits[u]);
+  }
+  int64_t g = 0;
+  for (; g + kDepth <= n_tiles; g += kDepth) {
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) {
+      compute(kf[u], vf[u], bits[u]);
+      const int32_t next = rows[u];
+      rows[u] = fetch_row(t_begin + 16 * (g + u + 2 * kDepth));
+      fetch_kv(next, kf[u], vf[u], bits[u]);
     }
   }
+#pragma unroll
+  for (int u = 0; u < kDepth; ++u)
+    if (g + u < n_tiles) compute(kf[u], vf[u], bits[u]);
 
   // Normalize; one split writes the output, several write partials for the merge.
   if (lane < GQ) l_lds[lane] = l_run;
@@ -285,31 +323,53 @@ __global__ void __launch_bounds__(64) paged_decode_kernel(const PagedDecodeArgs 
   if (lane < GQ) a.part_lse[base * a.num_heads + h0 + lane] = l_run > 0.0f ? m_run + __logf(l_run) : neg_inf;
 }
 
-// Combine the splits of one (sequence, head): weights exp(lse_i - max lse).
+// Combine the splits of one (sequence, head): weights exp(lse_i - max lse). The lanes first
+// share the max over the splits, then every lane sums its dims over all splits, four at a time
+// so that their loads overlap.
 template <int HD>
 __global__ void __launch_bounds__(64) paged_merge_kernel(const PagedDecodeArgs a) {
   constexpr int kDpl = HD / 64;
   const int64_t h = blockIdx.x, s = blockIdx.y;
+  const int lane = threadIdx.x;
   const float neg_inf = -__int_as_float(0x7F800000);
+  auto lse_of = [&](int i) { return a.part_lse[(int64_t(i) * a.num_seqs + s) * a.num_heads + h]; };
   float top = neg_inf;
-  for (int i = 0; i < a.splits; ++i) top = fmaxf(top, a.part_lse[(int64_t(i) * a.num_seqs + s) * a.num_heads + h]);
+  for (int i = lane; i < a.splits; i += 64) top = fmaxf(top, lse_of(i));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) top = fmaxf(top, __shfl_xor(top, off, 64));
   float acc[kDpl] = {};
   float wsum = 0.0f;
   if (top != neg_inf) {
-    for (int i = 0; i < a.splits; ++i) {
+    int i = 0;
+    for (; i + 4 <= a.splits; i += 4) {
+      float w[4], v[4][kDpl];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t base = (int64_t(i + u) * a.num_seqs + s) * a.num_heads + h;
+        const float lse = a.part_lse[base];
+        w[u] = lse == neg_inf ? 0.0f : __expf(lse - top);
+#pragma unroll
+        for (int d = 0; d < kDpl; ++d) v[u][d] = a.part_out[base * HD + kDpl * lane + d];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        wsum += w[u];
+#pragma unroll
+        for (int d = 0; d < kDpl; ++d) acc[d] = __builtin_fmaf(w[u], v[u][d], acc[d]);
+      }
+    }
+    for (; i < a.splits; ++i) {
       const int64_t base = (int64_t(i) * a.num_seqs + s) * a.num_heads + h;
       const float lse = a.part_lse[base];
-      if (lse == neg_inf) continue;
-      const float w = __expf(lse - top);
+      const float w = lse == neg_inf ? 0.0f : __expf(lse - top);
       wsum += w;
 #pragma unroll
-      for (int d = 0; d < kDpl; ++d) acc[d] = __builtin_fmaf(w, a.part_out[base * HD + kDpl * threadIdx.x + d], acc[d]);
+      for (int d = 0; d < kDpl; ++d) acc[d] = __builtin_fmaf(w, a.part_out[base * HD + kDpl * lane + d], acc[d]);
     }
   }
 #pragma unroll
   for (int d = 0; d < kDpl; ++d)
-    store_any(a.out, (s * a.num_heads + h) * HD + kDpl * threadIdx.x + d, a.out_dtype,
-              wsum > 0.0f ? acc[d] / wsum : 0.0f);
+    store_any(a.out, (s * a.num_heads + h) * HD + kDpl * lane + d, a.out_dtype, wsum > 0.0f ? acc[d] / wsum : 0.0f);
 }
 
 template <class C, int HD>

@@ -1,9 +1,11 @@
 """Paged KV-cache writes and decode attention on the GPU against the oracle.
 
 Writes are bit-exact (a copy with one round-to-nearest-even conversion). Attention outputs are
-compared with the oracle's float64 attention over the same cached values, as max |err| / max |ref|:
-the kernel computes in fp32 and rounds once into the query dtype, so the bound is that dtype's
-rounding plus fp32 accumulation: 1e-2 for bf16 outputs, 2e-3 for fp16, 1e-5 for fp32."""
+compared with the oracle's float64 attention over the same cached values, as max |err| / max |ref|.
+The kernel computes scores, softmax and sums in fp32, feeds the probabilities to the P V product
+in the cache dtype (as the reference's probabilities tensor is in the cache dtype) and rounds the
+output once into the query dtype; the bound is the coarser of the two dtypes' rounding: 1e-2 for
+bf16, 2e-3 for fp16."""
 
 from __future__ import annotations
 
@@ -77,7 +79,7 @@ def test_decode_attention_matches_oracle(case, cache_dtype, q_dtype):
                                     cache.value_cache.float().cpu().numpy(), 0, table, np.array(ctx),
                                     cache_dtype=NAMES[cache_dtype])
     got = out.float().cpu().numpy()
-    assert _rel(got, ref) <= TOL[q_dtype], (case, cache_dtype, q_dtype)
+    assert _rel(got, ref) <= max(TOL[q_dtype], TOL[cache_dtype]), (case, cache_dtype, q_dtype)
     for s, c in enumerate(ctx):  # no keys -> exact zeros
         if c == 0:
             assert not got[s].any()
