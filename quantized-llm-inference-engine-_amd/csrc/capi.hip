@@ -328,23 +328,31 @@ int describe_cache(llmopt::KvWriteArgs& a, void* key_cache, void* value_cache, i
   return LLMOPT_OK;
 }
 
-// Context splits for decode attention: enough (sequence, KV head, split) waves to cover the
-// chip (about 1024), at least four 16-token tiles per split.
-void plan_decode_splits(int64_t num_seqs, int64_t kv_heads, int64_t ldb, int64_t block_size, int* splits,
-                        int64_t* tiles_per_split) {
+// Work split for decode attention. Each (sequence, KV head) gets `parts` waves, about 2048 in
+// all (two per SIMD), each with at least four 16-token tiles. Up to 8 of them (4 for groups of 16
+// query heads, whose merge buffer in LDS is larger) form one workgroup and merge in LDS; beyond
+// that the context is cut into `splits` workgroups, at most 64, which a second kernel merges.
+struct DecodePlan {
+  int splits;
+  int waves;
+  int64_t tiles_per_split;
+};
+DecodePlan plan_decode(int64_t num_seqs, int64_t kv_heads, int64_t group, int64_t ldb, int64_t block_size) {
   const int64_t tiles = (ldb * block_size + 15) / 16;
   const int64_t pairs = num_seqs * kv_heads;
-  const int64_t want = pairs > 0 ? (1024 + pairs - 1) / pairs : 1;
-  int64_t per = want > 0 ? (tiles + want - 1) / want : tiles;
-  if (per < 4) per = 4;
+  const int64_t want = pairs > 0 ? (2048 + pairs - 1) / pairs : 1;
+  int64_t parts = (tiles + 3) / 4;
+  if (parts > want) parts = want;
+  if (parts < 1) parts = 1;
+  const int wmax = group >= 16 ? 4 : 8;
+  int waves = 1;
+  while (waves < wmax && waves < parts) waves *= 2;
+  int64_t splits = (parts + waves - 1) / waves;
+  if (splits > 64) splits = 64;
+  int64_t per = (tiles + splits - 1) / splits;
   if (per < 1) per = 1;
-  int64_t n = tiles > 0 ? (tiles + per - 1) / per : 1;
-  if (n > 1024) {  // keep the merge short
-    n = 1024;
-    per = (tiles + n - 1) / n;
-  }
-  *splits = int(n < 1 ? 1 : n);
-  *tiles_per_split = per;
+  splits = tiles > 0 ? (tiles + per - 1) / per : 1;  // no empty split
+  return DecodePlan{int(splits), waves, per};
 }
 
 }  // namespace
@@ -404,11 +412,10 @@ int llmopt_kv_write(void* key_cache, void* value_cache, int cache_dtype, int64_t
 size_t llmopt_paged_attention_workspace(int64_t num_seqs, int64_t num_heads, int64_t kv_heads, int64_t head_dim,
                                         int64_t ldb, int64_t block_size) {
   if (num_seqs <= 0 || num_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || ldb <= 0 || block_size <= 0) return 0;
-  int splits = 1;
-  int64_t per = 1;
-  plan_decode_splits(num_seqs, kv_heads, ldb, block_size, &splits, &per);
-  if (splits <= 1) return 0;
-  return size_t(splits) * size_t(num_seqs) * size_t(num_heads) * size_t(head_dim + 1) * sizeof(float);
+  if (num_heads % kv_heads != 0) return 0;
+  const DecodePlan plan = plan_decode(num_seqs, kv_heads, num_heads / kv_heads, ldb, block_size);
+  if (plan.splits <= 1) return 0;
+  return size_t(plan.splits) * size_t(num_seqs) * size_t(num_heads) * size_t(head_dim + 1) * sizeof(float);
 }
 
 int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_stride, const void* key_cache,
@@ -460,9 +467,9 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
   a.softcap = softcap;
   a.out = out;
   a.out_dtype = q_dtype;
-  int splits = 1;
-  int64_t per = 1;
-  plan_decode_splits(num_seqs, kv_heads, ldb, block_size, &splits, &per);
+  const DecodePlan plan = plan_decode(num_seqs, kv_heads, group, ldb, block_size);
+  int splits = plan.splits;
+  int64_t per = plan.tiles_per_split;
   const size_t need = llmopt_paged_attention_workspace(num_seqs, num_heads, kv_heads, head_dim, ldb, block_size);
   if (splits > 1 && (workspace == nullptr || workspace_bytes < need ||
                      reinterpret_cast<uintptr_t>(workspace) % 16 != 0)) {
@@ -471,6 +478,7 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
   }
   a.splits = splits;
   a.tiles_per_split = per < 1 ? 1 : per;
+  a.waves = plan.waves;
   if (splits > 1) {
     a.part_out = static_cast<float*>(workspace);
     a.part_lse = a.part_out + size_t(splits) * size_t(num_seqs) * size_t(num_heads) * size_t(head_dim);

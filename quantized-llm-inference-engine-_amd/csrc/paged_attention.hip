@@ -15,19 +15,21 @@
 // block_ids[s, t / block_size] at slot t % block_size; it is a key of the query iff
 // t < context_lens[s] and that block id is >= 0.
 //
-// Decode attention, per workgroup = one wave = (sequence, KV head, context split):
-//   * 16-token tiles. Scores S[token][head] = K Q^T * scale on v_mfma_f32_16x16x32: the A operand
-//     is 16 tokens x 32 dims of K (16 bytes per lane, read straight from the cache), the B operand
-//     the group's query heads (columns >= group are zero), HD / 32 MFMAs per tile;
-//   * online softmax per head in fp32 (running max and sum), masked tokens contribute nothing;
-//   * P V on the VALU with lanes over head dims (HD / 64 dims per lane): each token's V row is one
-//     coalesced 256-byte read per wave, the tile's probabilities come from LDS as broadcasts;
-//   * two or three tiles of K and V, and the block ids of as many after them, are in flight
-//     while a tile is computed;
-//   * with several splits each wave writes its normalized partial output and log-sum-exp, and a
-//     merge kernel combines them (the reference's merge_states, paged_attention.py:30-56).
-// Everything is computed in fp32 and rounded once into the query dtype; the reference rounds
-// its scores, probabilities and partial outputs to the cache dtype on the way.
+// Decode attention: one workgroup per (context split, KV head, sequence) with W = 1..8 waves that
+// take its 16-token tiles in turn:
+//   * scores S[token][head] = K Q^T * scale on v_mfma_f32_16x16x32: the A operand is 16 tokens x
+//     32 dims of K (16 bytes per lane, read straight from the cache), the B operand the group's
+//     query heads (columns >= group are zero), HD / 32 MFMAs per tile;
+//   * online softmax per head in fp32 (running max and sum); masked tokens contribute nothing;
+//   * O^T += V^T P on v_mfma_f32_16x16x16, HD / 16 MFMAs per tile: the probabilities, rounded to
+//     the cache dtype as the reference's softmax output is, are the B operand exactly as the
+//     score MFMA left them in the lanes, and each lane reads HD / 8 contiguous bytes of four V rows;
+//   * two tiles of K and V, and the block ids of two more, are in flight while a tile is computed;
+//   * the W waves merge their partial results in LDS; with several splits each workgroup writes
+//     its normalized partial output and log-sum-exp, and a merge kernel combines them (the
+//     reference's merge_states, paged_attention.py:30-56).
+// Scores, softmax and the output accumulate in fp32; the output is rounded once into the query
+// dtype.
 #include "qcommon.hpp"
 #include "qkernels.hpp"
 
@@ -111,46 +113,94 @@ __global__ void __launch_bounds__(256) kv_write_kernel(const KvWriteArgs a) {
 
 // ---- decode attention --------------------------------------------------------------------------
 
-template <class C, int HD, int GQ>
-__global__ void __launch_bounds__(64) paged_decode_kernel(const PagedDecodeArgs a) {
-  using Raw = typename C::raw;
-  constexpr int kNm = HD / 32;  // MFMAs per tile (32 dims each)
-  constexpr int kDpl = HD / 64;  // head dims per lane in P V
-  const int lane = threadIdx.x;
+// v_mfma_f32_16x16x16 (four 16-bit elements per lane) for P V, and the probabilities rounded to
+// the cache dtype as its operand (the reference's softmax output is in that dtype too).
+template <class C>
+struct Mfma16x16;
+template <>
+struct Mfma16x16<ActBf16> {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  __device__ static f32x4 run(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                     0, 0, 0);
+  }
+  __device__ static uint32_t pack(float lo, float hi) {
+    return uint32_t(__builtin_bit_cast(uint16_t, __bf16(lo))) | (uint32_t(__builtin_bit_cast(uint16_t, __bf16(hi))) << 16);
+  }
+};
+template <>
+struct Mfma16x16<ActF16> {
+  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+  __device__ static f32x4 run(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
+                                                 0);
+  }
+  __device__ static uint32_t pack(float lo, float hi) {
+    return uint32_t(__builtin_bit_cast(uint16_t, _Float16(lo))) |
+           (uint32_t(__builtin_bit_cast(uint16_t, _Float16(hi))) << 16);
+  }
+};
+
+// One wave per (context split, KV head, sequence). Lane l: col = l % 16, kb = l / 16.
+//   S = K Q^T on v_mfma_f32_16x16x32: lane l supplies K of token col (dims 32m + 8kb ..) and q of
+//   head col; it receives S[token 4kb + r][head col], r = 0..3.
+//   O^T += V^T P on v_mfma_f32_16x16x16 (M = 16 head dims, K = the 16 tokens, N = 16 heads): the
+//   B operand P[token 4kb + r][head col] is exactly what lane l holds after the softmax, so the
+//   probabilities never leave registers; the A operand is V of tokens 4kb .. 4kb + 3 at dims
+//   (HD/16) col + i for MFMA i, i.e. one contiguous HD/16-dim piece of four V rows per lane.
+//   Lane l accumulates O[head col][dims (HD/16)(4kb + r) + i]: HD/4 contiguous dims of one head,
+//   so the per-head rescale of the online softmax needs no data from other lanes.
+template <class C, int HD, int GQ, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) paged_decode_kernel(const PagedDecodeArgs a) {
+  constexpr int kNm = HD / 32;  // score MFMAs per tile (32 dims each)
+  constexpr int kNv = HD / 16;  // P V MFMAs per tile; also V dims per lane per token
+  constexpr int kVw = kNv / 2;  // 32-bit words of V per lane per token
+  const int lane = threadIdx.x & 63;
+  const int wave = W > 1 ? int(threadIdx.x >> 6) : 0;
   const int col = lane & 15;
   const int kb = lane >> 4;
   const int64_t split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
   const int64_t ctx = a.context_lens[s];
   const int64_t t_begin = split * a.tiles_per_split * 16;
   const int64_t t_end = ctx < t_begin + a.tiles_per_split * 16 ? ctx : t_begin + a.tiles_per_split * 16;
+  // The workgroup's tiles are dealt to its waves in turn: wave w takes tiles w, w + W, ...
+  auto tile_t0 = [&](int64_t j) -> int64_t { return t_begin + 16 * (wave + int64_t(W) * j); };
   const int64_t row_stride = a.kv_heads * HD;  // elements between two slots
-  const uint32_t cache_bytes = uint32_t(a.num_blocks * a.block_size * row_stride * int64_t(sizeof(Raw)));
+  const uint32_t cache_bytes = uint32_t(a.num_blocks * a.block_size * row_stride * 2);
   const auto krs = make_rsrc(a.key_cache, cache_bytes);
   const auto vrs = make_rsrc(a.value_cache, cache_bytes);
-  const uint32_t row_bytes = uint32_t(row_stride * int64_t(sizeof(Raw)));
-  const uint32_t head_off = uint32_t(kvh * HD * int64_t(sizeof(Raw)));
-  const uint32_t v_lane_off = uint32_t(kDpl * lane * int(sizeof(Raw)));
+  const uint32_t row_bytes = uint32_t(row_stride * 2);
+  const uint32_t head_off = uint32_t(kvh * HD * 2);
+  const uint32_t v_lane_off = uint32_t(kNv * col * 2);
   const int32_t* const table = a.block_ids + s * a.ldb;
 
-  __shared__ float p_lds[16][GQ < 4 ? 4 : GQ];  // [token][head]
-  __shared__ float a_lds[GQ < 4 ? 4 : GQ];      // per-head rescale of the running output
-  __shared__ float l_lds[GQ < 4 ? 4 : GQ];
-
-  // Query heads kvh * GQ + col (col < GQ) as the B operand, cast to the cache dtype (q.to(k.dtype)).
+  // Query heads kvh * GQ + col (col < GQ) as the B operand of the scores, cast to the cache dtype
+  // (q.to(k.dtype)); columns >= GQ are zero. One branch on the dtype, then independent loads.
   u32x4 qf[kNm];
   {
     const bool hv = col < GQ;
-    const int64_t h = kvh * GQ + (hv ? col : 0);
+    const int64_t q0 = s * a.q_seq_stride + (kvh * GQ + (hv ? col : 0)) * HD + 8 * kb;
+    float x[kNm][8];
+    if (a.q_dtype == kDtF32) {
+      const float* q = static_cast<const float*>(a.query) + q0;
+#pragma unroll
+      for (int m = 0; m < kNm; ++m)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[m][e] = q[32 * m + e];
+    } else {
+      const uint16_t* q = static_cast<const uint16_t*>(a.query) + q0;
+      const bool half = a.q_dtype == kDtF16;
+#pragma unroll
+      for (int m = 0; m < kNm; ++m)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[m][e] = half ? f16_to_f32(q[32 * m + e]) : bf16_to_f32(q[32 * m + e]);
+    }
 #pragma unroll
     for (int m = 0; m < kNm; ++m) {
       uint32_t w[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t d = 32 * m + 8 * kb + 2 * e;
-        const float x0 = hv ? load_any(a.query, s * a.q_seq_stride + h * HD + d, a.q_dtype) : 0.0f;
-        const float x1 = hv ? load_any(a.query, s * a.q_seq_stride + h * HD + d + 1, a.q_dtype) : 0.0f;
-        w[e] = uint32_t(C::store(x0)) | (uint32_t(C::store(x1)) << 16);
-      }
+      for (int e = 0; e < 4; ++e)
+        w[e] = hv ? uint32_t(C::store(x[m][2 * e])) | (uint32_t(C::store(x[m][2 * e + 1])) << 16) : 0u;
       qf[m] = u32x4{w[0], w[1], w[2], w[3]};
     }
   }
@@ -161,58 +211,68 @@ __global__ void __launch_bounds__(64) paged_decode_kernel(const PagedDecodeArgs 
   const uint32_t ldb32 = uint32_t(a.ldb);
   const uint32_t nblk = uint32_t(a.num_blocks);
   const uint32_t t_end32 = uint32_t(t_end > 0 ? t_end : 0);
-  auto fetch_row = [&](int64_t t0) -> int32_t {
+  // The table entry is loaded a full ring turn before its slot row is needed: fetch_block
+  // issues the load (in order, like the K/V loads, so that it stays where it is issued) and
+  // row_of turns the entry into a slot row when the tile's K/V loads are issued.
+  const auto trs = make_rsrc(table, uint32_t(a.ldb * 4));
+  auto fetch_block = [&](int64_t t0) -> int32_t {
+    const uint32_t bi = (uint32_t(t0) + uint32_t(col)) / bsz;
+    return int32_t(__builtin_amdgcn_raw_buffer_load_b32(trs, (bi < ldb32 ? bi : 0u) * 4u, 0, kLoadInOrder));
+  };
+  auto row_of = [&](int64_t t0, int32_t block) -> int32_t {
     const uint32_t t = uint32_t(t0) + uint32_t(col);
     const uint32_t bi = t / bsz;
-    int32_t block = -1;
-    if (t < t_end32 && bi < ldb32) block = table[bi];  // past the row: no key
-    const bool ok = block >= 0 && uint32_t(block) < nblk;
+    const bool ok = t < t_end32 && bi < ldb32 && block >= 0 && uint32_t(block) < nblk;  // else no key
     return ok ? int32_t(uint32_t(block) * bsz + (t - bi * bsz)) : -1;
   };
-  // K of token t0 + col (dims 8kb .. of each 32-dim slice) and this lane's dims of V for all 16
-  // tokens (slot rows broadcast with readlane, so each V row address is a scalar); masked tokens
-  // read slot row 0. Buffer loads with 32-bit offsets (the host keeps a layer's cache under
-  // 2 GiB), marked to stay in program order so that the ring below keeps them in flight.
-  auto fetch_kv = [&](int32_t row, u32x4* kf, uint32_t* vf, uint32_t& valid_bits) {
+  // K of token t0 + col (masked tokens read slot row 0; their scores are dropped) and V of tokens
+  // t0 + 4kb .. t0 + 4kb + 3, whose slot rows come from the lanes that computed them. A masked
+  // token's V is read at an offset past the cache (which the host keeps under 2 GiB), where
+  // buffer loads return zeros, so its product with a zero probability stays zero whatever the
+  // slot holds. Loads are marked to stay in program order so that the ring keeps them in flight.
+  constexpr uint32_t kPastCache = 0x80000000u;
+  auto fetch_kv = [&](int32_t row, u32x4* kf, uint32_t (*vf)[kVw], uint32_t& valid_bits) {
     valid_bits = uint32_t(__builtin_amdgcn_ballot_w64(row >= 0) & 0xFFFFu);
     const uint32_t r_own = uint32_t(row >= 0 ? row : 0);
 #pragma unroll
-    for (int m = 0; m < kNm; ++m)
-      kf[m] = buf_load16(krs, (r_own * row_bytes) + uint32_t(2 * (32 * m + 8 * kb)), head_off);
-    const int32_t row0 = row >= 0 ? row : 0;
+    for (int m = 0; m < kNm; ++m) kf[m] = buf_load16(krs, r_own * row_bytes + uint32_t(2 * (32 * m + 8 * kb)), head_off);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const uint32_t r = uint32_t(__builtin_amdgcn_readlane(row0, j));
-      if constexpr (kDpl == 2)
-        vf[j] = __builtin_amdgcn_raw_buffer_load_b32(vrs, v_lane_off, int(r * row_bytes + head_off), kLoadInOrder);
-      else
-        vf[j] = uint32_t(__builtin_amdgcn_raw_buffer_load_b16(vrs, v_lane_off, int(r * row_bytes + head_off),
-                                                              kLoadInOrder));
+    for (int k = 0; k < 4; ++k) {
+      const int32_t rv = __shfl(row, 4 * kb + k, 64);
+      const uint32_t off = rv >= 0 ? uint32_t(rv) * row_bytes + v_lane_off : kPastCache;
+      if constexpr (kVw == 4) {
+        const u32x4 w = buf_load16(vrs, off, head_off);
+        vf[k][0] = w.x, vf[k][1] = w.y, vf[k][2] = w.z, vf[k][3] = w.w;
+      } else {
+        const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrs, int(off), int(head_off), kLoadInOrder));
+        vf[k][0] = w.x, vf[k][1] = w.y;
+      }
     }
   };
 
   const float neg_inf = -__int_as_float(0x7F800000);
-  float m_run = neg_inf, l_run = 0.0f;  // for head `col`, replicated over the four lane rows
-  float o[GQ][kDpl];
+  float m_run = neg_inf;  // running max of head col (the same on the four lanes of a column)
+  float l_run = 0.0f;     // this lane's share of the running sum of head col
+  f32x4 o[kNv];
 #pragma unroll
-  for (int h = 0; h < GQ; ++h)
-#pragma unroll
-    for (int d = 0; d < kDpl; ++d) o[h][d] = 0.0f;
+  for (int i = 0; i < kNv; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // One tile: scores on the MFMA, online softmax, P V on the VALU.
-  auto compute = [&](const u32x4* kf, const uint32_t* vf, uint32_t bits) {
+  // One tile: scores, online softmax, P V, all on 64 lanes without LDS.
+  auto compute = [&](const u32x4* kf, const uint32_t (*vf)[kVw], uint32_t bits) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < kNm; ++m) acc = Mfma16x32<C>::run(kf[m], qf[m], acc);
-
-    // Rows 4kb .. 4kb + 3 of the tile, column = head `col`.
     float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = acc[r] * a.scale;
+    if (a.softcap > 0.0f) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = tanhf(sc[r] / a.softcap) * a.softcap;
+    }
     float tmax = neg_inf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float x = acc[r] * a.scale;
-      if (a.softcap > 0.0f) x = tanhf(x / a.softcap) * a.softcap;
-      sc[r] = ((bits >> (4 * kb + r)) & 1u) ? x : neg_inf;
+      sc[r] = ((bits >> (4 * kb + r)) & 1u) ? sc[r] : neg_inf;
       tmax = fmaxf(tmax, sc[r]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -220,76 +280,56 @@ __global__ void __launch_bounds__(64) paged_decode_kernel(const PagedDecodeArgs 
     const float m_new = fmaxf(m_run, tmax);
     const bool live = m_new != neg_inf;
     const float alpha = live ? __expf(m_run - m_new) : 1.0f;
-    float psum = 0.0f;
+    float p[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float p = live ? __expf(sc[r] - m_new) : 0.0f;
-      psum += p;
-      if (col < GQ) p_lds[4 * kb + r][col] = p;
-    }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l_run = alpha * l_run + psum;
+    for (int r = 0; r < 4; ++r) p[r] = live ? __expf(sc[r] - m_new) : 0.0f;
+    l_run = alpha * l_run + ((p[0] + p[1]) + (p[2] + p[3]));
     m_run = m_new;
-    if (lane < GQ) a_lds[lane] = alpha;
-    __syncthreads();
-
+    // Rescale only when some head's max moved (alpha is exactly 1 otherwise).
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) {
-      const float al = a_lds[h];
-#pragma unroll
-      for (int d = 0; d < kDpl; ++d) o[h][d] *= al;
+      for (int i = 0; i < kNv; ++i) o[i] *= alpha;
     }
+    const u32x2 pb = {Mfma16x16<C>::pack(p[0], p[1]), Mfma16x16<C>::pack(p[2], p[3])};
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float v[kDpl];
-      if constexpr (kDpl == 2) {
-        v[0] = C::load(Raw(vf[j] & 0xFFFFu));
-        v[1] = C::load(Raw(vf[j] >> 16));
-      } else {
-        v[0] = C::load(Raw(vf[j]));
-      }
-      if (!((bits >> j) & 1u)) {  // masked token: its slot may hold anything
-#pragma unroll
-        for (int d = 0; d < kDpl; ++d) v[d] = 0.0f;
-      }
-#pragma unroll
-      for (int h = 0; h < GQ; ++h) {
-        const float p = p_lds[j][h];
-#pragma unroll
-        for (int d = 0; d < kDpl; ++d) o[h][d] = __builtin_fmaf(p, v[d], o[h][d]);
-      }
+    for (int i = 0; i < kNv; ++i) {
+      // Dim (HD/16) col + i of tokens 4kb + 0..3: half i % 2 of word i / 2 of each V piece.
+      const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+      const u32x2 va = {__builtin_amdgcn_perm(vf[1][i >> 1], vf[0][i >> 1], sel),
+                        __builtin_amdgcn_perm(vf[3][i >> 1], vf[2][i >> 1], sel)};
+      o[i] = Mfma16x16<C>::run(va, pb, o[i]);
     }
-    __syncthreads();
   };
 
-  // A ring of kDepth tiles in flight. Slot u holds tile g + u of the current group; after it is
-  // computed it is refilled with tile g + u + kDepth, whose slot rows were loaded kDepth tiles
-  // earlier (rows[u]); the rows for the refill after that are loaded at the same time. The main
-  // loop runs whole groups with unconditional loads (past the last tile they read slot row 0 and
-  // are never used), so the loads keep one static order; the last partial group has no refills.
-  constexpr int kDepth = GQ >= 16 ? 1 : GQ >= 8 ? 2 : 3;  // registers: larger groups keep more accumulators
+  // A ring of kDepth tiles in flight. Slot u holds the wave's tile g + u of the current group;
+  // after it is computed it is refilled with tile g + u + kDepth, whose table entries were loaded
+  // kDepth tiles earlier (rows[u]); the entries for the refill after that are loaded at the same
+  // time. The main loop runs whole groups with unconditional loads (past the last tile they read
+  // slot row 0 or nothing and are never used), so the loads keep one static order; the last
+  // partial group has no refills.
+  constexpr int kDepth = 2;
   u32x4 kf[kDepth][kNm];
-  uint32_t vf[kDepth][16];
+  uint32_t vf[kDepth][4][kVw];
   uint32_t bits[kDepth];
   int32_t rows[kDepth];
-  const int64_t n_tiles = t_end > t_begin ? (t_end - t_begin + 15) / 16 : 0;
+  const int64_t n_all = t_end > t_begin ? (t_end - t_begin + 15) / 16 : 0;
+  const int64_t n_tiles = n_all > wave ? (n_all - wave + W - 1) / W : 0;
   if (n_tiles > 0) {
     int32_t first[kDepth];
 #pragma unroll
-    for (int u = 0; u < kDepth; ++u) first[u] = fetch_row(t_begin + 16 * u);
+    for (int u = 0; u < kDepth; ++u) first[u] = fetch_block(tile_t0(u));
 #pragma unroll
-    for (int u = 0; u < kDepth; ++u) rows[u] = fetch_row(t_begin + 16 * (u + kDepth));
+    for (int u = 0; u < kDepth; ++u) rows[u] = fetch_block(tile_t0(u + kDepth));
 #pragma unroll
-    for (int u = 0; u < kDepth; ++u) fetch_kv(first[u], kf[u], vf[u], bits[u]);
+    for (int u = 0; u < kDepth; ++u) fetch_kv(row_of(tile_t0(u), first[u]), kf[u], vf[u], bits[u]);
   }
   int64_t g = 0;
   for (; g + kDepth <= n_tiles; g += kDepth) {
 #pragma unroll
     for (int u = 0; u < kDepth; ++u) {
       compute(kf[u], vf[u], bits[u]);
-      const int32_t next = rows[u];
-      rows[u] = fetch_row(t_begin + 16 * (g + u + 2 * kDepth));
+      const int32_t next = row_of(tile_t0(g + u + kDepth), rows[u]);
+      rows[u] = fetch_block(tile_t0(g + u + 2 * kDepth));
       fetch_kv(next, kf[u], vf[u], bits[u]);
     }
   }
@@ -297,30 +337,91 @@ __global__ void __launch_bounds__(64) paged_decode_kernel(const PagedDecodeArgs 
   for (int u = 0; u < kDepth; ++u)
     if (g + u < n_tiles) compute(kf[u], vf[u], bits[u]);
 
-  // Normalize; one split writes the output, several write partials for the merge.
-  if (lane < GQ) l_lds[lane] = l_run;
-  __syncthreads();
+  // Lane l holds head col, dims (HD/4) kb + (HD/16) r + i, unnormalized, with the wave's running
+  // max m_run and (after this sum) its running sum l_run of that head.
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
   const int64_t h0 = kvh * GQ;
-  if (a.splits == 1) {
+  const int64_t d0 = (HD / 4) * kb;
+  if constexpr (W == 1) {
+    if (col >= GQ) return;
+    const int64_t h = h0 + col;
+    float v[4][kNv];
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) {
-      const float l = l_lds[h];
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int d = 0; d < kDpl; ++d)
-        store_any(a.out, (s * a.num_heads + h0 + h) * HD + kDpl * lane + d, a.out_dtype,
-                  l > 0.0f ? o[h][d] / l : 0.0f);
+      for (int i = 0; i < kNv; ++i) v[r][i] = l_run > 0.0f ? o[i][r] / l_run : 0.0f;
+    if (a.splits == 1) {
+      const int64_t base = (s * a.num_heads + h) * HD + d0;
+      if (a.out_dtype == kDtF32) {
+        float* out = static_cast<float*>(a.out) + base;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int i = 0; i < kNv; ++i) out[kNv * r + i] = v[r][i];
+      } else {
+        uint16_t* out = static_cast<uint16_t*>(a.out) + base;
+        const bool half = a.out_dtype == kDtF16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int i = 0; i < kNv; ++i) out[kNv * r + i] = half ? f32_to_f16_rne(v[r][i]) : f32_to_bf16_rne(v[r][i]);
+      }
+      return;
     }
-    return;
-  }
-  const int64_t base = split * a.num_seqs + s;
+    const int64_t base = (split * a.num_seqs + s) * a.num_heads + h;
+    float* part = a.part_out + base * HD + d0;
 #pragma unroll
-  for (int h = 0; h < GQ; ++h) {
-    const float l = l_lds[h];
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int d = 0; d < kDpl; ++d)
-      a.part_out[((base * a.num_heads + h0 + h) * HD) + kDpl * lane + d] = l > 0.0f ? o[h][d] / l : 0.0f;
+      for (int i = 0; i < kNv; ++i) part[kNv * r + i] = v[r][i];
+    if (kb == 0) a.part_lse[base] = l_run > 0.0f ? m_run + __logf(l_run) : neg_inf;
+  } else {
+    // Merge the W waves in LDS (the reference's merge_states over W parts): weights
+    // exp(m_w - max m), then one (head, dim) element per thread.
+    __shared__ float m_lds[W][GQ];
+    __shared__ float l_lds[W][GQ];
+    __shared__ float o_lds[W][GQ][HD];
+    if (col < GQ) {
+      if (kb == 0) m_lds[wave][col] = m_run, l_lds[wave][col] = l_run;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < kNv; ++i) o_lds[wave][col][d0 + kNv * r + i] = o[i][r];
+    }
+    __syncthreads();
+    for (int e = int(threadIdx.x); e < GQ * HD; e += 64 * W) {
+      const int hh = e / HD, d = e % HD;
+      float top = neg_inf;
+#pragma unroll
+      for (int w = 0; w < W; ++w) top = fmaxf(top, m_lds[w][hh]);
+      float lsum = 0.0f, acc = 0.0f;
+      if (top != neg_inf) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float mw = m_lds[w][hh];
+          const float f = mw == neg_inf ? 0.0f : __expf(mw - top);
+          lsum = __builtin_fmaf(f, l_lds[w][hh], lsum);
+          acc = __builtin_fmaf(f, o_lds[w][hh][d], acc);
+        }
+      }
+      const float val = lsum > 0.0f ? acc / lsum : 0.0f;
+      const int64_t h = h0 + hh;
+      if (a.splits == 1) {
+        const int64_t i = (s * a.num_heads + h) * HD + d;
+        if (a.out_dtype == kDtF32)
+          static_cast<float*>(a.out)[i] = val;
+        else if (a.out_dtype == kDtF16)
+          static_cast<uint16_t*>(a.out)[i] = f32_to_f16_rne(val);
+        else
+          static_cast<uint16_t*>(a.out)[i] = f32_to_bf16_rne(val);
+      } else {
+        const int64_t base = (split * a.num_seqs + s) * a.num_heads + h;
+        a.part_out[base * HD + d] = val;
+        if (d == 0) a.part_lse[base] = lsum > 0.0f ? top + __logf(lsum) : neg_inf;
+      }
+    }
   }
-  if (lane < GQ) a.part_lse[base * a.num_heads + h0 + lane] = l_run > 0.0f ? m_run + __logf(l_run) : neg_inf;
 }
 
 // Combine the splits of one (sequence, head): weights exp(lse_i - max lse). The lanes first
@@ -372,16 +473,29 @@ __global__ void __launch_bounds__(64) paged_merge_kernel(const PagedDecodeArgs a
     store_any(a.out, (s * a.num_heads + h) * HD + kDpl * lane + d, a.out_dtype, wsum > 0.0f ? acc[d] / wsum : 0.0f);
 }
 
+template <class C, int HD, int GQ>
+void launch_decode_group(const PagedDecodeArgs& a, dim3 grid, hipStream_t stream) {
+  switch (a.waves) {
+    case 1: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 1>), grid, dim3(64), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 2>), grid, dim3(128), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 4>), grid, dim3(256), 0, stream, a); break;
+    default:
+      if constexpr (GQ < 16) hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 8>), grid, dim3(512), 0, stream, a);
+      break;
+  }
+}
+
 template <class C, int HD>
 hipError_t launch_decode_hd(const PagedDecodeArgs& a, hipStream_t stream) {
   const dim3 grid(unsigned(a.splits), unsigned(a.kv_heads), unsigned(a.num_seqs));
   const int g = int(a.num_heads / a.kv_heads);
+  if (a.waves != 1 && a.waves != 2 && a.waves != 4 && !(a.waves == 8 && g < 16)) return hipErrorInvalidValue;
   switch (g) {
-    case 1: hipLaunchKernelGGL((paged_decode_kernel<C, HD, 1>), grid, dim3(64), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((paged_decode_kernel<C, HD, 2>), grid, dim3(64), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((paged_decode_kernel<C, HD, 4>), grid, dim3(64), 0, stream, a); break;
-    case 8: hipLaunchKernelGGL((paged_decode_kernel<C, HD, 8>), grid, dim3(64), 0, stream, a); break;
-    case 16: hipLaunchKernelGGL((paged_decode_kernel<C, HD, 16>), grid, dim3(64), 0, stream, a); break;
+    case 1: launch_decode_group<C, HD, 1>(a, grid, stream); break;
+    case 2: launch_decode_group<C, HD, 2>(a, grid, stream); break;
+    case 4: launch_decode_group<C, HD, 4>(a, grid, stream); break;
+    case 8: launch_decode_group<C, HD, 8>(a, grid, stream); break;
+    case 16: launch_decode_group<C, HD, 16>(a, grid, stream); break;
     default: return hipErrorInvalidValue;
   }
   if (a.splits > 1)

@@ -91,7 +91,8 @@ struct PagedDecodeArgs {
   float* part_out;  // [splits, num_seqs, num_heads, head_dim]
   float* part_lse;  // [splits, num_seqs, num_heads]
   int splits;
-  int64_t tiles_per_split;  // 16-token tiles per split
+  int64_t tiles_per_split;  // 16-token tiles per split (per workgroup)
+  int waves;                // waves per workgroup: 1, 2, 4 or 8 (8 only below 16 heads per KV head)
 };
 hipError_t launch_paged_decode(const PagedDecodeArgs& a, hipStream_t stream);
 hipError_t launch_linear_generic(const LinearArgs& a, hipStream_t stream);
