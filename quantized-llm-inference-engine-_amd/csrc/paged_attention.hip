@@ -212,12 +212,12 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   const uint32_t nblk = uint32_t(a.num_blocks);
   const uint32_t t_end32 = uint32_t(t_end > 0 ? t_end : 0);
   // The table entry is loaded a full ring turn before its slot row is needed: fetch_block
-  // issues the load (in order, like the K/V loads, so that it stays where it is issued) and
-  // row_of turns the entry into a slot row when the tile's K/V loads are issued.
+  // issues the load and row_of turns the entry into a slot row when the tile's K/V loads are
+  // issued.
   const auto trs = make_rsrc(table, uint32_t(a.ldb * 4));
   auto fetch_block = [&](int64_t t0) -> int32_t {
     const uint32_t bi = (uint32_t(t0) + uint32_t(col)) / bsz;
-    return int32_t(__builtin_amdgcn_raw_buffer_load_b32(trs, (bi < ldb32 ? bi : 0u) * 4u, 0, kLoadInOrder));
+    return int32_t(__builtin_amdgcn_raw_buffer_load_b32(trs, (bi < ldb32 ? bi : 0u) * 4u, 0, kLoadPolicy));
   };
   auto row_of = [&](int64_t t0, int32_t block) -> int32_t {
     const uint32_t t = uint32_t(t0) + uint32_t(col);
@@ -229,7 +229,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   // t0 + 4kb .. t0 + 4kb + 3, whose slot rows come from the lanes that computed them. A masked
   // token's V is read at an offset past the cache (which the host keeps under 2 GiB), where
   // buffer loads return zeros, so its product with a zero probability stays zero whatever the
-  // slot holds. Loads are marked to stay in program order so that the ring keeps them in flight.
+  // slot holds.
   constexpr uint32_t kPastCache = 0x80000000u;
   auto fetch_kv = [&](int32_t row, u32x4* kf, uint32_t (*vf)[kVw], uint32_t& valid_bits) {
     valid_bits = uint32_t(__builtin_amdgcn_ballot_w64(row >= 0) & 0xFFFFu);
@@ -244,7 +244,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
         const u32x4 w = buf_load16(vrs, off, head_off);
         vf[k][0] = w.x, vf[k][1] = w.y, vf[k][2] = w.z, vf[k][3] = w.w;
       } else {
-        const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrs, int(off), int(head_off), kLoadInOrder));
+        const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrs, int(off), int(head_off), kLoadPolicy));
         vf[k][0] = w.x, vf[k][1] = w.y;
       }
     }

@@ -114,15 +114,15 @@ __device__ __forceinline__ float dequant_exact(float q, float z, float s) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, int(bytes), 0x00020000);
 }
-// Streaming loads are marked volatile (bit 31 of the cache-policy operand, a compiler-only flag):
-// they then stay in program order, where a prefetch ring puts them, instead of being sunk next
-// to their first use, which would expose the full memory latency on every use.
-constexpr int kLoadInOrder = int(0x80000000u);
+// Loads use the default cache policy. Marking them volatile (bit 31 of the policy operand) would
+// pin them in program order, but the backend then also makes them system-coherent (sc0 sc1),
+// which cost 5-25% of the bandwidth of these streams on MI355X; the prefetch rings work without it.
+constexpr int kLoadPolicy = 0;
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), kLoadInOrder);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), kLoadPolicy);
 }
 __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(voff), int(soff), kLoadInOrder));
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(voff), int(soff), kLoadPolicy));
 }
 
 // Fast exact division of small non-negative integers by a runtime divisor (< 2^16, dividend
