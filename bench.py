@@ -81,6 +81,7 @@ def parse_args() -> argparse.Namespace:
                    help="also time the down projection at 8/4/2 bits, M in {1, 32, 2048}")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
+    p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Llama-3-8B generation")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--pmc-workload", action="store_true", help="only the dominant kernel + a copy")
     p.add_argument("--traffic-from", type=str, default=None, help="rocprofv3 --pmc output dir")
@@ -292,6 +293,8 @@ def main() -> int:
     result["dequant"] = dequant_rate(torch, ops, rotations)
     result["quantize"] = quantize_rate(torch, ops)
     result["attention"] = attention_rates(torch)
+    if not args.no_e2e:
+        result["e2e"] = end_to_end(torch)
     if not args.no_prefill:
         result["prefill"] = prefill(torch, ops, rotations)
     if args.sweep:
@@ -331,6 +334,41 @@ def prefill(torch, ops, rotations):
     return {"kernel": f"quantized-linear prefill, gate_up M={m} (K 4096, N 28672)", "mean_launch_us": round(us, 2),
             "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "bound": "mfma", "dense_comparator": dense}
+
+
+def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128):
+    """Llama-3-8B (random init, every decoder linear W4 g128 asymmetric RTN, fused q/k/v and
+    gate/up), 32 seeded prompts of 512 tokens, then 128 greedy steps through the paged cache
+    (block 16). Prefill: one forward over all prompts (the reference's torch sequence for the
+    prefill attention). Decode: each step one HIP-graph replay; tokens/s over steps 2..127."""
+    from llmopt.model import GreedyGenerator, ModelConfig, random_quantized_model
+
+    cfg = ModelConfig.llama3_8b()
+    t0 = time.perf_counter()
+    model = random_quantized_model(cfg, device="cuda:0", dtype=torch.bfloat16, seed=0)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    prompts = torch.randint(0, cfg.vocab_size, (seqs, prompt_len), generator=torch.Generator().manual_seed(1))
+    gen = GreedyGenerator(model, block_size=16)
+    gen.generate(prompts[:, :32], 4)  # warm-up: first calls, graph machinery
+    res = gen.generate(prompts, steps)
+    step_ms = res.decode_seconds / (steps - 2) * 1e3
+    packed = sum(b.numel() * b.element_size() for n, b in model.named_buffers() if "rotary" not in n)
+    out = {
+        "workload": f"llama3-8b, {seqs} prompts x {prompt_len} tokens, then {steps} greedy steps, W4 g128 asym "
+                    "RTN linears (fused qkv and gate_up), bf16, paged KV block 16",
+        "decode_tokens_per_s": round(res.decode_tokens_per_second, 1),
+        "decode_step_ms": round(step_ms, 3),
+        "prefill_tokens_per_s": round(seqs * prompt_len / res.prefill_seconds, 1),
+        "prefill_ms": round(res.prefill_seconds * 1e3, 1),
+        "packed_linear_bytes": packed,
+        "model_build_s": round(build_s, 2),
+    }
+    print(f"# e2e llama3-8b: prefill {out['prefill_ms']} ms ({out['prefill_tokens_per_s']:.0f} tok/s), decode "
+          f"{step_ms:.2f} ms/step ({out['decode_tokens_per_s']:.0f} tok/s)", file=sys.stderr, flush=True)
+    del model, gen, res
+    torch.cuda.empty_cache()
+    return out
 
 
 def dequant_rate(torch, ops, rotations):
