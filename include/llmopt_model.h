@@ -1,0 +1,49 @@
+/*
+ * llmopt_model.h -- C ABI of the decoder's elementwise steps in libllmopt_qlinear.so (gfx950):
+ * RMSNorm with an optional fused residual add, and the rotary embedding of q and k. Same
+ * conventions as llmopt_qlinear.h: device pointers owned by the caller, `stream` a hipStream_t
+ * as void*, LLMOPT_OK or a negative LLMOPT_ERR_* code with the message in llmopt_q_last_error(),
+ * dtype codes LLMOPT_DTYPE_* (F16 or BF16 here; other dtypes return LLMOPT_ERR_UNSUPPORTED and
+ * the Python layer runs the reference's torch sequence).
+ */
+#ifndef LLMOPT_MODEL_H_
+#define LLMOPT_MODEL_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * y = x * rsqrt(mean(x^2) + eps) * weight, per row, computed in fp32 and rounded once to dtype.
+ * Replaces RMSNorm.forward (src/llmopt/model/layers.py:14-31). With residual != NULL the input
+ * is first h = residual + x, rounded to dtype (the residual add of DecoderLayer.forward,
+ * layers.py:185-195), and h is written to h_out. x, residual, h_out, y: [rows, hidden] with row
+ * strides ldx, ldr, ldh, ldy elements; weight: [hidden] of dtype. Needs hidden % 8 == 0, row
+ * strides % 8 == 0 and 16-byte aligned pointers (else LLMOPT_ERR_UNSUPPORTED).
+ */
+int llmopt_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr, void* h_out, int64_t ldh,
+                   const void* weight, void* y, int64_t ldy, int64_t rows, int64_t hidden, float eps, int dtype,
+                   void* stream);
+
+/*
+ * Rotary embedding of q and k at positions[t] (int64): out = x * cos + rotate_half(x) * sin,
+ * rotate_half([a, b]) = [-b, a] over the two halves of each head; cos_table / sin_table are the
+ * fp32 [table_rows, head_dim] tables, cast to dtype as the reference casts them. Replaces
+ * apply_rotary_pos_emb with RotaryEmbedding.forward (src/llmopt/model/rotary.py:23-45,85-102);
+ * every product and sum is rounded to dtype as torch rounds it, so the result is identical.
+ * q: [tokens, heads, head_dim] with token stride ldq; k: [tokens, kv_heads, head_dim] with token
+ * stride ldk; q_out, k_out: contiguous. Positions outside [0, table_rows) are clamped (the
+ * Python layer raises for them first, as the reference does).
+ */
+int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, void* q_out, void* k_out,
+                const int64_t* positions, const float* cos_table, const float* sin_table, int64_t table_rows,
+                int64_t tokens, int64_t heads, int64_t kv_heads, int64_t head_dim, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif  // LLMOPT_MODEL_H_

@@ -11,6 +11,7 @@
 #include <string>
 
 #include "../../include/llmopt_attention.h"
+#include "../../include/llmopt_model.h"
 #include "../../include/llmopt_qlinear.h"
 #include "qcommon.hpp"
 #include "qkernels.hpp"
@@ -484,6 +485,69 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
     a.part_lse = a.part_out + size_t(splits) * size_t(num_seqs) * size_t(num_heads) * size_t(head_dim);
   }
   return hip_status(llmopt::launch_paged_decode(a, static_cast<hipStream_t>(stream)), "paged attention launch");
+}
+
+int llmopt_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr, void* h_out, int64_t ldh,
+                   const void* weight, void* y, int64_t ldy, int64_t rows, int64_t hidden, float eps, int dtype,
+                   void* stream) {
+  if (dtype != LLMOPT_DTYPE_BF16 && dtype != LLMOPT_DTYPE_F16)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "rmsnorm kernel: dtype %d (bf16 and fp16 only)", dtype);
+  if (rows < 0 || hidden < 1 || rows > 0x7FFFFFFF) return fail(LLMOPT_ERR_INVALID_ARG, "bad rmsnorm shape");
+  if (rows == 0) return LLMOPT_OK;
+  if (!x || !weight || !y || (residual && !h_out)) return fail(LLMOPT_ERR_INVALID_ARG, "null rmsnorm pointer");
+  if (ldx < hidden || ldy < hidden || (residual && (ldr < hidden || ldh < hidden)))
+    return fail(LLMOPT_ERR_INVALID_ARG, "rmsnorm row stride below hidden=%lld", (long long)hidden);
+  auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (hidden % 8 || ldx % 8 || ldy % 8 || (residual && (ldr % 8 || ldh % 8)) || !aligned(x) || !aligned(y) ||
+      !aligned(weight) || (residual && (!aligned(residual) || !aligned(h_out))))
+    return fail(LLMOPT_ERR_UNSUPPORTED, "rmsnorm kernel: needs hidden and row strides % 8 == 0, 16-byte aligned rows");
+  llmopt::RmsNormArgs a{};
+  a.x = x;
+  a.residual = residual;
+  a.h_out = h_out;
+  a.weight = weight;
+  a.y = y;
+  a.rows = rows;
+  a.hidden = hidden;
+  a.ldx = ldx;
+  a.ldr = ldr;
+  a.ldh = ldh;
+  a.ldy = ldy;
+  a.eps = eps;
+  a.dtype = dtype;
+  return hip_status(llmopt::launch_rmsnorm(a, static_cast<hipStream_t>(stream)), "rmsnorm launch");
+}
+
+int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, void* q_out, void* k_out,
+                const int64_t* positions, const float* cos_table, const float* sin_table, int64_t table_rows,
+                int64_t tokens, int64_t heads, int64_t kv_heads, int64_t head_dim, int dtype, void* stream) {
+  if (dtype != LLMOPT_DTYPE_BF16 && dtype != LLMOPT_DTYPE_F16)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "rope kernel: dtype %d (bf16 and fp16 only)", dtype);
+  if (tokens < 0 || tokens > 0x7FFFFFFF || heads < 1 || kv_heads < 0 || head_dim < 2 || head_dim % 2 ||
+      table_rows < 1)
+    return fail(LLMOPT_ERR_INVALID_ARG, "bad rope shape");
+  if (tokens == 0) return LLMOPT_OK;
+  if (!q || !q_out || !positions || !cos_table || !sin_table || (kv_heads > 0 && (!k || !k_out)))
+    return fail(LLMOPT_ERR_INVALID_ARG, "null rope pointer");
+  if (ldq < heads * head_dim || (kv_heads > 0 && ldk < kv_heads * head_dim))
+    return fail(LLMOPT_ERR_INVALID_ARG, "rope token stride below heads x head_dim");
+  llmopt::RopeArgs a{};
+  a.q = q;
+  a.k = k;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.positions = positions;
+  a.cos_table = cos_table;
+  a.sin_table = sin_table;
+  a.table_rows = table_rows;
+  a.tokens = tokens;
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.ldq = ldq;
+  a.ldk = ldk;
+  a.dtype = dtype;
+  return hip_status(llmopt::launch_rope(a, static_cast<hipStream_t>(stream)), "rope launch");
 }
 
 }  // extern "C"

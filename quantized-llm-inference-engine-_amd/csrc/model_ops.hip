@@ -1,0 +1,134 @@
+// The decoder's per-token elementwise steps as single kernels, with the reference's roundings.
+//
+// Replaces, on HIP devices:
+//   * RMSNorm.forward (src/llmopt/model/layers.py:14-31): y = x * rsqrt(mean(x^2) + eps) * w in
+//     fp32, rounded once to the activation dtype -- and, fused in front of it, the residual add
+//     of DecoderLayer.forward (layers.py:185-195), h = x + r rounded to the activation dtype as
+//     torch's bf16/fp16 add rounds it, with h written out as the new residual stream;
+//   * apply_rotary_pos_emb with RotaryEmbedding.forward (src/llmopt/model/rotary.py:23-45,
+//     85-102) for q and k together: the fp32 cos/sin tables cast to the activation dtype, then
+//     q * cos + rotate_half(q) * sin with each product and the sum rounded to the activation
+//     dtype, as torch evaluates the expression op by op -- so the result is bit-identical.
+// torch runs these as about 8 (norm) and 14 (rotary) separate kernels per layer and step.
+#include "qcommon.hpp"
+#include "qkernels.hpp"
+
+namespace llmopt {
+namespace {
+
+template <class Act>
+__device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = Act::load(typename Act::raw(w[i] & 0xFFFFu));
+    f[2 * i + 1] = Act::load(typename Act::raw(w[i] >> 16));
+  }
+}
+
+template <class Act>
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = uint32_t(Act::store(f[2 * i])) | (uint32_t(Act::store(f[2 * i + 1])) << 16);
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// One workgroup of 256 threads per row; 16-byte accesses (the host checks hidden % 8 == 0 and
+// 16-byte aligned rows). Pass 1 forms h (with the residual, if any), stores it and sums h^2;
+// pass 2 re-reads h (from L2) and normalizes.
+template <class Act>
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const RmsNormArgs a) {
+  using Raw = typename Act::raw;
+  const int64_t row = blockIdx.x;
+  const Raw* x = static_cast<const Raw*>(a.x) + row * a.ldx;
+  const Raw* r = a.residual ? static_cast<const Raw*>(a.residual) + row * a.ldr : nullptr;
+  Raw* h_out = a.h_out ? static_cast<Raw*>(a.h_out) + row * a.ldh : nullptr;
+  Raw* y = static_cast<Raw*>(a.y) + row * a.ldy;
+  const Raw* w = static_cast<const Raw*>(a.weight);
+  const int tid = threadIdx.x;
+
+  float ss = 0.0f;
+  for (int64_t e = int64_t(tid) * 8; e < a.hidden; e += 256 * 8) {
+    float h[8];
+    unpack8<Act>(*reinterpret_cast<const u32x4*>(x + e), h);
+    if (r) {
+      float rv[8];
+      unpack8<Act>(*reinterpret_cast<const u32x4*>(r + e), rv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) h[i] = Act::load(Act::store(rv[i] + h[i]));
+      *reinterpret_cast<u32x4*>(h_out + e) = pack8<Act>(h);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(h[i], h[i], ss);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  __shared__ float part[4];
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  const float total = (part[0] + part[1]) + (part[2] + part[3]);
+  const float inv = __frsqrt_rn(total / float(a.hidden) + a.eps);
+
+  const Raw* src = r ? h_out : x;
+  for (int64_t e = int64_t(tid) * 8; e < a.hidden; e += 256 * 8) {
+    float h[8], wv[8], o[8];
+    unpack8<Act>(*reinterpret_cast<const u32x4*>(src + e), h);
+    unpack8<Act>(*reinterpret_cast<const u32x4*>(w + e), wv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = __fmul_rn(__fmul_rn(h[i], inv), wv[i]);
+    *reinterpret_cast<u32x4*>(y + e) = pack8<Act>(o);
+  }
+}
+
+// One workgroup per token; a thread per (head, i < D/2) pair rotates dims i and i + D/2.
+template <class Act>
+__global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
+  using Raw = typename Act::raw;
+  const int64_t t = blockIdx.x;
+  const int half = int(a.head_dim / 2);
+  int64_t p = a.positions[t];
+  p = p < 0 ? 0 : (p >= a.table_rows ? a.table_rows - 1 : p);  // the host checks the range
+  const float* cs = a.cos_table + p * a.head_dim;
+  const float* sn = a.sin_table + p * a.head_dim;
+  const int64_t pairs = (a.heads + a.kv_heads) * half;
+  for (int64_t j = threadIdx.x; j < pairs; j += blockDim.x) {
+    const int64_t head = j / half;
+    const int i = int(j - head * half);
+    const bool is_q = head < a.heads;
+    const int64_t hh = is_q ? head : head - a.heads;
+    const Raw* src = static_cast<const Raw*>(is_q ? a.q : a.k) + t * (is_q ? a.ldq : a.ldk) + hh * a.head_dim;
+    Raw* dst = static_cast<Raw*>(is_q ? a.q_out : a.k_out) + (t * (is_q ? a.heads : a.kv_heads) + hh) * a.head_dim;
+    const float x1 = Act::load(src[i]), x2 = Act::load(src[i + half]);
+    // The tables are cast to the activation dtype first (cos.to(q.dtype)).
+    const float c1 = Act::load(Act::store(cs[i])), s1 = Act::load(Act::store(sn[i]));
+    const float c2 = Act::load(Act::store(cs[i + half])), s2 = Act::load(Act::store(sn[i + half]));
+    // rotate_half(x) = [-x2, x1]; every product and the sum rounded as torch rounds them.
+    const float lo = Act::load(Act::store(Act::load(Act::store(x1 * c1)) + Act::load(Act::store(-x2 * s1))));
+    const float hi = Act::load(Act::store(Act::load(Act::store(x2 * c2)) + Act::load(Act::store(x1 * s2))));
+    dst[i] = Act::store(lo);
+    dst[i + half] = Act::store(hi);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(const RmsNormArgs& a, hipStream_t stream) {
+  if (a.rows == 0) return hipSuccess;
+  if (a.dtype == kDtBf16)
+    hipLaunchKernelGGL(rmsnorm_kernel<ActBf16>, dim3(unsigned(a.rows)), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<ActF16>, dim3(unsigned(a.rows)), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope(const RopeArgs& a, hipStream_t stream) {
+  if (a.tokens == 0) return hipSuccess;
+  if (a.dtype == kDtBf16)
+    hipLaunchKernelGGL(rope_kernel<ActBf16>, dim3(unsigned(a.tokens)), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(rope_kernel<ActF16>, dim3(unsigned(a.tokens)), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace llmopt

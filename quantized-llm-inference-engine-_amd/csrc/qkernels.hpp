@@ -95,6 +95,31 @@ struct PagedDecodeArgs {
   int waves;                // waves per workgroup: 1, 2, 4 or 8 (8 only below 16 heads per KV head)
 };
 hipError_t launch_paged_decode(const PagedDecodeArgs& a, hipStream_t stream);
+
+struct RmsNormArgs {
+  const void* x;         // [rows, hidden], row stride ldx
+  const void* residual;  // optional [rows, hidden], row stride ldr: h = residual + x
+  void* h_out;           // with residual: h, row stride ldh
+  const void* weight;    // [hidden], the activation dtype
+  void* y;               // [rows, hidden], row stride ldy
+  int64_t rows, hidden, ldx, ldr, ldh, ldy;
+  float eps;
+  int dtype;             // kDtBf16 or kDtF16
+};
+hipError_t launch_rmsnorm(const RmsNormArgs& a, hipStream_t stream);
+
+struct RopeArgs {
+  const void* q;  // [tokens, heads, head_dim], token stride ldq
+  const void* k;  // [tokens, kv_heads, head_dim], token stride ldk
+  void* q_out;    // [tokens, heads, head_dim], contiguous
+  void* k_out;    // [tokens, kv_heads, head_dim], contiguous
+  const int64_t* positions;  // [tokens]
+  const float* cos_table;    // [table_rows, head_dim] fp32
+  const float* sin_table;
+  int64_t table_rows, tokens, heads, kv_heads, head_dim, ldq, ldk;
+  int dtype;
+};
+hipError_t launch_rope(const RopeArgs& a, hipStream_t stream);
 hipError_t launch_linear_generic(const LinearArgs& a, hipStream_t stream);
 // Decode and prefill report `fits = false` (and launch nothing) when the shape, alignment or
 // dtype is outside what the kernel handles.

@@ -64,6 +64,14 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _p, _int, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _int, _i64, _i64, _i64, _i64, _p],
     ),
     "llmopt_paged_attention_workspace": (_size, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "llmopt_rmsnorm": (
+        _int,
+        [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, ctypes.c_float, _int, _p],
+    ),
+    "llmopt_rope": (
+        _int,
+        [_p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _p],
+    ),
     "llmopt_paged_attention_decode": (
         _int,
         [_p, _int, _i64, _p, _p, _int, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64,

@@ -32,6 +32,9 @@ __all__ = [
     "quant_linear",
     "quant_linear_swiglu",
     "quantize_rtn",
+    "rmsnorm",
+    "rmsnorm_supported",
+    "rope",
     "unpack_nibbles",
 ]
 
@@ -444,3 +447,68 @@ def paged_decode_attention(
     )
     return out
 
+
+
+# ---- decoder elementwise steps -------------------------------------------------------------------
+
+
+def rmsnorm_supported(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None = None) -> bool:
+    """Whether :func:`rmsnorm` takes these tensors (bf16/fp16 on a HIP device, 16-byte rows)."""
+    if x.device.type != "cuda" or x.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != x.dtype:
+        return False
+    hidden = int(x.shape[-1]) if x.dim() else 0
+    if hidden == 0 or hidden % 8 or weight.numel() != hidden or not weight.is_contiguous():
+        return False
+    tensors = [x, weight] + ([residual] if residual is not None else [])
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype):
+        return False
+    return all(t.data_ptr() % 16 == 0 and (t.dim() < 2 or t.stride(-1) == 1) for t in tensors)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """``(y, h)``: ``h = residual + x`` (rounded to the dtype; None without a residual) and
+    ``y = RMSNorm(h or x) * weight``, in one kernel (``layers.py:14-31,185-195``)."""
+    shape = x.shape
+    hidden = int(shape[-1])
+    x2 = x.reshape(-1, hidden)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8:
+        x2 = x2.contiguous()
+    r2 = residual.reshape(-1, hidden).contiguous() if residual is not None else None
+    rows = int(x2.shape[0])
+    y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
+    h = torch.empty_like(y) if residual is not None else None
+    call(
+        load_library().llmopt_rmsnorm(
+            x2.data_ptr(), x2.stride(0), None if r2 is None else r2.data_ptr(), hidden,
+            None if h is None else h.data_ptr(), hidden, weight.data_ptr(), y.data_ptr(), hidden, rows, hidden,
+            float(eps), DTYPE_CODES[x.dtype], _stream_handle(x.device),
+        ),
+        "llmopt_rmsnorm",
+    )
+    return y.view(shape), (h.view(shape) if h is not None else None)
+
+
+def rope(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor, cos_table: torch.Tensor,
+         sin_table: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rotary embedding of ``q [tokens, heads, d]`` and ``k [tokens, kv_heads, d]`` (each with
+    unit stride inside a token) at ``positions [tokens]``; returns new contiguous tensors,
+    bit-identical to ``apply_rotary_pos_emb`` with the tables cast to the dtype."""
+    tokens, heads, d = (int(s) for s in q.shape)
+    kv_heads = int(k.shape[1])
+    if q.stride(2) != 1 or q.stride(1) != d or k.stride(2) != 1 or k.stride(1) != d:
+        q, k = q.contiguous(), k.contiguous()
+    pos = positions.to(device=q.device, dtype=torch.int64).contiguous()
+    cos_t = cos_table.to(device=q.device, dtype=torch.float32).contiguous()
+    sin_t = sin_table.to(device=q.device, dtype=torch.float32).contiguous()
+    q_out = torch.empty(tokens, heads, d, dtype=q.dtype, device=q.device)
+    k_out = torch.empty(tokens, kv_heads, d, dtype=k.dtype, device=k.device)
+    call(
+        load_library().llmopt_rope(
+            q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), q_out.data_ptr(), k_out.data_ptr(), pos.data_ptr(),
+            cos_t.data_ptr(), sin_t.data_ptr(), int(cos_t.shape[0]), tokens, heads, kv_heads, d,
+            DTYPE_CODES[q.dtype], _stream_handle(q.device),
+        ),
+        "llmopt_rope",
+    )
+    return q_out, k_out

@@ -7,7 +7,9 @@ does in the reference. :meth:`PagedAttentionLayer.fuse_qkv` and :meth:`SwiGLUMLP
 then merge the quantized projections into one packed weight each (one kernel launch for q, k
 and v; one for gate and up with the SiLU-times-up product in the kernel's epilogue). On HIP
 devices the attention step writes K/V with the cache-write kernels and, for one query token
-per sequence, runs the paged decode-attention kernel.
+per sequence, runs the paged decode-attention kernel; RMSNorm (with the residual add in front
+of it) and the rotary embedding run as one kernel each (``llmopt_rmsnorm``, ``llmopt_rope``)
+with the reference's roundings. Elsewhere every step is the reference's torch sequence.
 """
 
 from __future__ import annotations
@@ -23,6 +25,10 @@ from llmopt.quantization.quant_linear import QuantLinear
 __all__ = ["DecoderLayer", "PagedAttentionLayer", "RMSNorm", "SwiGLUMLP"]
 
 
+def _hip(x: torch.Tensor) -> bool:
+    return x.device.type == "cuda" and x.dtype in (torch.bfloat16, torch.float16)
+
+
 class RMSNorm(nn.Module):
     """``x / sqrt(mean(x^2) + eps) * weight`` in fp32, returned in the input dtype
     (``layers.py:14-31``)."""
@@ -32,10 +38,30 @@ class RMSNorm(nn.Module):
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(hidden_size))
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def _reference(self, x: torch.Tensor) -> torch.Tensor:
         x32 = x.to(torch.float32)
         inv = torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + self.eps)
         return (x32 * inv * self.weight.to(torch.float32)).to(x.dtype)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if _hip(x):
+            from llmopt.kernels import ops
+
+            if ops.rmsnorm_supported(x, self.weight):
+                return ops.rmsnorm(x, self.weight, self.eps)[0]
+        return self._reference(x)
+
+    def add_forward(self, x: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """``(norm(h), h)`` with ``h = residual + x``: the residual add and the norm after it
+        (``layers.py:185-195``), one kernel on HIP devices."""
+        if _hip(x):
+            from llmopt.kernels import ops
+
+            if ops.rmsnorm_supported(x, self.weight, residual):
+                y, h = ops.rmsnorm(x, self.weight, self.eps, residual)
+                return y, h
+        h = residual + x
+        return self._reference(h), h
 
 
 class SwiGLUMLP(nn.Module):
@@ -116,15 +142,25 @@ class PagedAttentionLayer(nn.Module):
         q, k, v = self._project(hidden)
         # Token-major [seq, q_len, heads, head_dim]: the cache layout, and cos/sin broadcast
         # over the heads of each token.
-        q = q.reshape(seqs, q_len, self.num_heads, self.head_dim)
-        k = k.reshape(seqs, q_len, self.num_kv_heads, self.head_dim)
         v = v.reshape(seqs, q_len, self.num_kv_heads, self.head_dim)
-        cos, sin = self.rotary(positions, dtype=q.dtype)
-        cos = cos.view(seqs, q_len, 1, self.head_dim)
-        sin = sin.view(seqs, q_len, 1, self.head_dim)
-        q, k = apply_rotary_pos_emb(q, k, cos, sin)
-        k = k.contiguous()
-        v = v.contiguous()
+        if _hip(q):
+            from llmopt.kernels import ops
+
+            self.rotary.check(positions)
+            q, k = ops.rope(q.view(total, self.num_heads, self.head_dim),
+                            k.view(total, self.num_kv_heads, self.head_dim), positions,
+                            self.rotary.cos_cached, self.rotary.sin_cached)
+            q = q.view(seqs, q_len, self.num_heads, self.head_dim)
+            k = k.view(seqs, q_len, self.num_kv_heads, self.head_dim)
+        else:
+            q = q.reshape(seqs, q_len, self.num_heads, self.head_dim)
+            k = k.reshape(seqs, q_len, self.num_kv_heads, self.head_dim)
+            cos, sin = self.rotary(positions, dtype=q.dtype)
+            cos = cos.view(seqs, q_len, 1, self.head_dim)
+            sin = sin.view(seqs, q_len, 1, self.head_dim)
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+            k = k.contiguous()
+            v = v.contiguous()
         query = q.permute(0, 2, 1, 3)  # [seq, heads, q_len, head_dim]
         if cache is not None and block_ids is not None and context_lens is not None:
             offsets = token_offsets if token_offsets is not None else context_lens - q_len
@@ -164,6 +200,7 @@ class DecoderLayer(nn.Module):
     def forward(self, hidden: torch.Tensor, positions: torch.Tensor, cache: object | None = None,
                 block_ids: torch.Tensor | None = None, context_lens: torch.Tensor | None = None,
                 token_offsets: torch.Tensor | None = None, q_len: int = 1) -> torch.Tensor:
-        hidden = hidden + self.self_attn(self.input_layernorm(hidden), positions, cache, block_ids,
-                                         context_lens, token_offsets, q_len)
-        return hidden + self.mlp(self.post_attention_layernorm(hidden))
+        attn = self.self_attn(self.input_layernorm(hidden), positions, cache, block_ids, context_lens,
+                              token_offsets, q_len)
+        normed, hidden = self.post_attention_layernorm.add_forward(attn, hidden)
+        return hidden + self.mlp(normed)

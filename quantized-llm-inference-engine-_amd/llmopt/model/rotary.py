@@ -43,13 +43,17 @@ class RotaryEmbedding(nn.Module):
         self.register_buffer("cos_cached", angles.cos().to(dtype), persistent=False)
         self.register_buffer("sin_cached", angles.sin().to(dtype), persistent=False)
 
-    def forward(self, positions: torch.Tensor, dtype: torch.dtype | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-        """``(cos, sin)``, each ``[len(positions), head_dim]``. Positions past the table raise
-        ``ValueError``; the check reads the positions on the host, so it is skipped while a
-        HIP graph is being captured (the replayed step must not synchronize)."""
+    def check(self, positions: torch.Tensor) -> None:
+        """Raise ``ValueError`` for a position past the table. The check reads the positions on
+        the host, so it is skipped while a HIP graph is being captured (a replayed step must not
+        synchronize)."""
         capturing = positions.is_cuda and torch.cuda.is_current_stream_capturing()
         if not capturing and positions.numel() and int(positions.max()) >= self.max_position_embeddings:
             raise ValueError(f"position {int(positions.max())} exceeds table length {self.max_position_embeddings}")
+
+    def forward(self, positions: torch.Tensor, dtype: torch.dtype | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """``(cos, sin)``, each ``[len(positions), head_dim]`` (see :meth:`check`)."""
+        self.check(positions)
         cos = self.cos_cached[positions]
         sin = self.sin_cached[positions]
         if dtype is not None:

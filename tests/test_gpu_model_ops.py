@@ -1,0 +1,66 @@
+"""The decoder's fused elementwise kernels against the reference's torch sequences:
+llmopt_rope (bit-identical to apply_rotary_pos_emb with the tables cast to the dtype,
+src/llmopt/model/rotary.py:23-45,85-102) and llmopt_rmsnorm (RMSNorm.forward with the residual
+add before it, src/llmopt/model/layers.py:14-31,185-195)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from llmopt.kernels import ops
+from llmopt.model import RMSNorm, RotaryEmbedding, apply_rotary_pos_emb
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("heads,kv_heads,d", [(32, 8, 128), (4, 2, 64), (6, 0, 16)])
+def test_rope_is_bit_identical_to_the_torch_sequence(dtype, heads, kv_heads, d):
+    g = torch.Generator(device=DEV).manual_seed(heads + d)
+    tokens = 37
+    rope = RotaryEmbedding(d, 4096, base=500000.0).to(DEV)
+    # q and k as column slices of one fused projection output, as the model passes them
+    fused = torch.randn(tokens, (heads + 2 * kv_heads) * d, generator=g, device=DEV).to(dtype)
+    q = fused[:, : heads * d].view(tokens, heads, d)
+    k = fused[:, heads * d : (heads + kv_heads) * d].view(tokens, kv_heads, d)
+    positions = torch.randint(0, 4096, (tokens,), generator=g, device=DEV)
+    got_q, got_k = ops.rope(q, k, positions, rope.cos_cached, rope.sin_cached)
+    cos, sin = rope(positions, dtype=dtype)
+    want_q, want_k = apply_rotary_pos_emb(q, k, cos[:, None, :], sin[:, None, :])
+    assert got_q.is_contiguous() and got_k.is_contiguous()
+    assert torch.equal(got_q, want_q)
+    assert torch.equal(got_k, want_k)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,hidden", [(1, 4096), (32, 4096), (5, 264)])
+def test_rmsnorm_with_residual_matches_the_torch_sequence(dtype, rows, hidden):
+    g = torch.Generator(device=DEV).manual_seed(rows * hidden)
+    norm = RMSNorm(hidden, eps=1e-5).to(DEV, dtype)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(hidden, generator=g, device=DEV) + 0.5)
+    x = torch.randn(rows, hidden, generator=g, device=DEV).to(dtype)
+    r = (torch.randn(rows, hidden, generator=g, device=DEV) * 4).to(dtype)
+    y, h = ops.rmsnorm(x, norm.weight, norm.eps, r)
+    assert torch.equal(h, r + x)  # the add rounds exactly as torch's
+    want = norm._reference(r + x)
+    # fp32 arithmetic in a different summation order, rounded once: at most one unit in the
+    # last place of the dtype (at most 2^-7 relative for bf16, 2^-10 for fp16) on a few elements
+    ulp = 2.0**-7 if dtype == torch.bfloat16 else 2.0**-10
+    diff = (y.float() - want.float()).abs()
+    assert float((diff / want.float().abs().clamp_min(1e-3)).max()) <= 1.01 * ulp
+    assert float((diff > 0).float().mean()) < 0.05
+    y2, none = ops.rmsnorm(x, norm.weight, norm.eps)
+    assert none is None
+    assert float(((y2.float() - norm._reference(x).float()).abs() / norm._reference(x).float().abs().clamp_min(1e-3)).max()) <= 1.01 * ulp
+
+
+def test_rmsnorm_module_takes_the_kernel_on_hip():
+    norm = RMSNorm(4096).to(DEV, torch.bfloat16)
+    x = torch.randn(3, 4096, device=DEV).to(torch.bfloat16)
+    assert ops.rmsnorm_supported(x, norm.weight)
+    assert not ops.rmsnorm_supported(x.float(), norm.weight.float())
+    y = norm(x)
+    assert torch.equal(y, ops.rmsnorm(x, norm.weight, norm.eps)[0])
