@@ -36,6 +36,7 @@ def test_rope_is_bit_identical_to_the_torch_sequence(dtype, heads, kv_heads, d):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows,hidden", [(1, 4096), (32, 4096), (5, 264)])
+@torch.no_grad()
 def test_rmsnorm_with_residual_matches_the_torch_sequence(dtype, rows, hidden):
     g = torch.Generator(device=DEV).manual_seed(rows * hidden)
     norm = RMSNorm(hidden, eps=1e-5).to(DEV, dtype)
@@ -57,6 +58,7 @@ def test_rmsnorm_with_residual_matches_the_torch_sequence(dtype, rows, hidden):
     assert float(((y2.float() - norm._reference(x).float()).abs() / norm._reference(x).float().abs().clamp_min(1e-3)).max()) <= 1.01 * ulp
 
 
+@torch.no_grad()
 def test_rmsnorm_module_takes_the_kernel_on_hip():
     norm = RMSNorm(4096).to(DEV, torch.bfloat16)
     x = torch.randn(3, 4096, device=DEV).to(torch.bfloat16)

@@ -194,14 +194,24 @@ def test_linear_small_shapes(algo, dtype, bits, symmetric, n, k, group, m):
 @pytest.mark.parametrize("symmetric", [False, True])
 @pytest.mark.parametrize("m", [5, 8, 16, 24, 33, 48])
 def test_linear_batched_decode_shapes(dtype, symmetric, m):
-    # K = 4096 (32 steps of 128 codes): at M <= 16 the multi-tile kernel with every wave's
-    # range loaded up front; 17-32 the ring configuration; above 32 the split-K GEMM.
+    # K = 4096 (32 steps of 128 codes), 64 tiles of 16 features: up to M = 32 the multi-tile
+    # kernel with every wave's range loaded up front; above 32 the split-K GEMM.
     qt = _host_qt(1024, 4096, 4, 128, symmetric, seed=m)
     gen = torch.Generator().manual_seed(m)
     x = torch.randn(m, 4096, generator=gen).to(dtype)
     bias = torch.randn(1024, generator=gen).to(dtype)
     y = ops.quant_linear(x.to(DEV), _to_device(qt), bias.to(DEV), dtype)
     assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), bias, dtype)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [20, 32])
+def test_linear_batched_decode_ring_configuration(dtype, m):
+    # 512 tiles of 16 features at M = 17-32: the four-tile workgroups with a ring of refills.
+    qt = _host_qt(8192, 4096, 4, 128, False, seed=m)
+    x = torch.randn(m, 4096, generator=torch.Generator().manual_seed(m)).to(dtype)
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None, dtype)
+    assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), None, dtype)) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
