@@ -23,6 +23,11 @@ namespace {
 // the GEMM against 105 us in the multi-tile decode kernel; at M = 32 the decode kernels lead).
 constexpr int64_t kDecodeMaxTokens = 32;
 
+// Whether the split-K GEMM takes a plain product of this size: every batch above
+// kDecodeMaxTokens, and from 24 tokens the long rows (K >= 8192, down: 40.7 -> 33.8 us at
+// M = 32), where the decode kernels' per-workgroup metadata outgrows them.
+bool gemm_first(int64_t M, int64_t K) { return M > kDecodeMaxTokens || (M >= 24 && K >= 8192); }
+
 thread_local std::string g_last_error;
 
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -151,8 +156,13 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
   }
 
   switch (algo) {
-    case LLMOPT_ALGO_AUTO:
-      if (M <= kDecodeMaxTokens) {
+    case LLMOPT_ALGO_AUTO: {
+      bool gemm = gemm_first(M, K);
+      if (gemm && M <= kDecodeMaxTokens) {  // worth it only with its K split
+        const size_t need = llmopt::gemm_workspace_bytes(M, N, K, a.group, a.fmt);
+        gemm = need > 0 && a.workspace != nullptr && a.workspace_bytes >= need;
+      }
+      if (!gemm) {
         err = llmopt::launch_linear_decode(a, s, &fits);
       } else {
         err = llmopt::launch_linear_gemm(a, s, &fits);
@@ -161,6 +171,7 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
       }
       if (!fits) err = llmopt::launch_linear_generic(a, s);
       break;
+    }
     case LLMOPT_ALGO_GENERIC:
       err = llmopt::launch_linear_generic(a, s);
       break;
@@ -254,8 +265,8 @@ int llmopt_q_quantize_rtn(const void* weight, int w_dtype, int64_t ldw, int64_t 
 }
 
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
-  // Only the prefill GEMM (M > kDecodeMaxTokens) splits K; the decode kernels reduce in LDS.
-  if (M <= kDecodeMaxTokens || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
+  // Only the GEMM splits K; the decode kernels reduce in LDS.
+  if (!gemm_first(M, K) || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
   const int64_t g = group_size <= 0 ? K : group_size;
   return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
 }

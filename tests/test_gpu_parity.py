@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 import torch
 
-from llmopt.kernels import ops
+from llmopt.kernels import _lib, ops
 from llmopt.kernels._lib import ALGO_AUTO, ALGO_DECODE, ALGO_GENERIC, ALGO_PREFILL
 from llmopt.quantization import QuantizedTensor, RoundToNearestQuantizer, dequantize, unpack_int4
 from oracle import quant_oracle as qo
@@ -212,6 +212,28 @@ def test_linear_batched_decode_ring_configuration(dtype, m):
     x = torch.randn(m, 4096, generator=torch.Generator().manual_seed(m)).to(dtype)
     y = ops.quant_linear(x.to(DEV), _to_device(qt), None, dtype)
     assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), None, dtype)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [24, 32])
+def test_linear_long_rows_at_24_to_32_tokens(dtype, m):
+    # K >= 8192 from 24 tokens: the split-K GEMM when the workspace is there (ops passes it),
+    # the decode kernels when it is not (a C-ABI caller without one).
+    qt = _host_qt(512, 8192, 4, 128, False, seed=m)
+    x = torch.randn(m, 8192, generator=torch.Generator().manual_seed(m)).to(dtype)
+    ref = _reference_linear(x, _oracle_dense(qt), None, dtype)
+    dq = _to_device(qt)
+    y = ops.quant_linear(x.to(DEV), dq, None, dtype)
+    assert _rel_err(y, ref) <= TOL[dtype]
+    lib = _lib.load_library()
+    assert lib.llmopt_q_linear_workspace(m, 512, 8192, 4, 128) > 0
+    xd = x.to(DEV)
+    y2 = torch.empty(m, 512, dtype=dtype, device=DEV)
+    rc = lib.llmopt_q_linear(xd.data_ptr(), m, 8192, 8192, dq.qweight.data_ptr(), 4096, dq.scales.data_ptr(),
+                             dq.zeros.data_ptr(), None, y2.data_ptr(), 512, 512, _lib.DTYPE_CODES[dtype], 4, 128, 0, 0,
+                             None, 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    assert _rel_err(y2, ref) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
