@@ -35,12 +35,15 @@ int llmopt_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr
  * apply_rotary_pos_emb with RotaryEmbedding.forward (src/llmopt/model/rotary.py:23-45,85-102);
  * every product and sum is rounded to dtype as torch rounds it, so the result is identical.
  * q: [tokens, heads, head_dim] with token stride ldq; k: [tokens, kv_heads, head_dim] with token
- * stride ldk; q_out, k_out: contiguous. Positions outside [0, table_rows) are clamped (the
- * Python layer raises for them first, as the reference does).
+ * stride ldk; q_out, k_out: contiguous. v (optional, may be NULL): [tokens, kv_heads, head_dim]
+ * with token stride ldv, copied unchanged to the contiguous v_out (the layer's cache write then
+ * reads contiguous rows). Positions outside [0, table_rows) are clamped (the Python layer raises
+ * for them first, as the reference does).
  */
-int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, void* q_out, void* k_out,
-                const int64_t* positions, const float* cos_table, const float* sin_table, int64_t table_rows,
-                int64_t tokens, int64_t heads, int64_t kv_heads, int64_t head_dim, int dtype, void* stream);
+int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, void* q_out,
+                void* k_out, void* v_out, const int64_t* positions, const float* cos_table, const float* sin_table,
+                int64_t table_rows, int64_t tokens, int64_t heads, int64_t kv_heads, int64_t head_dim, int dtype,
+                void* stream);
 
 #ifdef __cplusplus
 }

@@ -529,9 +529,10 @@ int llmopt_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr
   return hip_status(llmopt::launch_rmsnorm(a, static_cast<hipStream_t>(stream)), "rmsnorm launch");
 }
 
-int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, void* q_out, void* k_out,
-                const int64_t* positions, const float* cos_table, const float* sin_table, int64_t table_rows,
-                int64_t tokens, int64_t heads, int64_t kv_heads, int64_t head_dim, int dtype, void* stream) {
+int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, void* q_out,
+                void* k_out, void* v_out, const int64_t* positions, const float* cos_table, const float* sin_table,
+                int64_t table_rows, int64_t tokens, int64_t heads, int64_t kv_heads, int64_t head_dim, int dtype,
+                void* stream) {
   if (dtype != LLMOPT_DTYPE_BF16 && dtype != LLMOPT_DTYPE_F16)
     return fail(LLMOPT_ERR_UNSUPPORTED, "rope kernel: dtype %d (bf16 and fp16 only)", dtype);
   if (tokens < 0 || tokens > 0x7FFFFFFF || heads < 1 || kv_heads < 0 || head_dim < 2 || head_dim % 2 ||
@@ -542,11 +543,15 @@ int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, void* q_
     return fail(LLMOPT_ERR_INVALID_ARG, "null rope pointer");
   if (ldq < heads * head_dim || (kv_heads > 0 && ldk < kv_heads * head_dim))
     return fail(LLMOPT_ERR_INVALID_ARG, "rope token stride below heads x head_dim");
+  if (v && (!v_out || ldv < kv_heads * head_dim)) return fail(LLMOPT_ERR_INVALID_ARG, "bad rope v arguments");
   llmopt::RopeArgs a{};
   a.q = q;
   a.k = k;
   a.q_out = q_out;
   a.k_out = k_out;
+  a.v = kv_heads > 0 ? v : nullptr;
+  a.v_out = v_out;
+  a.ldv = ldv;
   a.positions = positions;
   a.cos_table = cos_table;
   a.sin_table = sin_table;

@@ -8,7 +8,8 @@
 //   * apply_rotary_pos_emb with RotaryEmbedding.forward (src/llmopt/model/rotary.py:23-45,
 //     85-102) for q and k together: the fp32 cos/sin tables cast to the activation dtype, then
 //     q * cos + rotate_half(q) * sin with each product and the sum rounded to the activation
-//     dtype, as torch evaluates the expression op by op -- so the result is bit-identical.
+//     dtype, as torch evaluates the expression op by op -- so the result is bit-identical; v is
+//     copied alongside k into a contiguous buffer for the cache write.
 // torch runs these as about 8 (norm) and 14 (rotary) separate kernels per layer and step.
 #include "qcommon.hpp"
 #include "qkernels.hpp"
@@ -81,33 +82,40 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const RmsNormArgs a) {
   }
 }
 
-// One workgroup per token; a thread per (head, i < D/2) pair rotates dims i and i + D/2.
+// Grid (token, chunk of 256 pairs); a thread per (head, i < D/2) pair rotates dims i and
+// i + D/2 of q or k, and for the KV heads also copies v's dims i and i + D/2 (when v is given),
+// so that the cache write that follows reads contiguous rows.
 template <class Act>
 __global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
   using Raw = typename Act::raw;
   const int64_t t = blockIdx.x;
   const int half = int(a.head_dim / 2);
+  const int64_t j = int64_t(blockIdx.y) * 256 + threadIdx.x;
+  if (j >= (a.heads + a.kv_heads) * half) return;
   int64_t p = a.positions[t];
   p = p < 0 ? 0 : (p >= a.table_rows ? a.table_rows - 1 : p);  // the host checks the range
   const float* cs = a.cos_table + p * a.head_dim;
   const float* sn = a.sin_table + p * a.head_dim;
-  const int64_t pairs = (a.heads + a.kv_heads) * half;
-  for (int64_t j = threadIdx.x; j < pairs; j += blockDim.x) {
-    const int64_t head = j / half;
-    const int i = int(j - head * half);
-    const bool is_q = head < a.heads;
-    const int64_t hh = is_q ? head : head - a.heads;
-    const Raw* src = static_cast<const Raw*>(is_q ? a.q : a.k) + t * (is_q ? a.ldq : a.ldk) + hh * a.head_dim;
-    Raw* dst = static_cast<Raw*>(is_q ? a.q_out : a.k_out) + (t * (is_q ? a.heads : a.kv_heads) + hh) * a.head_dim;
-    const float x1 = Act::load(src[i]), x2 = Act::load(src[i + half]);
-    // The tables are cast to the activation dtype first (cos.to(q.dtype)).
-    const float c1 = Act::load(Act::store(cs[i])), s1 = Act::load(Act::store(sn[i]));
-    const float c2 = Act::load(Act::store(cs[i + half])), s2 = Act::load(Act::store(sn[i + half]));
-    // rotate_half(x) = [-x2, x1]; every product and the sum rounded as torch rounds them.
-    const float lo = Act::load(Act::store(Act::load(Act::store(x1 * c1)) + Act::load(Act::store(-x2 * s1))));
-    const float hi = Act::load(Act::store(Act::load(Act::store(x2 * c2)) + Act::load(Act::store(x1 * s2))));
-    dst[i] = Act::store(lo);
-    dst[i + half] = Act::store(hi);
+  const int64_t head = j / half;
+  const int i = int(j - head * half);
+  const bool is_q = head < a.heads;
+  const int64_t hh = is_q ? head : head - a.heads;
+  const Raw* src = static_cast<const Raw*>(is_q ? a.q : a.k) + t * (is_q ? a.ldq : a.ldk) + hh * a.head_dim;
+  Raw* dst = static_cast<Raw*>(is_q ? a.q_out : a.k_out) + (t * (is_q ? a.heads : a.kv_heads) + hh) * a.head_dim;
+  const float x1 = Act::load(src[i]), x2 = Act::load(src[i + half]);
+  // The tables are cast to the activation dtype first (cos.to(q.dtype)).
+  const float c1 = Act::load(Act::store(cs[i])), s1 = Act::load(Act::store(sn[i]));
+  const float c2 = Act::load(Act::store(cs[i + half])), s2 = Act::load(Act::store(sn[i + half]));
+  // rotate_half(x) = [-x2, x1]; every product and the sum rounded as torch rounds them.
+  const float lo = Act::load(Act::store(Act::load(Act::store(x1 * c1)) + Act::load(Act::store(-x2 * s1))));
+  const float hi = Act::load(Act::store(Act::load(Act::store(x2 * c2)) + Act::load(Act::store(x1 * s2))));
+  dst[i] = Act::store(lo);
+  dst[i + half] = Act::store(hi);
+  if (!is_q && a.v) {
+    const Raw* vs = static_cast<const Raw*>(a.v) + t * a.ldv + hh * a.head_dim;
+    Raw* vd = static_cast<Raw*>(a.v_out) + (t * a.kv_heads + hh) * a.head_dim;
+    vd[i] = vs[i];
+    vd[i + half] = vs[i + half];
   }
 }
 
@@ -124,10 +132,11 @@ hipError_t launch_rmsnorm(const RmsNormArgs& a, hipStream_t stream) {
 
 hipError_t launch_rope(const RopeArgs& a, hipStream_t stream) {
   if (a.tokens == 0) return hipSuccess;
+  const dim3 grid(unsigned(a.tokens), unsigned(((a.heads + a.kv_heads) * (a.head_dim / 2) + 255) / 256));
   if (a.dtype == kDtBf16)
-    hipLaunchKernelGGL(rope_kernel<ActBf16>, dim3(unsigned(a.tokens)), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(rope_kernel<ActBf16>, grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL(rope_kernel<ActF16>, dim3(unsigned(a.tokens)), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(rope_kernel<ActF16>, grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -113,6 +113,9 @@ struct RopeArgs {
   const void* k;  // [tokens, kv_heads, head_dim], token stride ldk
   void* q_out;    // [tokens, heads, head_dim], contiguous
   void* k_out;    // [tokens, kv_heads, head_dim], contiguous
+  const void* v;  // optional [tokens, kv_heads, head_dim], token stride ldv: copied to v_out
+  void* v_out;
+  int64_t ldv;
   const int64_t* positions;  // [tokens]
   const float* cos_table;    // [table_rows, head_dim] fp32
   const float* sin_table;

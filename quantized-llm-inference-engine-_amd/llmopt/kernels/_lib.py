@@ -70,7 +70,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "llmopt_rope": (
         _int,
-        [_p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _p],
+        [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _p],
     ),
     "llmopt_paged_attention_decode": (
         _int,

@@ -490,25 +490,36 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
 
 
 def rope(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor, cos_table: torch.Tensor,
-         sin_table: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+         sin_table: torch.Tensor, v: torch.Tensor | None = None) -> tuple[torch.Tensor, ...]:
     """Rotary embedding of ``q [tokens, heads, d]`` and ``k [tokens, kv_heads, d]`` (each with
     unit stride inside a token) at ``positions [tokens]``; returns new contiguous tensors,
-    bit-identical to ``apply_rotary_pos_emb`` with the tables cast to the dtype."""
+    bit-identical to ``apply_rotary_pos_emb`` with the tables cast to the dtype. With ``v``
+    (shaped like ``k``) a contiguous copy of it is returned third."""
     tokens, heads, d = (int(s) for s in q.shape)
     kv_heads = int(k.shape[1])
-    if q.stride(2) != 1 or q.stride(1) != d or k.stride(2) != 1 or k.stride(1) != d:
-        q, k = q.contiguous(), k.contiguous()
+
+    def inner_ok(t: torch.Tensor) -> bool:
+        return t.stride(2) == 1 and t.stride(1) == d
+
+    if not inner_ok(q):
+        q = q.contiguous()
+    if not inner_ok(k):
+        k = k.contiguous()
+    if v is not None and not inner_ok(v):
+        v = v.contiguous()
     pos = positions.to(device=q.device, dtype=torch.int64).contiguous()
     cos_t = cos_table.to(device=q.device, dtype=torch.float32).contiguous()
     sin_t = sin_table.to(device=q.device, dtype=torch.float32).contiguous()
     q_out = torch.empty(tokens, heads, d, dtype=q.dtype, device=q.device)
     k_out = torch.empty(tokens, kv_heads, d, dtype=k.dtype, device=k.device)
+    v_out = torch.empty_like(k_out) if v is not None else None
     call(
         load_library().llmopt_rope(
-            q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), q_out.data_ptr(), k_out.data_ptr(), pos.data_ptr(),
-            cos_t.data_ptr(), sin_t.data_ptr(), int(cos_t.shape[0]), tokens, heads, kv_heads, d,
-            DTYPE_CODES[q.dtype], _stream_handle(q.device),
+            q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), None if v is None else v.data_ptr(),
+            0 if v is None else v.stride(0), q_out.data_ptr(), k_out.data_ptr(),
+            None if v_out is None else v_out.data_ptr(), pos.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(),
+            int(cos_t.shape[0]), tokens, heads, kv_heads, d, DTYPE_CODES[q.dtype], _stream_handle(q.device),
         ),
         "llmopt_rope",
     )
-    return q_out, k_out
+    return (q_out, k_out) if v_out is None else (q_out, k_out, v_out)

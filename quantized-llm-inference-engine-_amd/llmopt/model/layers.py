@@ -142,17 +142,19 @@ class PagedAttentionLayer(nn.Module):
         q, k, v = self._project(hidden)
         # Token-major [seq, q_len, heads, head_dim]: the cache layout, and cos/sin broadcast
         # over the heads of each token.
-        v = v.reshape(seqs, q_len, self.num_kv_heads, self.head_dim)
         if _hip(q):
             from llmopt.kernels import ops
 
             self.rotary.check(positions)
-            q, k = ops.rope(q.view(total, self.num_heads, self.head_dim),
-                            k.view(total, self.num_kv_heads, self.head_dim), positions,
-                            self.rotary.cos_cached, self.rotary.sin_cached)
+            q, k, v = ops.rope(q.view(total, self.num_heads, self.head_dim),
+                               k.view(total, self.num_kv_heads, self.head_dim), positions,
+                               self.rotary.cos_cached, self.rotary.sin_cached,
+                               v=v.view(total, self.num_kv_heads, self.head_dim))
             q = q.view(seqs, q_len, self.num_heads, self.head_dim)
             k = k.view(seqs, q_len, self.num_kv_heads, self.head_dim)
+            v = v.view(seqs, q_len, self.num_kv_heads, self.head_dim)
         else:
+            v = v.reshape(seqs, q_len, self.num_kv_heads, self.head_dim)
             q = q.reshape(seqs, q_len, self.num_heads, self.head_dim)
             k = k.reshape(seqs, q_len, self.num_kv_heads, self.head_dim)
             cos, sin = self.rotary(positions, dtype=q.dtype)
@@ -200,7 +202,22 @@ class DecoderLayer(nn.Module):
     def forward(self, hidden: torch.Tensor, positions: torch.Tensor, cache: object | None = None,
                 block_ids: torch.Tensor | None = None, context_lens: torch.Tensor | None = None,
                 token_offsets: torch.Tensor | None = None, q_len: int = 1) -> torch.Tensor:
-        attn = self.self_attn(self.input_layernorm(hidden), positions, cache, block_ids, context_lens,
-                              token_offsets, q_len)
+        hidden, mlp_out = self.forward_chained(hidden, None, positions, cache, block_ids, context_lens,
+                                               token_offsets, q_len)
+        return hidden + mlp_out
+
+    def forward_chained(self, hidden: torch.Tensor, pending: torch.Tensor | None, positions: torch.Tensor,
+                        cache: object | None = None, block_ids: torch.Tensor | None = None,
+                        context_lens: torch.Tensor | None = None, token_offsets: torch.Tensor | None = None,
+                        q_len: int = 1) -> tuple[torch.Tensor, torch.Tensor]:
+        """The layer with its final residual add left to the caller: takes ``hidden`` plus the
+        previous layer's not-yet-added MLP output ``pending`` (or None) and returns ``(hidden,
+        mlp_out)``. The input stream is ``hidden + pending``, formed inside the first norm's
+        kernel, so a stack of layers runs one fused add + norm per residual add."""
+        if pending is None:
+            normed = self.input_layernorm(hidden)
+        else:
+            normed, hidden = self.input_layernorm.add_forward(pending, hidden)
+        attn = self.self_attn(normed, positions, cache, block_ids, context_lens, token_offsets, q_len)
         normed, hidden = self.post_attention_layernorm.add_forward(attn, hidden)
-        return hidden + self.mlp(normed)
+        return hidden, self.mlp(normed)

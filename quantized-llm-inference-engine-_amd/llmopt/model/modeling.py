@@ -62,16 +62,21 @@ class DecoderOnlyModel(nn.Module):
         input_ids = input_ids.reshape(-1)
         positions = positions.reshape(-1)
         hidden = self.embed_tokens(input_ids)
+        pending = None  # each layer's MLP output, added inside the next norm's kernel
         for layer in self.layers:
-            hidden = layer(hidden, positions, cache=cache, block_ids=block_ids, context_lens=context_lens,
-                           token_offsets=token_offsets, q_len=q_len)
+            hidden, pending = layer.forward_chained(hidden, pending, positions, cache=cache, block_ids=block_ids,
+                                                    context_lens=context_lens, token_offsets=token_offsets,
+                                                    q_len=q_len)
         seqs = int(hidden.shape[0]) // max(1, q_len)
         if last_only:
-            # RMSNorm and lm_head act row by row, so normalizing the kept rows only is exact.
-            last = self.norm(last_token_hidden(hidden, q_len).contiguous())
-            return ModelOutput(logits=self.lm_head(last).view(seqs, 1, -1))
-        logits = self.lm_head(self.norm(hidden))
-        return ModelOutput(logits=logits.view(seqs, q_len, -1))
+            # The residual add, RMSNorm and lm_head act row by row, so keeping only the last rows
+            # first is exact.
+            hidden = last_token_hidden(hidden, q_len).contiguous()
+            if pending is not None:
+                pending = last_token_hidden(pending, q_len).contiguous()
+        normed = self.norm(hidden) if pending is None else self.norm.add_forward(pending, hidden)[0]
+        logits = self.lm_head(normed)
+        return ModelOutput(logits=logits.view(seqs, 1 if last_only else q_len, -1))
 
     def allocate_cache(self, num_blocks: int, block_size: int, dtype: torch.dtype, device: torch.device | str) -> object:
         """A :class:`PagedKVCache` for this model (``modeling.py:132-145``)."""

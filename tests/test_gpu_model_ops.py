@@ -26,12 +26,16 @@ def test_rope_is_bit_identical_to_the_torch_sequence(dtype, heads, kv_heads, d):
     q = fused[:, : heads * d].view(tokens, heads, d)
     k = fused[:, heads * d : (heads + kv_heads) * d].view(tokens, kv_heads, d)
     positions = torch.randint(0, 4096, (tokens,), generator=g, device=DEV)
+    v = fused[:, (heads + kv_heads) * d :].view(tokens, kv_heads, d)
     got_q, got_k = ops.rope(q, k, positions, rope.cos_cached, rope.sin_cached)
     cos, sin = rope(positions, dtype=dtype)
     want_q, want_k = apply_rotary_pos_emb(q, k, cos[:, None, :], sin[:, None, :])
     assert got_q.is_contiguous() and got_k.is_contiguous()
     assert torch.equal(got_q, want_q)
     assert torch.equal(got_k, want_k)
+    q3, k3, v3 = ops.rope(q, k, positions, rope.cos_cached, rope.sin_cached, v=v)
+    assert torch.equal(q3, want_q) and torch.equal(k3, want_k)
+    assert v3.is_contiguous() and torch.equal(v3, v)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
