@@ -24,17 +24,23 @@ dense_comparator  (in roofline and prefill) torch's dense bf16 F.linear on the d
 dequant, quantize, attention  the device dequantize and RTN quantizer on gate_up, and the
                decode-step paged attention / KV write / last-token vocabulary projection of the
                end-to-end Llama-3-8B workload (32 sequences, 512-token prompts)
+e2e            that workload end to end (config 5): the Llama-3-8B model, every decoder linear
+               W4 g128 asymmetric, 32 prompts of 512 tokens, one prefill forward, then 128
+               greedy decode steps through the paged cache, each step one HIP-graph replay;
+               decode and prefill tokens/s (reported, not a roofline figure)
 cpu_baseline   the reference's host sequence (dequantize once, cache the dense bf16 weight,
                F.linear) on this host's cores, for a bounded number of the same decode steps
 
 Every single-projection timing (roofline, prefill, --sweep, --bits-sweep) rotates over at least
 512 MiB of that projection's own weight copies.
 
-Modes: default prints the JSON line. `--pmc-workload` runs only the dominant kernel and a
+Modes: default prints the JSON line. `--e2e-only` runs only the end-to-end generation (for a
+kernel trace of it). `--pmc-workload` runs only the dominant kernel and a
 256 MiB copy (for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`); `--traffic-from DIR`
 turns two such rocprofv3 CSV outputs into profiles/traffic_decode_gate_up_m1.json.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--bits-sweep] [--no-cpu]
+       [--no-prefill] [--no-e2e] [--e2e-only]
 """
 
 from __future__ import annotations
@@ -82,6 +88,7 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Llama-3-8B generation")
+    p.add_argument("--e2e-only", action="store_true", help="only the end-to-end generation (for profiling)")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--pmc-workload", action="store_true", help="only the dominant kernel + a copy")
     p.add_argument("--traffic-from", type=str, default=None, help="rocprofv3 --pmc output dir")
@@ -177,6 +184,9 @@ def main() -> int:
     _lib.load_library()
     torch.cuda.set_device(0)
     bf16 = torch.bfloat16
+    if args.e2e_only:
+        print(json.dumps({"e2e": end_to_end(torch)}), flush=True)
+        return 0
 
     layer_bytes = sum(algorithmic_bytes(0, n, k) for _, n, k in PROJECTIONS)
     copies = max(2, -(-MIN_ROTATION_BYTES // layer_bytes))
