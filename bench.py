@@ -346,16 +346,21 @@ def prefill(torch, ops, rotations):
             "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "bound": "mfma", "dense_comparator": dense}
 
 
-def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128):
+def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128, ref_steps: int = 16):
     """Llama-3-8B (random init, every decoder linear W4 g128 asymmetric RTN, fused q/k/v and
     gate/up), 32 seeded prompts of 512 tokens, then 128 greedy steps through the paged cache
     (block 16). Prefill: one forward over all prompts (the reference's torch sequence for the
-    prefill attention). Decode: each step one HIP-graph replay; tokens/s over steps 2..127."""
-    from llmopt.model import GreedyGenerator, ModelConfig, random_quantized_model
+    prefill attention). Decode: each step one HIP-graph replay; tokens/s over steps 2..127.
+    Beside it, the reference's way on the same GPU (`reference_twin`: dense bf16 linears holding
+    the dequantized weights, torch norms / rotary / attention over the gathered cache, eager
+    steps as the reference's engine runs them) for `ref_steps` steps."""
+    from llmopt.model import GreedyGenerator, ModelConfig, fuse_projections_, random_quantized_model, reference_twin
 
     cfg = ModelConfig.llama3_8b()
     t0 = time.perf_counter()
-    model = random_quantized_model(cfg, device="cuda:0", dtype=torch.bfloat16, seed=0)
+    model = random_quantized_model(cfg, device="cuda:0", dtype=torch.bfloat16, seed=0, fuse=False)
+    ref = reference_twin(model)
+    fuse_projections_(model)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
     prompts = torch.randint(0, cfg.vocab_size, (seqs, prompt_len), generator=torch.Generator().manual_seed(1))
@@ -364,6 +369,12 @@ def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128):
     res = gen.generate(prompts, steps)
     step_ms = res.decode_seconds / (steps - 2) * 1e3
     packed = sum(b.numel() * b.element_size() for n, b in model.named_buffers() if "rotary" not in n)
+    ref_gen = GreedyGenerator(ref, block_size=16, use_graph=False)
+    ref_gen.generate(prompts[:, :32], 4)
+    ref_res = ref_gen.generate(prompts, ref_steps)
+    # Random-init weights give nearly flat logits, so greedy tokens part ways on rounding noise;
+    # the logits themselves are what to compare.
+    diff = float((res.prefill_logits - ref_res.prefill_logits).abs().max() / ref_res.prefill_logits.abs().max())
     out = {
         "workload": f"llama3-8b, {seqs} prompts x {prompt_len} tokens, then {steps} greedy steps, W4 g128 asym "
                     "RTN linears (fused qkv and gate_up), bf16, paged KV block 16",
@@ -373,10 +384,20 @@ def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128):
         "prefill_ms": round(res.prefill_seconds * 1e3, 1),
         "packed_linear_bytes": packed,
         "model_build_s": round(build_s, 2),
+        "reference_way": {
+            "how": "dense bf16 F.linear on the dequantized weights, torch norms/rotary/attention over the "
+                   f"gathered cache, eager steps; {ref_steps} steps",
+            "decode_tokens_per_s": round(ref_res.decode_tokens_per_second, 1),
+            "decode_step_ms": round(ref_res.decode_seconds / (ref_steps - 2) * 1e3, 3),
+            "prefill_tokens_per_s": round(seqs * prompt_len / ref_res.prefill_seconds, 1),
+            "prefill_logits_max_abs_rel_diff": round(diff, 5),
+        },
     }
     print(f"# e2e llama3-8b: prefill {out['prefill_ms']} ms ({out['prefill_tokens_per_s']:.0f} tok/s), decode "
-          f"{step_ms:.2f} ms/step ({out['decode_tokens_per_s']:.0f} tok/s)", file=sys.stderr, flush=True)
-    del model, gen, res
+          f"{step_ms:.2f} ms/step ({out['decode_tokens_per_s']:.0f} tok/s); the reference's way: decode "
+          f"{out['reference_way']['decode_step_ms']:.2f} ms/step, prefill "
+          f"{out['reference_way']['prefill_tokens_per_s']:.0f} tok/s", file=sys.stderr, flush=True)
+    del model, ref, gen, ref_gen, res, ref_res
     torch.cuda.empty_cache()
     return out
 

@@ -37,6 +37,7 @@ class RMSNorm(nn.Module):
         super().__init__()
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.fused_ops = True  # False: always the torch sequence (a reference-style comparator)
 
     def _reference(self, x: torch.Tensor) -> torch.Tensor:
         x32 = x.to(torch.float32)
@@ -44,7 +45,7 @@ class RMSNorm(nn.Module):
         return (x32 * inv * self.weight.to(torch.float32)).to(x.dtype)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if _hip(x):
+        if self.fused_ops and _hip(x):
             from llmopt.kernels import ops
 
             if ops.rmsnorm_supported(x, self.weight):
@@ -54,7 +55,7 @@ class RMSNorm(nn.Module):
     def add_forward(self, x: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """``(norm(h), h)`` with ``h = residual + x``: the residual add and the norm after it
         (``layers.py:185-195``), one kernel on HIP devices."""
-        if _hip(x):
+        if self.fused_ops and _hip(x):
             from llmopt.kernels import ops
 
             if ops.rmsnorm_supported(x, self.weight, residual):
@@ -115,6 +116,7 @@ class PagedAttentionLayer(nn.Module):
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, hidden, bias=False)
         self.qkv_proj: FusedQuantLinear | None = None
         self.rotary = RotaryEmbedding(self.head_dim, config.max_position_embeddings, config.rope_theta)
+        self.fused_ops = True  # False: the torch rotary sequence even on HIP devices
         self.attn = PagedAttention(self.num_heads, self.num_kv_heads, self.head_dim,
                                    config=PagedAttentionConfig(block_size=16), backend=backend)
 
@@ -142,7 +144,7 @@ class PagedAttentionLayer(nn.Module):
         q, k, v = self._project(hidden)
         # Token-major [seq, q_len, heads, head_dim]: the cache layout, and cos/sin broadcast
         # over the heads of each token.
-        if _hip(q):
+        if self.fused_ops and _hip(q):
             from llmopt.kernels import ops
 
             self.rotary.check(positions)

@@ -22,7 +22,7 @@ from llmopt.logits import last_token_hidden
 from llmopt.model.config import ModelConfig
 from llmopt.model.layers import DecoderLayer, RMSNorm
 
-__all__ = ["DecoderOnlyModel", "ModelOutput", "fuse_projections_", "random_quantized_model"]
+__all__ = ["DecoderOnlyModel", "ModelOutput", "fuse_projections_", "random_quantized_model", "reference_twin"]
 
 
 @dataclass
@@ -139,3 +139,42 @@ def random_quantized_model(config: ModelConfig, *, device: torch.device | str, d
     if fuse:
         fuse_projections_(model)
     return model.eval()
+
+
+@torch.no_grad()
+def reference_twin(model: DecoderOnlyModel) -> DecoderOnlyModel:
+    """A copy of an unfused quantized ``model`` that computes the way the reference does: each
+    ``QuantLinear`` becomes a dense ``nn.Linear`` holding its dequantized weight (what the
+    reference's ``QuantLinear`` caches and multiplies, ``quant_linear.py:93-113``), norms and
+    rotary run the torch sequences, attention the torch sequence over the gathered cache
+    (backend ``"sdpa"``). For measuring the reference's approach on the same device."""
+    import copy
+
+    from llmopt.attention.paged_attention import PagedAttention, PagedAttentionConfig
+    from llmopt.quantization.quant_linear import QuantLinear
+    from llmopt.quantization.quantizers import dequantize
+
+    twin = copy.deepcopy(model)
+    swaps = []
+    for parent in twin.modules():
+        for name, child in parent.named_children():
+            if isinstance(child, QuantLinear):
+                swaps.append((parent, name, child))
+            elif name in ("qkv_proj", "gate_up") and child is not None:
+                raise ValueError("reference_twin needs the unfused model (build it before fuse_projections_)")
+    for parent, name, child in swaps:
+        dense = nn.Linear(child.in_features, child.out_features, bias=child.bias is not None,
+                          device="meta")
+        dense.weight = nn.Parameter(dequantize(child.quantized_tensor(), child.config.compute_dtype),
+                                    requires_grad=False)
+        if child.bias is not None:
+            dense.bias = nn.Parameter(child.bias.detach().clone(), requires_grad=False)
+        setattr(parent, name, dense)
+    for module in twin.modules():
+        if hasattr(module, "fused_ops"):
+            module.fused_ops = False
+        if isinstance(module, DecoderLayer):
+            attn = module.self_attn
+            attn.attn = PagedAttention(attn.num_heads, attn.num_kv_heads, attn.head_dim,
+                                       config=PagedAttentionConfig(block_size=16), backend="sdpa")
+    return twin

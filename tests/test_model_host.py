@@ -154,3 +154,20 @@ def test_quantize_model_then_fuse_on_a_dense_model():
     assert fuse_projections_(model) == 4
     layer = next(m for m in model.modules() if isinstance(m, DecoderLayer))
     assert not hasattr(layer.self_attn, "q_proj") and not hasattr(layer.mlp, "gate_proj")
+
+
+def test_reference_twin_computes_the_same_model_densely():
+    from llmopt.model import reference_twin
+
+    model = random_quantized_model(ModelConfig.tiny(), device="cpu", dtype=torch.float32, seed=2, fuse=False)
+    twin = reference_twin(model)
+    assert type(twin.layers[0].self_attn.q_proj) is torch.nn.Linear
+    assert not twin.layers[0].input_layernorm.fused_ops and twin.layers[0].self_attn.attn.backend == "sdpa"
+    fuse_projections_(model)
+    with pytest.raises(ValueError):
+        reference_twin(model)
+    prompts = torch.randint(0, 512, (2, 11), generator=torch.Generator().manual_seed(9))
+    a = GreedyGenerator(model).generate(prompts, 4)
+    b = GreedyGenerator(twin).generate(prompts, 4)
+    assert torch.equal(a.tokens, b.tokens)
+    assert torch.allclose(a.prefill_logits, b.prefill_logits, rtol=1e-5, atol=1e-6)
