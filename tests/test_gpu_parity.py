@@ -207,9 +207,11 @@ def test_linear_batched_decode_shapes(dtype, symmetric, m):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m", [20, 32])
-def test_linear_batched_decode_ring_configuration(dtype, m):
-    # 512 tiles of 16 features at M = 17-32: the four-tile workgroups with a ring of refills.
-    qt = _host_qt(8192, 4096, 4, 128, False, seed=m)
+@pytest.mark.parametrize("n", [6144, 16384])
+def test_linear_batched_decode_ring_configuration(dtype, m, n):
+    # M = 17-32 with rings of refills: 384 tiles of 16 features on two-wave, two-tile
+    # workgroups; 1024 tiles on four-wave, four-tile workgroups.
+    qt = _host_qt(n, 4096, 4, 128, False, seed=m)
     x = torch.randn(m, 4096, generator=torch.Generator().manual_seed(m)).to(dtype)
     y = ops.quant_linear(x.to(DEV), _to_device(qt), None, dtype)
     assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), None, dtype)) <= TOL[dtype]
