@@ -958,6 +958,233 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WP
   }
 }
 
+// ---- N-split kernel (5..32 tokens, many tiles) -------------------------------------------------
+//
+// One workgroup owns NW * NT tiles of 16 output features, NT per wave, and all of K: no
+// reduction across waves. Each wave streams its tiles' codes through a register ring of R * C
+// steps.
+// The activations of C steps at a time are fetched once per workgroup, arranged into MFMA
+// operand order, summed per token (the zero-point term: one MFMA chain against ones per step
+// and token block, instead of one per wave) and staged in LDS, double-buffered with one barrier
+// per C steps. Piece ((mb * 4 + kq) * 4 + j) * 16 + col of a step holds x[16 mb + col][32 kq +
+// 8 j .. + 8], which lane (col, kq) of every wave reads as fragment j. The staging waves hold
+// whole token blocks: wave w fetches pieces (kPer * w + e) * 64 + lane, e < kPer, kPer a
+// multiple of 4, so pieces e = 4p .. 4p+3 are the four k-quarters of one (step, token block)
+// and lane j * 16 + col of each is row col, k-slice j of an MFMA operand. Arithmetic as in the
+// multi-tile kernel.
+template <class Act, int MB, int NT, int NW, int C, int R>
+__global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, uint32_t group_magic) {
+  using Raw = typename Act::raw;
+  constexpr int kStepPieces = MB * 256;             // 16-byte activation pieces per step
+  constexpr int kChunk = C * kStepPieces;           // pieces per chunk
+  constexpr int kPer = kChunk / (NW * 64);          // pieces per thread per chunk
+  static_assert(kPer * NW * 64 == kChunk && kPer % 4 == 0, "whole token blocks per wave");
+  extern __shared__ u32x4 lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;
+  const int kq = lane >> 4;
+  const int64_t n0 = int64_t(blockIdx.x) * (16 * NT * NW);
+  const bool asym = !a.symmetric;
+  const int G = int(a.G);
+  const int steps = int(a.K / 128);
+  const int mstride = G + 2;
+  f32x2* const sz_lds = reinterpret_cast<f32x2*>(lds);
+  u32x4* const xbuf = lds + (16 * NT * NW * mstride * 8 + 15) / 16;  // [2][kChunk] pieces
+  float* const xs_lds = reinterpret_cast<float*>(xbuf + 2 * kChunk);  // [2][C][MB][16] sums
+
+  // ---- activations: this thread's pieces of a chunk ----
+  const uint32_t xbytes = uint32_t(a.M * a.ldx * 2);
+  const auto xr = make_rsrc(a.x, xbytes);
+  uint32_t xoff[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int q = ((kPer * wave + e) * 64 + lane) % kStepPieces;
+    const int64_t row = 16 * (q >> 8) + (q & 15);
+    // Token rows past M read past the end of x: the buffer returns zeros.
+    xoff[e] = row < a.M ? uint32_t(row * a.ldx * 2 + 64 * ((q >> 6) & 3) + 16 * ((q >> 4) & 3)) : xbytes;
+  }
+  u32x4 xreg[kPer];
+  auto load_x = [&](int chunk) {
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      int step = chunk * C + ((kPer * wave + e) * 64) / kStepPieces;
+      step = step < steps ? step : steps - 1;
+      xreg[e] = buf_load16(xr, xoff[e], uint32_t(step) * 256);
+    }
+  };
+  const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  auto store_x = [&](int buf) {
+    u32x4* dst = xbuf + buf * kChunk;
+#pragma unroll
+    for (int p = 0; p < kPer / 4; ++p) {
+      f32x4 sum = zero4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 4 * p + i;
+        const u32x4 v = arrange<Act, kNibble>(xreg[e]);
+        dst[(kPer * wave + e) * 64 + lane] = v;
+        sum = Mfma16<Act>::run(v, ones, sum);
+      }
+      // Lane (c, r4) holds the sums of tokens 4 r4 .. 4 r4 + 3 of this (step, token block),
+      // whose index within the chunk is (kPer * wave + 4 p) / 4.
+      if (col == 0)
+        *reinterpret_cast<f32x4*>(xs_lds + (buf * C * MB + (kPer * wave + 4 * p) / 4) * 16 + 4 * kq) = sum;
+    }
+  };
+
+  // ---- the wave's codes: a ring of R * C steps over its NT tiles ----
+  const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
+  uint32_t qoff[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    int64_t n = n0 + 16 * (wave * NT + t) + col;
+    n = n < a.N ? n : a.N - 1;  // rows past N repeat row N-1; their sums are never stored
+    qoff[t] = uint32_t(n * a.ldq + 16 * kq);
+  }
+  u32x4 cw[R * C][NT];
+  auto load_codes = [&](int slot, int step) {
+    const uint32_t so = uint32_t(step < steps ? step : steps - 1) * 64;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) cw[slot][t] = buf_load16(wq, qoff[t], so);
+  };
+
+  // ---- prologue: loads of chunk 0 and the first R * C steps of codes, then the metadata of rows
+  //      n0 .. n0 + 16 NT NW - 1 (one contiguous run of the [N, G] tensors) into LDS ----
+  load_x(0);
+#pragma unroll
+  for (int u = 0; u < R * C; ++u) load_codes(u, u);
+  const uint32_t meta_bytes = uint32_t(a.N * a.G * 4);
+  const auto ms = make_rsrc(a.scales, meta_bytes);
+  const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_bytes);
+  const int pieces = 16 * NT * NW * G / 4;  // G % 4 == 0 (host check)
+  const uint32_t mbase = uint32_t(n0 * a.G * 4);
+  const float z_shift = Act::kNibbleOffset;
+  const float z_const = a.zero_const + z_shift;
+  for (int p = tid; p < pieces; p += NW * 64) {
+    const uint32_t off = mbase + uint32_t(p) * 16;  // rows past N: past the tensors, zeros
+    const f32x4 sf = __builtin_bit_cast(f32x4, buf_load16(ms, off, 0));
+    const f32x4 zf = __builtin_bit_cast(f32x4, buf_load16(mz, off, 0));
+    const int row = (p * 4) / G;
+    const int g = p * 4 - row * G;
+    // Symmetric codes use the constant offset, so the arithmetic below never branches.
+    f32x4 lo, hi;
+    lo[0] = sf[0]; lo[1] = asym ? zf[0] + z_shift : z_const;
+    lo[2] = sf[1]; lo[3] = asym ? zf[1] + z_shift : z_const;
+    hi[0] = sf[2]; hi[1] = asym ? zf[2] + z_shift : z_const;
+    hi[2] = sf[3]; hi[3] = asym ? zf[3] + z_shift : z_const;
+    *reinterpret_cast<f32x4*>(sz_lds + row * mstride + g) = lo;
+    *reinterpret_cast<f32x4*>(sz_lds + row * mstride + g + 2) = hi;
+  }
+  store_x(0);
+  __syncthreads();
+
+  const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
+  f32x4 tot[NT][MB];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) tot[t][mb] = zero4;
+  const f32x2* const sz_row = sz_lds + (16 * wave * NT + col) * mstride;
+
+  // Chunk c reads buffer c % 2 while the registers fetch chunk c + 1 (the last chunk again at
+  // the end, so that the loads keep one static order); they go to the other buffer, last read
+  // during chunk c - 1, which the barrier at the end of chunk c - 1 has released. R chunks at a
+  // time, so that every ring slot index is a constant.
+  const int chunks = steps / C;  // steps % (R * C) == 0 (host check)
+  for (int c0 = 0; c0 < chunks; c0 += R)
+#pragma unroll
+  for (int rr = 0; rr < R; ++rr) {
+    const int c = c0 + rr;
+    load_x(c + 1 < chunks ? c + 1 : c);
+    const u32x4* xb = xbuf + (c & 1) * kChunk;
+    const float* xsb = xs_lds + (c & 1) * (C * MB * 16);
+#pragma unroll
+    for (int u = 0; u < C; ++u) {
+      const int step = c * C + u;
+      const int g = int(div_small(uint32_t(step), group_magic));
+      u32x4 xa[MB][4];
+      f32x4 xs[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xa[mb][j] = xb[u * kStepPieces + ((mb * 4 + kq) * 4 + j) * 16 + col];
+        xs[mb] = *reinterpret_cast<const f32x4*>(xsb + (u * MB + mb) * 16 + 4 * kq);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f32x2 sz = sz_row[16 * t * mstride + g];
+        const u32x4 q = cw[rr * C + u][t];
+        const u32x4 b[4] = {nib.operand(q.x), nib.operand(q.y), nib.operand(q.z), nib.operand(q.w)};
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          f32x4 acc = Mfma16<Act>::run(xa[mb][0], b[0], zero4);
+#pragma unroll
+          for (int j = 1; j < 4; ++j) acc = Mfma16<Act>::run(xa[mb][j], b[j], acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            tot[t][mb][r] = __builtin_fmaf(sz[0], __builtin_fmaf(-sz[1], xs[mb][r], acc[r]), tot[t][mb][r]);
+        }
+      }
+      load_codes(rr * C + u, step + R * C);
+    }
+    store_x((c + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- lane (col, kq) holds tokens 16 mb + 4 kq + r of feature n0 + 16 (wave NT + t) + col ----
+  const Raw* bias = static_cast<const Raw*>(a.bias);
+  Raw* y = static_cast<Raw*>(a.y);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int64_t nn = n0 + 16 * (wave * NT + t) + col;
+    const float b0 = (bias && nn < a.N) ? Act::load(bias[nn]) : 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = 16 * mb + 4 * kq + r;
+        const float v = tot[t][mb][r] + b0;
+        if (a.epilogue == kEpiSwiglu) {
+          // Gate rows 8p .. 8p+3 and up rows 8p+4 .. 8p+7 sit four lanes apart (N % 8 == 0).
+          const float up = __shfl_xor(v, 4, 64);
+          if (m < a.M && nn < a.N && (nn & 4) == 0)
+            y[m * a.ldy + (nn >> 3) * 4 + (nn & 3)] = Act::store(swiglu<Act>(v, up));
+        } else if (m < a.M && nn < a.N) {
+          y[m * a.ldy + nn] = Act::store(v);
+        }
+      }
+  }
+}
+
+// Fewest tokens for which the N-split kernel beats the multi-tile one on large grids.
+constexpr int64_t kNxMinTokens = 5;
+
+template <int MB, int NT, int NW, int C>
+constexpr size_t nx_lds_bytes(int64_t G) {
+  return size_t((16 * NT * NW * (G + 2) * 8 + 15) / 16) * 16 + size_t(2) * C * MB * 256 * 16 +
+         size_t(2) * C * MB * 16 * 4;
+}
+
+template <class Act, int MB, int NT, int NW, int C, int R>
+hipError_t launch_nx_cfg(const LinearArgs& a, uint32_t magic, hipStream_t stream) {
+  const int64_t steps = a.K / 128;
+  if (a.M > 16 * MB || steps % (R * C) != 0 || steps < R * C) return hipErrorInvalidValue;
+  const size_t lds = nx_lds_bytes<MB, NT, NW, C>(a.G);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  auto kern = decode_nx_kernel<Act, MB, NT, NW, C, R>;
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (e != hipSuccess) return e;
+  }
+  const int64_t blocks = ((a.N + 15) / 16 + NT * NW - 1) / (NT * NW);
+  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(NW * 64), lds, stream, a, magic);
+  return hipGetLastError();
+}
+
 // ---- dispatch ----------------------------------------------------------------------------------
 
 template <class Act, int FMT, int CB, int MB, int NT, int NW>
@@ -1199,6 +1426,23 @@ MtConfig pick_mt(const LinearArgs& a, int64_t steps) {
   return MtConfig{2, 4, 2, 8};
 }
 
+// 5 .. 32 tokens over at least 1024 output tiles (gate_up): the N-split kernel, eight waves of
+// one tile each per workgroup, activations shared through LDS (gate_up at M = 8 / 16 / 24 / 32:
+// 22.1 / 24.6 / 30.6 / 33.9 -> 17.9 / 19.3 / 21.5 / 22.6 us). Smaller grids keep the multi-tile
+// kernel: eight tiles per workgroup leave too few workgroups to fill the chip.
+template <class Act>
+bool try_nx(const LinearArgs& a, int64_t steps, uint32_t magic, hipStream_t stream, hipError_t* err) {
+  if (a.M < kNxMinTokens || a.M > 32 || (a.N + 15) / 16 < 1024) return false;
+  if (a.M <= 16) {
+    if (steps % 8 != 0 || nx_lds_bytes<1, 1, 8, 8>(a.G) > 160 * 1024) return false;
+    *err = launch_nx_cfg<Act, 1, 1, 8, 8, 1>(a, magic, stream);
+  } else {
+    if (steps % 4 != 0 || nx_lds_bytes<2, 1, 8, 4>(a.G) > 160 * 1024) return false;
+    *err = launch_nx_cfg<Act, 2, 1, 8, 4, 1>(a, magic, stream);
+  }
+  return true;
+}
+
 // M <= 64, 2/4-bit codes, groups of a multiple of 128 codes: the multi-tile kernel.
 bool try_mt(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.fmt != kNibble || a.M < 1 || a.M > 64) return false;
@@ -1210,14 +1454,17 @@ bool try_mt(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.M * a.ldx * 2 >= (int64_t(1) << 31) || a.K * 2 >= (int64_t(1) << 31)) return false;
   if ((a.N + 15) / 16 > 0x7FFFFFFF) return false;
   const int64_t steps = a.K / 128;
+  const uint32_t per_group = uint32_t(a.group / 128);
+  const uint32_t magic = per_group == 1 ? 0u
+      : uint32_t((uint64_t(1) << 32) / per_group + ((uint64_t(1) << 32) % per_group != 0));
+  if (a.act == kDtBf16 ? try_nx<ActBf16>(a, steps, magic, stream, err)
+                       : try_nx<ActF16>(a, steps, magic, stream, err))
+    return true;
   const MtConfig c = pick_mt(a, steps);
   if (c.nt == 0 || steps % c.nw != 0) return false;
   // The metadata block of the workgroup must fit in LDS, and its loads in two per thread.
   if (size_t(16) * c.nt * (a.G + 2) * 8 > 160 * 1024) return false;
   if (int64_t(16) * c.nt * a.G / 4 > int64_t(kMtMetaPer) * c.nw * 64) return false;
-  const uint32_t per_group = uint32_t(a.group / 128);
-  const uint32_t magic = per_group == 1 ? 0u
-      : uint32_t((uint64_t(1) << 32) / per_group + ((uint64_t(1) << 32) % per_group != 0));
   *err = a.act == kDtBf16 ? launch_mt<ActBf16>(a, c, int(steps), magic, stream)
                           : launch_mt<ActF16>(a, c, int(steps), magic, stream);
   return true;

@@ -209,12 +209,27 @@ def test_linear_batched_decode_shapes(dtype, symmetric, m):
 @pytest.mark.parametrize("m", [20, 32])
 @pytest.mark.parametrize("n", [6144, 16384])
 def test_linear_batched_decode_ring_configuration(dtype, m, n):
-    # M = 17-32 with rings of refills: 384 tiles of 16 features on two-wave, two-tile
-    # workgroups; 1024 tiles on four-wave, four-tile workgroups.
+    # M = 17-32: 384 tiles of 16 features on two-wave, two-tile workgroups; 1024 tiles on
+    # eight-wave workgroups of one tile per wave.
     qt = _host_qt(n, 4096, 4, 128, False, seed=m)
     x = torch.randn(m, 4096, generator=torch.Generator().manual_seed(m)).to(dtype)
     y = ops.quant_linear(x.to(DEV), _to_device(qt), None, dtype)
     assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), None, dtype)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [5, 8, 16, 17, 32])
+@pytest.mark.parametrize("n, group, symmetric", [(16400, 128, False), (16384, 256, True)])
+def test_linear_n_split_decode(dtype, m, n, group, symmetric):
+    # 5-32 tokens over at least 1024 tiles of 16 features: eight single-tile waves per
+    # workgroup sharing the activations through LDS. N = 16400 leaves the last workgroup one
+    # live tile (rows past N); groups of 256 codes span two steps; bias on.
+    qt = _host_qt(n, 4096, 4, group, symmetric, seed=m + n)
+    gen = torch.Generator().manual_seed(m)
+    x = torch.randn(m, 4096, generator=gen).to(dtype)
+    bias = torch.randn(n, generator=gen).to(dtype)
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), bias.to(DEV), dtype)
+    assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), bias, dtype)) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
