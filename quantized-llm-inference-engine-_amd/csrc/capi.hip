@@ -6,6 +6,7 @@
 // shapes that one does not take, and the generic kernel for shapes, alignments or dtypes the
 // fast kernels do not take. Error text is kept per host thread.
 #include <stdarg.h>
+#include <algorithm>
 #include <stdio.h>
 
 #include <string>
@@ -158,9 +159,13 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
   switch (algo) {
     case LLMOPT_ALGO_AUTO: {
       bool gemm = gemm_first(M, K);
-      if (gemm && M <= kDecodeMaxTokens) {  // worth it only with its K split
+      if (gemm && M <= kDecodeMaxTokens) {
+        // The decode path's K-split kernel first, then the GEMM, which is worth it only with
+        // its own K split; each needs its workspace.
+        const size_t nx = llmopt::nx_split_workspace_bytes(M, N, K, a.group, bits);
         const size_t need = llmopt::gemm_workspace_bytes(M, N, K, a.group, a.fmt);
-        gemm = need > 0 && a.workspace != nullptr && a.workspace_bytes >= need;
+        const bool ws_nx = nx > 0 && a.workspace != nullptr && a.workspace_bytes >= nx;
+        gemm = !ws_nx && need > 0 && a.workspace != nullptr && a.workspace_bytes >= need;
       }
       if (!gemm) {
         err = llmopt::launch_linear_decode(a, s, &fits);
@@ -265,10 +270,13 @@ int llmopt_q_quantize_rtn(const void* weight, int w_dtype, int64_t ldw, int64_t 
 }
 
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
-  // Only the GEMM splits K; the decode kernels reduce in LDS.
-  if (!gemm_first(M, K) || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
+  // The GEMM's K split, and the decode path's K-split kernel at 5-32 tokens on grids of fewer
+  // than 1024 tiles of 16 features; the other decode kernels reduce in LDS.
+  if (M <= 0 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
   const int64_t g = group_size <= 0 ? K : group_size;
-  return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
+  const size_t nx = M <= kDecodeMaxTokens ? llmopt::nx_split_workspace_bytes(M, N, K, g, bits) : 0;
+  if (!gemm_first(M, K)) return nx;
+  return std::max(nx, llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble));
 }
 
 int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,

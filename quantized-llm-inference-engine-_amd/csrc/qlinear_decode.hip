@@ -18,6 +18,8 @@
 //     sum_k (q_k - z) s x_k = s * (sum_k (OFF + q_k) x_k - (OFF + z) * sum_k x_k)
 // where sum_k x_k comes from one extra MFMA against a ones operand. The codes land in the
 // operand in the order (k0,k4,k1,k5,k2,k6,k3,k7); the activations are permuted to match.
+#include <algorithm>
+
 #include "qcommon.hpp"
 #include "qkernels.hpp"
 
@@ -972,8 +974,13 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WP
 // multiple of 4, so pieces e = 4p .. 4p+3 are the four k-quarters of one (step, token block)
 // and lane j * 16 + col of each is row col, k-slice j of an MFMA operand. Arithmetic as in the
 // multi-tile kernel.
+//
+// With `partials`, workgroup (x, y) covers steps [y * split_steps, (y + 1) * split_steps) only,
+// stages the metadata of that slice's groups and writes its fp32 sums, without bias or
+// activation, to partials[y][m][n] for the fixed-order reduction kernel.
 template <class Act, int MB, int NT, int NW, int C, int R>
-__global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, uint32_t group_magic) {
+__global__ void __launch_bounds__(NW * 64)
+    decode_nx_kernel(const LinearArgs a, uint32_t group_magic, int split_steps, float* partials) {
   using Raw = typename Act::raw;
   constexpr int kStepPieces = MB * 256;             // 16-byte activation pieces per step
   constexpr int kChunk = C * kStepPieces;           // pieces per chunk
@@ -988,8 +995,12 @@ __global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, 
   const int64_t n0 = int64_t(blockIdx.x) * (16 * NT * NW);
   const bool asym = !a.symmetric;
   const int G = int(a.G);
-  const int steps = int(a.K / 128);
-  const int mstride = G + 2;
+  const int s0 = int(blockIdx.y) * split_steps;  // this workgroup's K slice: steps s0 .. s_end - 1
+  const int s_end = s0 + split_steps;
+  // Groups g0 .. g0 + gs - 1 of the slice; rows of gs + 2 pairs in LDS.
+  const int g0 = partials ? int(div_small(uint32_t(s0), group_magic)) : 0;
+  const int gs = partials ? int(div_small(uint32_t(s_end - 1), group_magic)) + 1 - g0 : G;
+  const int mstride = gs + 2;
   f32x2* const sz_lds = reinterpret_cast<f32x2*>(lds);
   u32x4* const xbuf = lds + (16 * NT * NW * mstride * 8 + 15) / 16;  // [2][kChunk] pieces
   float* const xs_lds = reinterpret_cast<float*>(xbuf + 2 * kChunk);  // [2][C][MB][16] sums
@@ -1009,8 +1020,8 @@ __global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, 
   auto load_x = [&](int chunk) {
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-      int step = chunk * C + ((kPer * wave + e) * 64) / kStepPieces;
-      step = step < steps ? step : steps - 1;
+      int step = s0 + chunk * C + ((kPer * wave + e) * 64) / kStepPieces;
+      step = step < s_end ? step : s_end - 1;
       xreg[e] = buf_load16(xr, xoff[e], uint32_t(step) * 256);
     }
   };
@@ -1046,7 +1057,7 @@ __global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, 
   }
   u32x4 cw[R * C][NT];
   auto load_codes = [&](int slot, int step) {
-    const uint32_t so = uint32_t(step < steps ? step : steps - 1) * 64;
+    const uint32_t so = uint32_t(step < s_end ? step : s_end - 1) * 64;
 #pragma unroll
     for (int t = 0; t < NT; ++t) cw[slot][t] = buf_load16(wq, qoff[t], so);
   };
@@ -1055,7 +1066,7 @@ __global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, 
   //      n0 .. n0 + 16 NT NW - 1 (one contiguous run of the [N, G] tensors) into LDS ----
   load_x(0);
 #pragma unroll
-  for (int u = 0; u < R * C; ++u) load_codes(u, u);
+  for (int u = 0; u < R * C; ++u) load_codes(u, s0 + u);
   const uint32_t meta_bytes = uint32_t(a.N * a.G * 4);
   const auto ms = make_rsrc(a.scales, meta_bytes);
   const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_bytes);
@@ -1063,7 +1074,18 @@ __global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, 
   const uint32_t mbase = uint32_t(n0 * a.G * 4);
   const float z_shift = Act::kNibbleOffset;
   const float z_const = a.zero_const + z_shift;
-  for (int p = tid; p < pieces; p += NW * 64) {
+  if (partials) {
+    // The slice's groups: a run of gs floats per row, not 16-byte aligned in general.
+    for (int i = tid; i < 16 * NT * NW * gs; i += NW * 64) {
+      const int row = i / gs;
+      const int gg = i - row * gs;
+      const uint32_t off = uint32_t(((n0 + row) * a.G + g0 + gg) * 4);  // rows past N: zeros
+      const float sc = buf_load_f32(ms, off, 0);
+      const float zr = buf_load_f32(mz, off, 0);
+      sz_lds[row * mstride + gg] = f32x2{sc, asym ? zr + z_shift : z_const};
+    }
+  }
+  for (int p = partials ? pieces : tid; p < pieces; p += NW * 64) {
     const uint32_t off = mbase + uint32_t(p) * 16;  // rows past N: past the tensors, zeros
     const f32x4 sf = __builtin_bit_cast(f32x4, buf_load16(ms, off, 0));
     const f32x4 zf = __builtin_bit_cast(f32x4, buf_load16(mz, off, 0));
@@ -1093,7 +1115,7 @@ __global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, 
   // the end, so that the loads keep one static order); they go to the other buffer, last read
   // during chunk c - 1, which the barrier at the end of chunk c - 1 has released. R chunks at a
   // time, so that every ring slot index is a constant.
-  const int chunks = steps / C;  // steps % (R * C) == 0 (host check)
+  const int chunks = split_steps / C;  // split_steps % (R * C) == 0 (host check)
   for (int c0 = 0; c0 < chunks; c0 += R)
 #pragma unroll
   for (int rr = 0; rr < R; ++rr) {
@@ -1103,8 +1125,8 @@ __global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, 
     const float* xsb = xs_lds + (c & 1) * (C * MB * 16);
 #pragma unroll
     for (int u = 0; u < C; ++u) {
-      const int step = c * C + u;
-      const int g = int(div_small(uint32_t(step), group_magic));
+      const int step = s0 + c * C + u;
+      const int g = int(div_small(uint32_t(step), group_magic)) - g0;
       u32x4 xa[MB][4];
       f32x4 xs[MB];
 #pragma unroll
@@ -1135,6 +1157,21 @@ __global__ void __launch_bounds__(NW * 64) decode_nx_kernel(const LinearArgs a, 
   }
 
   // ---- lane (col, kq) holds tokens 16 mb + 4 kq + r of feature n0 + 16 (wave NT + t) + col ----
+  if (partials) {
+    float* part = partials + size_t(blockIdx.y) * size_t(a.M) * size_t(a.N);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int64_t nn = n0 + 16 * (wave * NT + t) + col;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = 16 * mb + 4 * kq + r;
+          if (m < a.M && nn < a.N) part[m * a.N + nn] = tot[t][mb][r];
+        }
+    }
+    return;
+  }
   const Raw* bias = static_cast<const Raw*>(a.bias);
   Raw* y = static_cast<Raw*>(a.y);
 #pragma unroll
@@ -1168,11 +1205,23 @@ constexpr size_t nx_lds_bytes(int64_t G) {
          size_t(2) * C * MB * 16 * 4;
 }
 
+// splits > 1: K in `splits` equal slices, fp32 partial sums into a.workspace (splits * M * N
+// floats), then the reduction kernel.
 template <class Act, int MB, int NT, int NW, int C, int R>
-hipError_t launch_nx_cfg(const LinearArgs& a, uint32_t magic, hipStream_t stream) {
+hipError_t launch_nx_cfg(const LinearArgs& a, uint32_t magic, hipStream_t stream, int splits = 1) {
   const int64_t steps = a.K / 128;
-  if (a.M > 16 * MB || steps % (R * C) != 0 || steps < R * C) return hipErrorInvalidValue;
-  const size_t lds = nx_lds_bytes<MB, NT, NW, C>(a.G);
+  if (splits < 1 || steps % splits != 0) return hipErrorInvalidValue;
+  const int64_t split_steps = steps / splits;
+  if (a.M > 16 * MB || split_steps % (R * C) != 0 || split_steps < R * C) return hipErrorInvalidValue;
+  float* partials = nullptr;
+  int64_t gs = a.G;
+  if (splits > 1) {
+    if (!a.workspace || a.workspace_bytes < size_t(splits) * a.M * a.N * 4) return hipErrorInvalidValue;
+    partials = static_cast<float*>(a.workspace);
+    const int64_t per_group = a.group / 128;
+    gs = std::min<int64_t>(a.G, (split_steps + per_group - 1) / per_group + 1);
+  }
+  const size_t lds = nx_lds_bytes<MB, NT, NW, C>(gs);
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   auto kern = decode_nx_kernel<Act, MB, NT, NW, C, R>;
   if (lds > 65536) {
@@ -1181,8 +1230,11 @@ hipError_t launch_nx_cfg(const LinearArgs& a, uint32_t magic, hipStream_t stream
     if (e != hipSuccess) return e;
   }
   const int64_t blocks = ((a.N + 15) / 16 + NT * NW - 1) / (NT * NW);
-  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(NW * 64), lds, stream, a, magic);
-  return hipGetLastError();
+  hipLaunchKernelGGL(kern, dim3(unsigned(blocks), unsigned(splits)), dim3(NW * 64), lds, stream, a, magic,
+                     int(split_steps), partials);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  return launch_splitk_reduce(a, partials, splits, stream);
 }
 
 // ---- dispatch ----------------------------------------------------------------------------------
@@ -1430,8 +1482,35 @@ MtConfig pick_mt(const LinearArgs& a, int64_t steps) {
 // one tile each per workgroup, activations shared through LDS (gate_up at M = 8 / 16 / 24 / 32:
 // 22.1 / 24.6 / 30.6 / 33.9 -> 17.9 / 19.3 / 21.5 / 22.6 us). Smaller grids keep the multi-tile
 // kernel: eight tiles per workgroup leave too few workgroups to fill the chip.
+//
+// Smaller grids with long rows (down: K 14336), given a workspace, from 12 tokens: the same
+// kernel over K slices, enough of them for 256 workgroups, then the fixed-order reduction of
+// the slices' fp32 sums (down at M = 16 / 24 / 32: 27.3 / 34.4 / 34.3 -> 24.0 / 25.7 / 26.8 us,
+// the last two against the split-K GEMM). With K = 4096 (qkv, o) the slices are too short to
+// pay for the partial sums and the second launch (M = 32: 14.3 / 12.3 -> 20.8 / 13.7 us).
+int nx_splits(int64_t M, int64_t N, int64_t steps) {
+  if (M < 12 || M > 32 || N % 8 != 0 || steps < 64) return 0;
+  const int64_t tiles = (N + 15) / 16;
+  if (tiles >= 1024) return 0;
+  const int64_t chunks = steps / (M <= 16 ? 8 : 4);
+  if (chunks * (M <= 16 ? 8 : 4) != steps) return 0;
+  const int64_t wgs = (tiles + 7) / 8;
+  for (int64_t s = 2; s <= chunks; ++s)
+    if (chunks % s == 0 && wgs * s >= 256) return int(s);
+  return 0;
+}
+
 template <class Act>
 bool try_nx(const LinearArgs& a, int64_t steps, uint32_t magic, hipStream_t stream, hipError_t* err) {
+  const int splits = nx_splits(a.M, a.N, steps);
+  if (splits > 0) {
+    if (!a.workspace || a.workspace_bytes < size_t(splits) * a.M * a.N * 4 ||
+        reinterpret_cast<uintptr_t>(a.workspace) % 16 != 0)
+      return false;
+    *err = a.M <= 16 ? launch_nx_cfg<Act, 1, 1, 8, 8, 1>(a, magic, stream, splits)
+                     : launch_nx_cfg<Act, 2, 1, 8, 4, 1>(a, magic, stream, splits);
+    return true;
+  }
   if (a.M < kNxMinTokens || a.M > 32 || (a.N + 15) / 16 < 1024) return false;
   if (a.M <= 16) {
     if (steps % 8 != 0 || nx_lds_bytes<1, 1, 8, 8>(a.G) > 160 * 1024) return false;
@@ -1511,6 +1590,13 @@ hipError_t launch_skinny(const LinearArgs& a, hipStream_t stream, bool* fits) {
 
 
 }  // namespace
+
+size_t nx_split_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
+  if (bits != 2 && bits != 4) return 0;
+  if (group % 128 != 0 || K % 128 != 0 || (K / group) % 4 != 0) return 0;
+  const int splits = nx_splits(M, N, K / 128);
+  return splits > 0 ? size_t(splits) * size_t(M) * size_t(N) * 4 : 0;
+}
 
 hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* fits) {
   *fits = false;

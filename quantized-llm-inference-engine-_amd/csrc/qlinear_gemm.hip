@@ -584,6 +584,17 @@ void launch_act(const LinearArgs& a, const GemmPlan& plan, int splits, hipStream
 
 }  // namespace
 
+hipError_t launch_splitk_reduce(const LinearArgs& a, const float* partials, int splits, hipStream_t stream) {
+  const int64_t threads = a.epilogue == kEpiSwiglu ? a.M * (a.N / 8) : a.M * ((a.N + 3) / 4);
+  if (a.act == kDtBf16)
+    hipLaunchKernelGGL(splitk_reduce_kernel<ActBf16>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
+                       a, partials, splits);
+  else
+    hipLaunchKernelGGL(splitk_reduce_kernel<ActF16>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
+                       a, partials, splits);
+  return hipGetLastError();
+}
+
 size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int fmt) {
   return plan_gemm(M, N, K, group, fmt).workspace();
 }

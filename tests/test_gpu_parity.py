@@ -219,17 +219,51 @@ def test_linear_batched_decode_ring_configuration(dtype, m, n):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m", [5, 8, 16, 17, 32])
-@pytest.mark.parametrize("n, group, symmetric", [(16400, 128, False), (16384, 256, True)])
-def test_linear_n_split_decode(dtype, m, n, group, symmetric):
+@pytest.mark.parametrize("n, bits, group, symmetric", [(16400, 4, 128, False), (16384, 4, 256, True),
+                                                     (16384, 2, 128, False)])
+def test_linear_n_split_decode(dtype, m, n, bits, group, symmetric):
     # 5-32 tokens over at least 1024 tiles of 16 features: eight single-tile waves per
     # workgroup sharing the activations through LDS. N = 16400 leaves the last workgroup one
-    # live tile (rows past N); groups of 256 codes span two steps; bias on.
-    qt = _host_qt(n, 4096, 4, group, symmetric, seed=m + n)
+    # live tile (rows past N); groups of 256 codes span two steps; 2-bit codes; bias on.
+    qt = _host_qt(n, 4096, bits, group, symmetric, seed=m + n)
     gen = torch.Generator().manual_seed(m)
     x = torch.randn(m, 4096, generator=gen).to(dtype)
     bias = torch.randn(n, generator=gen).to(dtype)
     y = ops.quant_linear(x.to(DEV), _to_device(qt), bias.to(DEV), dtype)
     assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), bias, dtype)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [5, 12, 17, 32])
+@pytest.mark.parametrize("n, k, group, symmetric", [(6144, 4096, 128, False), (4096, 14336, 128, False),
+                                                   (2048, 8192, 256, True)])
+def test_linear_n_split_over_k_slices(dtype, m, n, k, group, symmetric):
+    # Fewer than 1024 tiles and long rows: the N-split kernel over K slices (fp32 partial sums
+    # in the workspace, then the fixed-order reduction, which adds the bias), and the same call
+    # through the C-ABI without a workspace, which takes the other decode kernels.
+    qt = _host_qt(n, k, 4, group, symmetric, seed=m + k)
+    gen = torch.Generator().manual_seed(m)
+    x = torch.randn(m, k, generator=gen).to(dtype)
+    bias = torch.randn(n, generator=gen).to(dtype)
+    ref = _reference_linear(x, _oracle_dense(qt), bias, dtype)
+    dq = _to_device(qt)
+    xd, bd = x.to(DEV), bias.to(DEV)
+    y = ops.quant_linear(xd, dq, bd, dtype)
+    assert _rel_err(y, ref) <= TOL[dtype]
+    lib = _lib.load_library()
+    # Slices are taken from 12 tokens with K >= 8192, where they give the grid at least 256
+    # workgroups of 8 tiles: down (K 14336) always, K 8192 on 128 tiles from 17 tokens
+    # (chunks of 4 steps instead of 8).
+    splits = m >= 12 and (k == 14336 or (k == 8192 and m >= 17))
+    assert (lib.llmopt_q_linear_workspace(m, n, k, 4, group) > 0) == splits
+    y2 = torch.empty(m, n, dtype=dtype, device=DEV)
+    qw, ldq, sc, zr, _, _, grp, signed = ops._weight_args(dq, xd.device)
+    rc = lib.llmopt_q_linear(xd.data_ptr(), m, k, k, qw.data_ptr(), ldq, sc.data_ptr(),
+                             zr.data_ptr() if zr is not None else None, bd.data_ptr(), y2.data_ptr(), n, n,
+                             _lib.DTYPE_CODES[dtype], 4, grp, int(symmetric), int(signed), None, 0,
+                             torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    assert _rel_err(y2, ref) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
