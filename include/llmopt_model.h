@@ -45,6 +45,23 @@ int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
                 int64_t table_rows, int64_t tokens, int64_t heads, int64_t kv_heads, int64_t head_dim, int dtype,
                 void* stream);
 
+/*
+ * llmopt_rope for a decode step (one token per sequence, tokens = seqs) fused with the cache
+ * write that follows it: the rotated k and the unchanged v go straight into this layer's paged
+ * cache (key_cache / value_cache [num_blocks, block_size, kv_heads, head_dim], of dtype) at the
+ * slot of token_offsets[s] in block block_ids[s, token_offsets[s] / block_size] (int32, row
+ * stride ldb); a block id outside [0, num_blocks) is replaced by block 0, and an offset past the
+ * table row writes nothing. Replaces the rotary step of the attention layer followed by
+ * PagedKVCache.write_decode (src/llmopt/cache/paged_cache.py:246-277), whose results it gives
+ * bit for bit; q_out as in llmopt_rope.
+ */
+int llmopt_rope_kv_write_decode(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                                void* q_out, const int64_t* positions, const float* cos_table,
+                                const float* sin_table, int64_t table_rows, int64_t seqs, int64_t heads,
+                                int64_t kv_heads, int64_t head_dim, int dtype, void* key_cache, void* value_cache,
+                                int64_t num_blocks, int64_t block_size, const int32_t* block_ids, int64_t ldb,
+                                const int32_t* token_offsets, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

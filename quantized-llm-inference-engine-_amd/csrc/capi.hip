@@ -574,4 +574,48 @@ int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
   return hip_status(llmopt::launch_rope(a, static_cast<hipStream_t>(stream)), "rope launch");
 }
 
+int llmopt_rope_kv_write_decode(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                                void* q_out, const int64_t* positions, const float* cos_table,
+                                const float* sin_table, int64_t table_rows, int64_t seqs, int64_t heads,
+                                int64_t kv_heads, int64_t head_dim, int dtype, void* key_cache, void* value_cache,
+                                int64_t num_blocks, int64_t block_size, const int32_t* block_ids, int64_t ldb,
+                                const int32_t* token_offsets, void* stream) {
+  if (dtype != LLMOPT_DTYPE_BF16 && dtype != LLMOPT_DTYPE_F16)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "rope kernel: dtype %d (bf16 and fp16 only)", dtype);
+  if (seqs < 0 || seqs > 0x7FFFFFFF || heads < 1 || kv_heads < 1 || head_dim < 2 || head_dim % 2 ||
+      table_rows < 1 || num_blocks < 1 || block_size < 1 || ldb < 1)
+    return fail(LLMOPT_ERR_INVALID_ARG, "bad rope / cache shape");
+  if (seqs == 0) return LLMOPT_OK;
+  if (!q || !k || !v || !q_out || !positions || !cos_table || !sin_table || !key_cache || !value_cache ||
+      !block_ids || !token_offsets)
+    return fail(LLMOPT_ERR_INVALID_ARG, "null rope / cache pointer");
+  if (ldq < heads * head_dim || ldk < kv_heads * head_dim || ldv < kv_heads * head_dim)
+    return fail(LLMOPT_ERR_INVALID_ARG, "rope token stride below heads x head_dim");
+  llmopt::RopeArgs a{};
+  a.q = q;
+  a.k = k;
+  a.q_out = q_out;
+  a.v = v;
+  a.ldv = ldv;
+  a.positions = positions;
+  a.cos_table = cos_table;
+  a.sin_table = sin_table;
+  a.table_rows = table_rows;
+  a.tokens = seqs;
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.ldq = ldq;
+  a.ldk = ldk;
+  a.dtype = dtype;
+  a.key_cache = key_cache;
+  a.value_cache = value_cache;
+  a.block_ids = block_ids;
+  a.offsets = token_offsets;
+  a.ldb = ldb;
+  a.num_blocks = num_blocks;
+  a.block_size = block_size;
+  return hip_status(llmopt::launch_rope(a, static_cast<hipStream_t>(stream)), "rope launch");
+}
+
 }  // extern "C"

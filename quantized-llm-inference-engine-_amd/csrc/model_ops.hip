@@ -102,6 +102,19 @@ __global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
   const int64_t hh = is_q ? head : head - a.heads;
   const Raw* src = static_cast<const Raw*>(is_q ? a.q : a.k) + t * (is_q ? a.ldq : a.ldk) + hh * a.head_dim;
   Raw* dst = static_cast<Raw*>(is_q ? a.q_out : a.k_out) + (t * (is_q ? a.heads : a.kv_heads) + hh) * a.head_dim;
+  Raw* vd = a.v_out ? static_cast<Raw*>(a.v_out) + (t * a.kv_heads + hh) * a.head_dim : nullptr;
+  if (!is_q && a.key_cache) {
+    // The decode cache write (paged_cache.py:246-277): block block_ids[t, off / B], replaced by
+    // block 0 outside [0, num_blocks); an offset past the table row writes nothing.
+    const int64_t off = a.offsets[t];
+    const int64_t index = off >= 0 ? off / a.block_size : -1;
+    if (index < 0 || index >= a.ldb) return;
+    int64_t block = a.block_ids[t * a.ldb + index];
+    if (block < 0 || block >= a.num_blocks) block = 0;
+    const int64_t row = ((block * a.block_size + off % a.block_size) * a.kv_heads + hh) * a.head_dim;
+    dst = static_cast<Raw*>(a.key_cache) + row;
+    vd = static_cast<Raw*>(a.value_cache) + row;
+  }
   const float x1 = Act::load(src[i]), x2 = Act::load(src[i + half]);
   // The tables are cast to the activation dtype first (cos.to(q.dtype)).
   const float c1 = Act::load(Act::store(cs[i])), s1 = Act::load(Act::store(sn[i]));
@@ -113,7 +126,6 @@ __global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
   dst[i + half] = Act::store(hi);
   if (!is_q && a.v) {
     const Raw* vs = static_cast<const Raw*>(a.v) + t * a.ldv + hh * a.head_dim;
-    Raw* vd = static_cast<Raw*>(a.v_out) + (t * a.kv_heads + hh) * a.head_dim;
     vd[i] = vs[i];
     vd[i + half] = vs[i + half];
   }

@@ -121,6 +121,14 @@ struct RopeArgs {
   const float* sin_table;
   int64_t table_rows, tokens, heads, kv_heads, head_dim, ldq, ldk;
   int dtype;
+  // Optional (decode, one token per sequence): k and v go straight to this layer's paged
+  // cache [num_blocks, block_size, kv_heads, head_dim] of the same dtype, at the slot of
+  // offsets[t] in block_ids[t, :], instead of k_out / v_out.
+  void* key_cache;
+  void* value_cache;
+  const int32_t* block_ids;  // [tokens, ldb]
+  const int32_t* offsets;    // [tokens]
+  int64_t ldb, num_blocks, block_size;
 };
 hipError_t launch_rope(const RopeArgs& a, hipStream_t stream);
 hipError_t launch_linear_generic(const LinearArgs& a, hipStream_t stream);

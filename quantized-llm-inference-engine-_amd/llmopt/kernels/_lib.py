@@ -72,6 +72,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int,
         [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _p],
     ),
+    "llmopt_rope_kv_write_decode": (
+        _int,
+        [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _p, _p, _i64, _i64,
+         _p, _i64, _p, _p],
+    ),
     "llmopt_paged_attention_decode": (
         _int,
         [_p, _int, _i64, _p, _p, _int, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64,

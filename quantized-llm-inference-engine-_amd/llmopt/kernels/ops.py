@@ -35,6 +35,7 @@ __all__ = [
     "rmsnorm",
     "rmsnorm_supported",
     "rope",
+    "rope_kv_write_decode",
     "unpack_nibbles",
 ]
 
@@ -523,3 +524,40 @@ def rope(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor, cos_table: t
         "llmopt_rope",
     )
     return (q_out, k_out) if v_out is None else (q_out, k_out, v_out)
+
+
+def rope_kv_write_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
+                         cos_table: torch.Tensor, sin_table: torch.Tensor, key_cache: torch.Tensor,
+                         value_cache: torch.Tensor, block_ids: torch.Tensor,
+                         token_offsets: torch.Tensor) -> torch.Tensor:
+    """``rope`` for one token per sequence (``q [seqs, heads, d]``, ``k``/``v [seqs, kv_heads,
+    d]``) with the rotated k and v stored straight into one layer's paged cache slots, as
+    ``PagedKVCache.write_decode`` stores them (``paged_cache.py:246-277``); returns the rotated q.
+    The cache must hold the activations' dtype."""
+    seqs, heads, d = (int(s) for s in q.shape)
+    kv_heads = int(k.shape[1])
+    nb, bs, kvh, hd, _ = _layer_cache(key_cache, value_cache)
+    if key_cache.dtype != q.dtype or (kvh, hd) != (kv_heads, d) or tuple(v.shape) != tuple(k.shape):
+        raise ValueError("rope_kv_write_decode: cache dtype/shape does not match q/k/v")
+
+    def inner_ok(t: torch.Tensor) -> bool:
+        return t.stride(2) == 1 and t.stride(1) == d
+
+    q, k, v = (t if inner_ok(t) else t.contiguous() for t in (q, k, v))
+    dev = q.device
+    pos = positions.to(device=dev, dtype=torch.int64).contiguous()
+    cos_t = cos_table.to(device=dev, dtype=torch.float32).contiguous()
+    sin_t = sin_table.to(device=dev, dtype=torch.float32).contiguous()
+    table = _int32(block_ids, dev)
+    offsets = _int32(token_offsets, dev)
+    q_out = torch.empty(seqs, heads, d, dtype=q.dtype, device=dev)
+    call(
+        load_library().llmopt_rope_kv_write_decode(
+            q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), q_out.data_ptr(),
+            pos.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), int(cos_t.shape[0]), seqs, heads, kv_heads, d,
+            DTYPE_CODES[q.dtype], key_cache.data_ptr(), value_cache.data_ptr(), nb, bs, table.data_ptr(),
+            int(table.shape[1]), offsets.data_ptr(), _stream_handle(dev),
+        ),
+        "llmopt_rope_kv_write_decode",
+    )
+    return q_out

@@ -131,6 +131,15 @@ class PagedAttentionLayer(nn.Module):
         del self.q_proj, self.k_proj, self.v_proj
         return True
 
+    @staticmethod
+    def _fused_cache_write(cache: object, q: torch.Tensor) -> bool:
+        """Whether the rotary kernel can store k and v into ``cache`` itself: a paged cache on
+        the device holding the activations' dtype."""
+        kc = getattr(cache, "key_cache", None)
+        vc = getattr(cache, "value_cache", None)
+        return (isinstance(kc, torch.Tensor) and isinstance(vc, torch.Tensor) and kc.dim() == 5
+                and kc.dtype == q.dtype and vc.dtype == q.dtype and kc.device == q.device)
+
     def _project(self, hidden: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         if self.qkv_proj is not None:
             return self.qkv_proj(hidden)
@@ -144,7 +153,24 @@ class PagedAttentionLayer(nn.Module):
         q, k, v = self._project(hidden)
         # Token-major [seq, q_len, heads, head_dim]: the cache layout, and cos/sin broadcast
         # over the heads of each token.
-        if self.fused_ops and _hip(q):
+        paged = cache is not None and block_ids is not None and context_lens is not None
+        offsets = None
+        if paged:
+            offsets = token_offsets if token_offsets is not None else context_lens - q_len
+        written = False  # k and v already in the cache
+        if self.fused_ops and _hip(q) and paged and q_len == 1 and self._fused_cache_write(cache, q):
+            from llmopt.kernels import ops
+
+            # Decode: the rotary kernel stores k and v straight into the cache slots.
+            self.rotary.check(positions)
+            q = ops.rope_kv_write_decode(
+                q.view(total, self.num_heads, self.head_dim), k.view(total, self.num_kv_heads, self.head_dim),
+                v.view(total, self.num_kv_heads, self.head_dim), positions, self.rotary.cos_cached,
+                self.rotary.sin_cached, cache.key_cache[self.layer_idx], cache.value_cache[self.layer_idx],
+                block_ids, offsets)
+            q = q.view(seqs, q_len, self.num_heads, self.head_dim)
+            written = True
+        elif self.fused_ops and _hip(q):
             from llmopt.kernels import ops
 
             self.rotary.check(positions)
@@ -166,9 +192,10 @@ class PagedAttentionLayer(nn.Module):
             k = k.contiguous()
             v = v.contiguous()
         query = q.permute(0, 2, 1, 3)  # [seq, heads, q_len, head_dim]
-        if cache is not None and block_ids is not None and context_lens is not None:
-            offsets = token_offsets if token_offsets is not None else context_lens - q_len
-            if q_len == 1:
+        if paged:
+            if written:
+                pass
+            elif q_len == 1:
                 cache.write_decode(self.layer_idx, block_ids, offsets, k[:, 0], v[:, 0])
             else:
                 cache.write(self.layer_idx, block_ids, offsets, k, v)

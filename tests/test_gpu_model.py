@@ -74,20 +74,22 @@ def test_decode_steps_run_the_attention_and_cache_kernels(models, monkeypatch):
     from llmopt.kernels import ops
 
     gpu, _ = models
-    calls = {"attn": 0, "write": 0}
-    attn, write = ops.paged_decode_attention, ops.kv_write_decode
+    calls = {"attn": 0, "write": 0, "rope_write": 0}
+    originals = {name: getattr(ops, fn) for name, fn in
+                 (("attn", "paged_decode_attention"), ("write", "kv_write_decode"),
+                  ("rope_write", "rope_kv_write_decode"))}
 
-    def count_attn(*a, **k):
-        calls["attn"] += 1
-        return attn(*a, **k)
+    def counting(name):
+        def wrapped(*a, **k):
+            calls[name] += 1
+            return originals[name](*a, **k)
+        return wrapped
 
-    def count_write(*a, **k):
-        calls["write"] += 1
-        return write(*a, **k)
-
-    monkeypatch.setattr(ops, "paged_decode_attention", count_attn)
-    monkeypatch.setattr(ops, "kv_write_decode", count_write)
+    monkeypatch.setattr(ops, "paged_decode_attention", counting("attn"))
+    monkeypatch.setattr(ops, "kv_write_decode", counting("write"))
+    monkeypatch.setattr(ops, "rope_kv_write_decode", counting("rope_write"))
     prompts = torch.randint(0, 512, (2, 5), generator=torch.Generator().manual_seed(3))
     GreedyGenerator(gpu, use_graph=False).generate(prompts, 3)
     layers = len(gpu.layers)
-    assert calls == {"attn": 2 * layers, "write": 2 * layers}
+    # Each decode step's k and v go into the cache from the rotary kernel itself.
+    assert calls == {"attn": 2 * layers, "write": 0, "rope_write": 2 * layers}

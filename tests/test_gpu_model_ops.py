@@ -70,3 +70,32 @@ def test_rmsnorm_module_takes_the_kernel_on_hip():
     assert not ops.rmsnorm_supported(x.float(), norm.weight.float())
     y = norm(x)
     assert torch.equal(y, ops.rmsnorm(x, norm.weight, norm.eps)[0])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@torch.no_grad()
+def test_rope_kv_write_decode_matches_rope_then_write(dtype):
+    # The fused decode kernel against llmopt_rope followed by llmopt_kv_write_decode: the same
+    # q bit for bit and the same caches, including a block id past the pool (-> block 0) and
+    # an offset past the table row (nothing written).
+    seqs, heads, kvh, d, nb, bs = 6, 8, 2, 128, 12, 16
+    gen = torch.Generator().manual_seed(7)
+    q = torch.randn(seqs, heads * d + 64, generator=gen).to(dtype).to(DEV)[:, : heads * d].view(seqs, heads, d)
+    k = torch.randn(seqs, kvh, d, generator=gen).to(dtype).to(DEV)
+    v = torch.randn(seqs, kvh, d, generator=gen).to(dtype).to(DEV)
+    pos = torch.tensor([0, 5, 17, 31, 40, 63], device=DEV)
+    rot = RotaryEmbedding(d, 128, base=500000.0).to(DEV)
+    table = torch.randint(0, nb, (seqs, 4), generator=gen, dtype=torch.int32).to(DEV)
+    table[2, 1] = nb + 3
+    offsets = torch.tensor([0, 5, 17, 31, 40, 64], dtype=torch.int32, device=DEV)
+    init = torch.randn(nb, bs, kvh, d, generator=gen).to(dtype).to(DEV)
+    kc1, vc1 = init.clone(), init.clone() * 2
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    q1, k1, v1 = ops.rope(q, k, pos, rot.cos_cached, rot.sin_cached, v=v)
+    ops.kv_write_decode(kc1, vc1, table, offsets, k1, v1)
+    q2 = ops.rope_kv_write_decode(q, k, v, pos, rot.cos_cached, rot.sin_cached, kc2, vc2, table, offsets)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2)
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert not torch.equal(kc2, init)
