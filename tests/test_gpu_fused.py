@@ -19,7 +19,7 @@ import pytest
 import torch
 from torch import nn
 
-from llmopt.kernels import ops
+from llmopt.kernels import _lib, ops
 from llmopt.quantization import (
     FusedQuantLinear,
     QuantLinear,
@@ -145,3 +145,21 @@ def test_swiglu_rejects_bad_row_count():
     qt = _to_device(_host_qt(12, 256, 4, 128, False, seed=3))
     with pytest.raises(ValueError):
         ops.quant_linear_swiglu(torch.randn(2, 256, device=DEV).to(torch.bfloat16), qt, None, torch.bfloat16)
+
+
+@pytest.mark.parametrize("m", [12, 32])
+def test_swiglu_long_rows_over_k_slices(m):
+    # Long rows on a small grid with the workspace the swiglu entry point asks for: the decode
+    # kernel over K slices, whose reduction applies SiLU(gate) * up.
+    dtype = torch.bfloat16
+    inter, k = 2048, 14336  # 256 tiles of fused rows: 14 slices of K
+    assert _lib.load_library().llmopt_q_linear_workspace(m, 2 * inter, k, 4, 128) > 0
+    gate = _to_device(_host_qt(inter, k, 4, 128, False, seed=11))
+    up = _to_device(_host_qt(inter, k, 4, 128, False, seed=12))
+    fused = interleave_gate_up(gate, up)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(dtype).to(DEV)
+    y = ops.quant_linear_swiglu(x, fused, None, dtype)
+    g = (x.float() @ dequantize(gate, dtype).float().t().contiguous()).to(dtype)
+    u = (x.float() @ dequantize(up, dtype).float().t().contiguous()).to(dtype)
+    ref = torch.nn.functional.silu(g.float()).to(dtype).float() * u.float()
+    assert _rel_err(y, ref) <= SWIGLU_TOL
