@@ -24,7 +24,9 @@ extern "C" {
  * (src/llmopt/cache/paged_cache.py:246-277). keys/values: [num_seqs, kv_heads, head_dim] of
  * src_dtype, row stride src_seq_stride elements; converted to cache_dtype with round-to-nearest-
  * even, as .to(dtype) does. A block id outside [0, num_blocks) writes block 0, as the reference
- * does; an offset whose block index is outside [0, ldb) writes nothing (the reference raises).
+ * does; an offset whose block index is outside [0, ldb) writes nothing, where the reference
+ * raises IndexError (index past the row) or writes the row's last block (negative offset,
+ * through negative indexing).
  */
 int llmopt_kv_write_decode(void* key_cache, void* value_cache, int cache_dtype, int64_t num_blocks,
                            int64_t block_size, int64_t kv_heads, int64_t head_dim, const int32_t* block_ids,

@@ -50,10 +50,14 @@ int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
  * write that follows it: the rotated k and the unchanged v go straight into this layer's paged
  * cache (key_cache / value_cache [num_blocks, block_size, kv_heads, head_dim], of dtype) at the
  * slot of token_offsets[s] in block block_ids[s, token_offsets[s] / block_size] (int32, row
- * stride ldb); a block id outside [0, num_blocks) is replaced by block 0, and an offset past the
- * table row writes nothing. Replaces the rotary step of the attention layer followed by
- * PagedKVCache.write_decode (src/llmopt/cache/paged_cache.py:246-277), whose results it gives
- * bit for bit; q_out as in llmopt_rope.
+ * stride ldb); a block id outside [0, num_blocks) is replaced by block 0, as the reference does.
+ * Replaces the rotary step of the attention layer followed by PagedKVCache.write_decode
+ * (src/llmopt/cache/paged_cache.py:246-277), whose results it gives bit for bit for offsets
+ * whose block index lies in [0, ldb). Outside that range it differs: such a token's k and v
+ * are not written, where the reference raises IndexError (index past the row) or, through
+ * negative indexing, writes into the row's last block (negative offset). The offsets live on
+ * the device, so checking them would need a host sync; callers that can hold such offsets
+ * check them first. q_out as in llmopt_rope.
  */
 int llmopt_rope_kv_write_decode(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
                                 void* q_out, const int64_t* positions, const float* cos_table,

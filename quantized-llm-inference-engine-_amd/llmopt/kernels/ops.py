@@ -345,6 +345,15 @@ def _int32(t: torch.Tensor, device: torch.device) -> torch.Tensor:
     return t.to(device=device, dtype=torch.int32).contiguous()
 
 
+def _check_rows(what: str, seqs: int, **tensors: torch.Tensor) -> None:
+    """Each per-sequence tensor must have a row for every one of ``seqs`` sequences: the
+    kernels read row ``s`` of each for every ``s < seqs`` (the reference's indexing raises)."""
+    for name, t in tensors.items():
+        rows = int(t.shape[0]) if t.dim() > 0 else 1
+        if rows < seqs:
+            raise ValueError(f"{what}: {name} has {rows} rows for {seqs} sequences")
+
+
 def _layer_cache(key_cache: torch.Tensor, value_cache: torch.Tensor) -> tuple[int, int, int, int, int]:
     """Geometry of one layer's caches ``[num_blocks, block_size, kv_heads, head_dim]``."""
     if key_cache.dim() != 4 or key_cache.shape != value_cache.shape:
@@ -367,6 +376,9 @@ def kv_write_decode(key_cache, value_cache, block_ids, token_offsets, keys, valu
     dev = key_cache.device
     if keys.dtype not in DTYPE_CODES:
         keys, values = keys.to(key_cache.dtype), values.to(key_cache.dtype)
+    if int(values.shape[0]) != seqs or block_ids.dim() != 2:
+        raise ValueError("kv_write_decode: values must match keys, block_ids must be [seqs, blocks]")
+    _check_rows("kv_write_decode", seqs, block_ids=block_ids, token_offsets=token_offsets.reshape(-1))
     k = keys.reshape(seqs, kvh * hd).contiguous()
     v = values.reshape(seqs, kvh * hd).to(k.dtype).contiguous()
     table = _int32(block_ids, dev)
@@ -391,6 +403,9 @@ def kv_write(key_cache, value_cache, block_ids, token_offsets, keys, values) -> 
     dev = key_cache.device
     if keys.dtype not in DTYPE_CODES:
         keys, values = keys.to(key_cache.dtype), values.to(key_cache.dtype)
+    if int(values.shape[0]) != seqs or block_ids.dim() != 2:
+        raise ValueError("kv_write: values must match keys, block_ids must be [seqs, blocks]")
+    _check_rows("kv_write", seqs, block_ids=block_ids, token_offsets=token_offsets.reshape(-1))
     k = keys.reshape(seqs, q_len, kvh * hd).contiguous()
     v = values.reshape(seqs, q_len, kvh * hd).to(k.dtype).contiguous()
     table = _int32(block_ids, dev)
@@ -539,6 +554,10 @@ def rope_kv_write_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, posi
     nb, bs, kvh, hd, _ = _layer_cache(key_cache, value_cache)
     if key_cache.dtype != q.dtype or (kvh, hd) != (kv_heads, d) or tuple(v.shape) != tuple(k.shape):
         raise ValueError("rope_kv_write_decode: cache dtype/shape does not match q/k/v")
+    if int(k.shape[0]) != seqs or block_ids.dim() != 2:
+        raise ValueError("rope_kv_write_decode: k/v need one row per query row, block_ids [seqs, blocks]")
+    _check_rows("rope_kv_write_decode", seqs, positions=positions.reshape(-1),
+                token_offsets=token_offsets.reshape(-1), block_ids=block_ids)
 
     def inner_ok(t: torch.Tensor) -> bool:
         return t.stride(2) == 1 and t.stride(1) == d

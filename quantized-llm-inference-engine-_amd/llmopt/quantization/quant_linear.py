@@ -154,16 +154,21 @@ def replace_linear_modules(
     model: nn.Module,
     replacements: dict[nn.Module, nn.Module],
 ) -> nn.Module:
-    """Swap every child found in ``replacements`` for its value, in place."""
-    if not replacements:
-        return model
-    located: dict[nn.Module, tuple[nn.Module, str]] = {}
-    for parent in model.modules():
-        for name, child in parent.named_children():
-            if child in replacements:
-                located[child] = (parent, name)
-    for child, (parent, name) in located.items():
-        setattr(parent, name, replacements[child])
+    """Put ``replacements[child]`` in place of every child module that is a key (in place).
+
+    Behaviour of ``quant_linear.py:122-136``. The slots are found first and filled after,
+    so a replacement that itself contains replaced modules is not visited. A module
+    registered under several parents is replaced in each of them; ``model`` itself is
+    never replaced.
+    """
+    slots = [
+        (parent, attr)
+        for parent in model.modules()
+        for attr, child in parent.named_children()
+        if child in replacements
+    ]
+    for parent, attr in slots:
+        setattr(parent, attr, replacements[getattr(parent, attr)])
     return model
 
 
@@ -178,56 +183,42 @@ def quantize_model_(
     ignore_layers: tuple[str, ...] = ("lm_head", "embed_tokens"),
     inplace: bool = True,
 ) -> nn.Module:
-    """Replace every eligible ``nn.Linear`` with a :class:`QuantLinear` (``quant_linear.py:139-207``).
+    """Swap every eligible ``nn.Linear`` of ``model`` for a :class:`QuantLinear` and return it.
 
-    Layers whose name contains an ``ignore_layers`` token stay dense. When the
-    group size does not divide ``in_features`` the layer uses
-    ``gcd(in_features, group_size)`` instead. With ``strategy="gptq"`` and
-    calibration batches, per-layer Hessians are collected with forward hooks
-    (collection stops at the first batch the model cannot run). ``inplace`` is
-    accepted for API parity; the model is always modified in place.
+    Behaviour of ``quant_linear.py:139-207``:
+
+    * eligible: an ``nn.Linear`` whose qualified name contains none of ``ignore_layers``;
+    * each layer is quantized with groups of ``gcd(in_features, group_size)`` columns, so a
+      width that ``group_size`` does not divide still quantizes;
+    * ``strategy="gptq"`` with ``calibration_batches`` uses the layers' input Hessians;
+      collection ends at the first batch the model cannot run; GPTQ keeps its default
+      damping and activation order;
+    * each ``QuantLinear`` computes in its original layer's weight dtype, and the old
+      layer's weight is overwritten with its dequantization.
+
+    ``inplace`` is accepted for signature compatibility: the model is always modified.
     """
+    from llmopt.quantization.calibration import collect_hessians
     from llmopt.quantization.quantizers import build_quantizer
 
     del inplace
-    targets: list[tuple[str, nn.Linear]] = []
-    for name, module in model.named_modules():
-        if not isinstance(module, nn.Linear):
-            continue
-        if any(token in name for token in ignore_layers):
-            continue
-        if module.in_features % group_size:
-            logger.debug(
-                "%s: in_features=%d is not a multiple of group_size=%d, using %d instead",
-                name,
-                module.in_features,
-                group_size,
-                math.gcd(module.in_features, group_size),
-            )
-        targets.append((name, module))
-
+    layers = [
+        module
+        for name, module in model.named_modules()
+        if isinstance(module, nn.Linear) and not any(tok in name for tok in ignore_layers)
+    ]
     hessians: dict[nn.Module, torch.Tensor] = {}
     if strategy == "gptq" and calibration_batches:
-        from llmopt.quantization.calibration import HessianCollector
+        hessians = collect_hessians(model, layers, calibration_batches, stop_at_failure=True)
 
-        for _, module in targets:
-            with HessianCollector([module], device=module.weight.device) as collector:
-                for batch in calibration_batches:
-                    try:
-                        model(batch.to(module.weight.device))
-                    except Exception:  # noqa: BLE001 - calibration is best effort
-                        break
-                hessians.update(collector.results())
-
-    replacements: dict[nn.Module, nn.Module] = {}
-    for _, module in targets:
-        group = math.gcd(module.in_features, group_size) or group_size
-        quantizer = build_quantizer(strategy, bits=bits, group_size=group, symmetric=symmetric)
-        quantized = quantizer.quantize(module.weight.detach().to(torch.float32), hessians.get(module))
-        replacements[module] = QuantLinear.from_float(
-            module, quantized, compute_dtype=module.weight.dtype
+    swaps: dict[nn.Module, nn.Module] = {}
+    for layer in layers:
+        group = math.gcd(layer.in_features, group_size) or group_size
+        if group != group_size:
+            logger.debug("in_features=%d: groups of %d columns instead of %d", layer.in_features, group, group_size)
+        packed = build_quantizer(strategy, bits=bits, group_size=group, symmetric=symmetric).quantize(
+            layer.weight.detach().to(torch.float32), hessians.get(layer)
         )
-        module.weight.data = quantized.dequantize().to(module.weight.dtype)
-
-    replace_linear_modules(model, replacements)
-    return model
+        swaps[layer] = QuantLinear.from_float(layer, packed, compute_dtype=layer.weight.dtype)
+        layer.weight.data = packed.dequantize().to(layer.weight.dtype)
+    return replace_linear_modules(model, swaps)

@@ -149,3 +149,33 @@ def test_last_token_logits_match_the_full_projection():
     assert torch.equal(last_token_hidden(hidden, 7), hidden.view(3, 7, 64)[:, -1])
     with pytest.raises(ValueError):
         last_token_hidden(hidden, 4)
+
+
+def test_cache_write_wrappers_reject_short_per_sequence_tensors():
+    # The kernels read row s of every per-sequence tensor for s < seqs; the wrappers reject
+    # short ones before anything reaches the device (the reference's indexing raises too).
+    from llmopt.kernels import ops
+
+    kc = torch.zeros(4, 16, 2, 8, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    q = torch.zeros(3, 4, 8, dtype=torch.bfloat16)
+    k = torch.zeros(3, 2, 8, dtype=torch.bfloat16)
+    table = torch.zeros(3, 2, dtype=torch.int32)
+    offs = torch.zeros(3, dtype=torch.int32)
+    pos = torch.zeros(3, dtype=torch.int64)
+    cos = torch.ones(32, 8)
+    bad = {
+        "positions": (pos[:2], offs, table, k),
+        "token_offsets": (pos, offs[:1], table, k),
+        "block_ids": (pos, offs, table[:2], k),
+        "k rows": (pos, offs, table, k[:2]),
+    }
+    for name, (p, o, t, kk) in bad.items():
+        with pytest.raises(ValueError):
+            ops.rope_kv_write_decode(q, kk, kk.clone(), p, cos, cos, kc, vc, t, o)
+    with pytest.raises(ValueError):
+        ops.kv_write_decode(kc, vc, table[:1], offs, k, k)
+    with pytest.raises(ValueError):
+        ops.kv_write_decode(kc, vc, table, offs[:2], k, k)
+    with pytest.raises(ValueError):
+        ops.kv_write(kc, vc, table[:2], offs, k[:, None], k[:, None])

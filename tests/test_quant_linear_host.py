@@ -190,3 +190,81 @@ def test_apply_quantization_writes_dequantized_weights():
     assert not torch.equal(before, after)
     assert result.compression_ratio > 1 and "layers to 4-bit" in result.summary()
     assert "quantized=rtn-4bit" in repr(model.layers[0].q_proj)
+
+
+def test_one_calibration_pass_equals_a_pass_per_layer():
+    # collect_hessians hooks every layer at once; a pass per layer (the reference's loop,
+    # calibration.py:180-190) must give the same Gram matrices, bit for bit.
+    from llmopt.quantization.calibration import collect_hessians
+
+    model = _tiny()
+    layers = [m for n, m in model.named_modules() if isinstance(m, nn.Linear) and "lm_head" not in n]
+    batches = CalibrationHarness(num_samples=3, seq_length=8, seed=1).synthetic(256)
+    together = collect_hessians(model, layers, batches, stop_at_failure=True)
+    assert len(together) == len(layers)
+    for layer in layers:
+        with HessianCollector([layer]) as alone:
+            for batch in batches:
+                model(batch)
+        assert torch.equal(together[layer], alone.hessian_for(layer))
+
+
+def test_collect_hessians_failure_policies():
+    from llmopt.quantization.calibration import collect_hessians
+
+    model = _tiny()
+    layer = model.layers[0].q_proj
+    good = torch.randint(0, 256, (1, 4))
+    bad = torch.full((1, 4), 999)  # out of the embedding's range: the forward raises
+    skip = collect_hessians(model, [layer], [good, bad, good], stop_at_failure=False)
+    stop = collect_hessians(model, [layer], [good, bad, good], stop_at_failure=True)
+    one = collect_hessians(model, [layer], [good], stop_at_failure=True)
+    torch.testing.assert_close(skip[layer], one[layer])  # two equal batches: same (2/n) X^T X
+    torch.testing.assert_close(stop[layer], one[layer])
+    assert collect_hessians(model, [layer], [bad], stop_at_failure=False) == {}
+    # 1-D batches get a batch dimension when asked to (apply_quantization's convention).
+    flat = collect_hessians(model, [layer], [good[0]], stop_at_failure=True, add_batch_dim=True)
+    torch.testing.assert_close(flat[layer], one[layer])
+
+
+def test_gptq_apply_quantization_uses_calibration_hessians():
+    from llmopt.quantization import GPTQQuantizer
+    from llmopt.quantization.calibration import collect_hessians
+
+    model = _tiny()
+    batches = CalibrationHarness(num_samples=2, seq_length=16, seed=5).synthetic(256)
+    layer = model.layers[1].gate_proj
+    h = collect_hessians(model, [layer], batches, stop_at_failure=False)[layer]
+    expect = GPTQQuantizer(bits=4, group_size=16, symmetric=True).quantize(layer.weight.detach().clone(), h)
+    # apply_quantization takes group_size as given (no gcd fallback): 16 divides every width.
+    result = apply_quantization(model, strategy="gptq", bits=4, group_size=16, calibration_batches=batches)
+    got = result.quantizers["layers.1.gate_proj"]
+    assert torch.equal(got.qweight, expect.qweight) and torch.equal(got.scales, expect.scales)
+    with pytest.raises(ValueError):
+        apply_quantization(_tiny(), strategy="awq")
+
+
+def test_replace_linear_modules_shared_child_and_nested_replacement():
+    shared = nn.Linear(4, 4)
+    model = nn.Sequential(nn.Sequential(shared), nn.Sequential(shared))
+    new = nn.Sequential(nn.Linear(4, 4))
+    replace_linear_modules(model, {shared: new, new[0]: nn.Identity()})
+    assert model[0][0] is new and model[1][0] is new
+    assert isinstance(new[0], nn.Linear)  # the replacement's own children are not visited
+
+
+def test_harness_batches_follow_the_seeded_per_sample_draws():
+    harness = CalibrationHarness(num_samples=4, seq_length=6, seed=9)
+    gen = torch.Generator().manual_seed(9)
+    expect = [torch.randint(0, 50, (1, 6), generator=gen, dtype=torch.long) for _ in range(4)]
+    got = harness.synthetic(50)
+    assert len(got) == 4 and all(torch.equal(a, b) for a, b in zip(got, expect))
+
+    class Tok:
+        def encode(self, text):
+            return [ord(c) for c in text]
+
+    rows = CalibrationHarness(seq_length=5).from_tokenizer(Tok(), ["abc", "", "abcdefg"])
+    assert [r.tolist() for r in rows] == [[[97, 98, 99, 0, 0]], [[97, 98, 99, 100, 101]]]
+    with pytest.raises(TypeError):
+        CalibrationHarness().from_tokenizer(object(), ["x"])
