@@ -10,34 +10,11 @@ import pytest
 import torch
 
 from llmopt.model import GreedyGenerator, ModelConfig, random_quantized_model
+from model_helpers import forced_logits as _forced_logits
+from model_helpers import rel as _rel
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
-
-
-def _rel(a: torch.Tensor, b: torch.Tensor) -> float:
-    a, b = a.double().cpu(), b.double().cpu()
-    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
-
-
-@torch.no_grad()
-def _forced_logits(model, prompts: torch.Tensor, forced: torch.Tensor) -> torch.Tensor:
-    """Last-position logits of the prefill and of each teacher-forced decode step:
-    ``[steps + 1, seq, vocab]``."""
-    dev = model.embed_tokens.weight.device
-    seqs, plen = prompts.shape
-    steps = forced.shape[1]
-    per = -(-(plen + steps + 1) // 16)
-    cache = model.allocate_cache(seqs * per, 16, model.embed_tokens.weight.dtype, dev)
-    table = torch.arange(seqs * per, dtype=torch.int32, device=dev).view(seqs, per)
-    out = [model(prompts.to(dev).reshape(-1), torch.arange(plen, device=dev).repeat(seqs), cache=cache,
-                 block_ids=table, context_lens=torch.full((seqs,), plen, dtype=torch.int32, device=dev),
-                 q_len=plen, last_only=True).last_logits()]
-    for i in range(steps):
-        pos = torch.full((seqs,), plen + i, dtype=torch.long, device=dev)
-        out.append(model(forced[:, i].to(dev), pos, cache=cache, block_ids=table,
-                         context_lens=(pos + 1).to(torch.int32), q_len=1, last_only=True).last_logits())
-    return torch.stack(out).float().cpu()
 
 
 @pytest.fixture(scope="module")

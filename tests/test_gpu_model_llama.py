@@ -1,0 +1,117 @@
+"""End-to-end parity of the decoder at Llama-3-8B width, and the drift of a deep model.
+
+* Llama-3-8B-shaped decoder (hidden 4096, 32 / 8 heads of 128, FFN 14336, vocab 128256,
+  every decoder linear RTN W4 g128 asymmetric), cut to 1 and 2 layers: the HIP model (fused
+  q/k/v and gate/up, SwiGLU epilogue, fused norm and rotary kernels, paged decode attention)
+  runs a 32-sequence prefill (256 rows: the prefill GEMM) and teacher-forced decode steps of
+  32 tokens (the decode kernels of the end-to-end workload). The reference is the
+  reference's own computation: a dense bf16 ``nn.Linear`` per projection holding the
+  oracle's dequantized weight (what ``QuantLinear`` caches and multiplies,
+  src/llmopt/quantization/quant_linear.py:93-113), torch norms, rotary and gathered-cache
+  attention (src/llmopt/model/layers.py, attention/paged_attention.py), run on the host.
+  Bound on the last-position logits, max|a - b| / max|b|: 1.5e-2 per decoder layer.
+* A deep, narrow decoder (32 layers, hidden 256): bf16 rounding differences grow with depth,
+  so the HIP model is held to the accuracy of the reference's own bf16 computation: both are
+  compared with the same reference run in float32, and the HIP model's error must stay within
+  twice the reference-bf16 error (+2e-3). Its distance to the reference bf16 run stays under
+  1e-1, and wherever the float32 logits lead by a clear margin both pick the same token.
+"""
+
+from __future__ import annotations
+
+import copy
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+from llmopt.model import ModelConfig, fuse_projections_, random_quantized_model, reference_twin
+from model_helpers import confident_positions, forced_logits, rel
+from oracle import quant_oracle as qo
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+PER_LAYER_BOUND = 1.5e-2
+
+
+@torch.no_grad()
+def _oracle_twin(model):
+    """``reference_twin`` of an unfused quantized model, moved to the host, with every dense
+    weight replaced by the oracle's dequantization of the packed codes (checked equal, bit for
+    bit, to the device dequantization the twin was built with)."""
+    from llmopt.quantization.quant_linear import QuantLinear
+
+    packed = {name: m.quantized_tensor() for name, m in model.named_modules() if isinstance(m, QuantLinear)}
+    twin = reference_twin(model).to("cpu")
+    modules = dict(twin.named_modules())
+    for name, qt in packed.items():
+        dense = qo.dequantize(qt.qweight.cpu().numpy(), qt.scales.cpu().numpy(), qt.zeros.cpu().numpy(),
+                              qt.bits, qt.group_size, qt.symmetric, qt.shape)
+        weight = torch.from_numpy(qo.round_to_dtype(dense, "bfloat16")).to(torch.bfloat16)
+        layer = modules[name]
+        assert torch.equal(layer.weight.view(torch.int16), weight.view(torch.int16)), name
+        layer.weight.data = weight
+    return twin
+
+
+@pytest.fixture(scope="module")
+def llama_two_layers():
+    cfg = dataclasses.replace(ModelConfig.llama3_8b(), num_hidden_layers=2)
+    gpu = random_quantized_model(cfg, device=DEV, dtype=torch.bfloat16, seed=0, fuse=False)
+    twin = _oracle_twin(gpu)
+    fuse_projections_(gpu)
+    torch.cuda.empty_cache()
+    return gpu, twin
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("layers", [1, 2])
+def test_llama3_8b_width_decoder_matches_the_oracle_reference(llama_two_layers, layers):
+    gpu, twin = llama_two_layers
+    keep_gpu, keep_twin = gpu.layers, twin.layers
+    gpu.layers, twin.layers = keep_gpu[:layers], keep_twin[:layers]
+    try:
+        g = torch.Generator().manual_seed(5)
+        prompts = torch.randint(0, 128256, (32, 8), generator=g)
+        forced = torch.randint(0, 128256, (32, 3), generator=g)
+        got = forced_logits(gpu, prompts, forced)
+        want = forced_logits(twin, prompts, forced)
+    finally:
+        gpu.layers, twin.layers = keep_gpu, keep_twin
+    errs = [rel(got[i], want[i]) for i in range(got.shape[0])]
+    print(f"{layers} layer(s): max-abs-rel per step (prefill, decode...):", ["%.2e" % e for e in errs], flush=True)
+    assert max(errs) <= PER_LAYER_BOUND * layers, errs
+    sure = confident_positions(want, 2 * PER_LAYER_BOUND * layers * float(want.abs().max()))
+    assert torch.equal(got.argmax(-1)[sure], want.argmax(-1)[sure])
+
+
+@pytest.fixture(scope="module")
+def deep_narrow():
+    cfg = dataclasses.replace(ModelConfig.tiny(), num_hidden_layers=32)
+    gpu = random_quantized_model(cfg, device=DEV, dtype=torch.bfloat16, seed=1, fuse=False)
+    twin = _oracle_twin(gpu)
+    fuse_projections_(gpu)
+    return gpu, twin
+
+
+@pytest.mark.timeout(600)
+def test_deep_decoder_drift_is_the_reference_bf16_drift(deep_narrow):
+    gpu, twin = deep_narrow
+    g = torch.Generator().manual_seed(6)
+    prompts = torch.randint(0, 512, (8, 24), generator=g)
+    forced = torch.randint(0, 512, (8, 6), generator=g)
+    hip = forced_logits(gpu, prompts, forced)
+    ref_bf16 = forced_logits(twin, prompts, forced)
+    exact = forced_logits(copy.deepcopy(twin).float(), prompts, forced)
+    e_hip = max(rel(hip[i], exact[i]) for i in range(hip.shape[0]))
+    e_ref = max(rel(ref_bf16[i], exact[i]) for i in range(hip.shape[0]))
+    e_pair = max(rel(hip[i], ref_bf16[i]) for i in range(hip.shape[0]))
+    print(f"32 layers: HIP vs fp32 {e_hip:.3e}, reference bf16 vs fp32 {e_ref:.3e}, HIP vs reference bf16 "
+          f"{e_pair:.3e}", flush=True)
+    assert e_hip <= 2 * e_ref + 2e-3
+    assert e_pair <= 1e-1
+    sure = confident_positions(exact, 2 * (e_hip + e_ref) * float(exact.abs().max()))
+    assert sure.any()
+    assert torch.equal(hip.argmax(-1)[sure], exact.argmax(-1)[sure])
+    assert torch.equal(ref_bf16.argmax(-1)[sure], exact.argmax(-1)[sure])

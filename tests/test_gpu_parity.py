@@ -355,23 +355,29 @@ def projections():
 
 
 @pytest.mark.parametrize("name", list(PROJECTIONS))
-@pytest.mark.parametrize("m", [1, 8, 32, 64, 256, 2048])
+@pytest.mark.parametrize("m", [1, 8, 32, 64, 256, 2048, 8192])
 def test_projection_sampled_columns_and_gpu_fp32(projections, name, m):
+    # Decode and prefill batches of the Llama-3-8B projections, up to the 8192-token prefill.
+    # The CPU reference runs on 256 sampled output columns (and, above 2048 tokens, 256
+    # sampled rows: each output row depends only on its own activation row); every output
+    # is checked against a torch fp32 GPU matmul of the bit-exact dequantized weight.
     qt, dqt, dense = projections[name]
     n, k = qt.shape
     gen = torch.Generator().manual_seed(m)
     x = torch.randn(m, k, generator=gen).to(torch.bfloat16)
     y = ops.quant_linear(x.to(DEV), dqt, None, torch.bfloat16)
     cols = np.sort(np.random.default_rng(m).choice(n, size=256, replace=False))
-    ref = _reference_linear(x, dense, None, torch.bfloat16, cols=cols)
-    assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= 1e-2
+    rows = np.arange(m) if m <= 2048 else np.sort(np.random.default_rng(m + 1).choice(m, size=256, replace=False))
+    ref = _reference_linear(x[torch.from_numpy(rows)], dense, None, torch.bfloat16, cols=cols)
+    got = y[torch.from_numpy(rows).to(DEV)][:, torch.from_numpy(cols).to(DEV)]
+    assert _rel_err(got, ref) <= 1e-2
     w32 = dequantize(dqt, torch.bfloat16).float()  # bit-exact (checked above)
     ref_gpu = torch.matmul(x.to(DEV).float(), w32.t().contiguous())
     assert _rel_err(y, ref_gpu) <= 1e-2
 
 
 @pytest.mark.parametrize("name", list(PROJECTIONS))
-@pytest.mark.parametrize("m", [1, 64, 2048])
+@pytest.mark.parametrize("m", [1, 64, 2048, 8192])
 def test_projection_one_hot_rows_return_weight_columns(projections, name, m):
     _, dqt, dense = projections[name]
     n, k = dense.shape
@@ -383,16 +389,19 @@ def test_projection_one_hot_rows_return_weight_columns(projections, name, m):
     np.testing.assert_array_equal(_bits_of(y), expect)
 
 
-@pytest.mark.parametrize("m", [1, 32, 2048])
-def test_projection_scaling_by_two_is_exact(projections, m):
-    _, dqt, _ = projections["down"]
-    x = torch.randn(m, 14336, device=DEV).to(torch.bfloat16)
+@pytest.mark.parametrize("name,m", [("down", 1), ("down", 32), ("down", 2048)]
+                         + [(name, 8192) for name in PROJECTIONS])
+def test_projection_scaling_by_two_is_exact(projections, name, m):
+    qt, dqt, _ = projections[name]
+    x = torch.randn(m, qt.shape[1], device=DEV).to(torch.bfloat16)
     y1 = ops.quant_linear(x, dqt, None, torch.bfloat16)
     y2 = ops.quant_linear(x * 2, dqt, None, torch.bfloat16)
     assert torch.equal(y2, y1 * 2)
 
 
-@pytest.mark.parametrize("bits,symmetric,m", [(8, False, 1), (8, False, 32), (8, False, 2048), (2, False, 1), (2, False, 2048), (8, True, 32)])
+@pytest.mark.parametrize("bits,symmetric,m", [(8, False, 1), (8, False, 32), (8, False, 2048), (2, False, 1),
+                                              (2, False, 12), (2, False, 16), (2, False, 32), (2, False, 2048),
+                                              (8, True, 32)])
 def test_down_projection_bit_width_sweep(bits, symmetric, m):
     qt = _host_qt(4096, 14336, bits, 128, symmetric, seed=bits)
     dqt = _to_device(qt)
@@ -411,3 +420,48 @@ def test_fp32_compute_single_linear_config():
     y = ops.quant_linear(x.to(DEV), _to_device(qt), None, torch.float32)
     ref = _reference_linear(x, _oracle_dense(qt), None, torch.float32)
     assert _rel_err(y, ref) <= 2e-3
+
+
+# ---- GPTQ-quantized weights through the kernels ------------------------------------------------
+
+@pytest.fixture(scope="module")
+def gptq_down():
+    """The down projection (K 14336, N 4096) quantized by GPTQQuantizer: 4 bits, groups of
+    128, damping 0.01, activation order, calibrated on H = (2/128) X^T X of 128 token rows
+    gathered from a seeded N(0, 1) embedding table (seed 2) at seeded random ids (seed 3).
+    Weights 0.02 N(0, 1), seed 0. Runs on the GPU (torch), asymmetric and symmetric grids."""
+    from llmopt.quantization import GPTQQuantizer
+
+    k, n = 14336, 4096
+    table = torch.randn(1024, k, generator=torch.Generator().manual_seed(2))
+    ids = torch.randint(0, 1024, (128,), generator=torch.Generator().manual_seed(3))
+    x_cal = table[ids].to(DEV)
+    hessian = (2.0 / 128) * (x_cal.t() @ x_cal)
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(0)) * 0.02).to(DEV)
+    out = {}
+    for symmetric in (False, True):
+        qt = GPTQQuantizer(bits=4, group_size=128, symmetric=symmetric).quantize(w, hessian)
+        host = QuantizedTensor(qt.qweight.cpu(), qt.scales.cpu(), qt.zeros.cpu(), 4, 128, symmetric, qt.shape)
+        out[symmetric] = (qt, _oracle_dense(host))
+    return out
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("symmetric", [False, True])
+@pytest.mark.parametrize("m", [1, 32, 2048])
+def test_gptq_down_projection_through_the_kernels(gptq_down, symmetric, m):
+    qt, dense = gptq_down[symmetric]
+    assert qt.qweight.device.type == "cuda" and qt.qweight.shape == (4096, 7168)
+    x = torch.randn(m, 14336, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    y = ops.quant_linear(x.to(DEV), qt, None, torch.bfloat16)
+    cols = np.sort(np.random.default_rng(m + 7).choice(4096, size=256, replace=False))
+    ref = _reference_linear(x, dense, None, torch.bfloat16, cols=cols)
+    assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= 1e-2
+    # The device dequantization of a GPTQ weight is the oracle's, bit for bit.
+    np.testing.assert_array_equal(_bits_of(dequantize(qt, torch.bfloat16)), _expected_bits(dense, torch.bfloat16))
+    # One-hot rows read back single weight columns exactly.
+    picks = np.random.default_rng(m).choice(14336, size=min(m, 64), replace=False)
+    hot = torch.zeros(len(picks), 14336, dtype=torch.bfloat16)
+    hot[torch.arange(len(picks)), torch.from_numpy(picks)] = 1.0
+    yh = ops.quant_linear(hot.to(DEV), qt, None, torch.bfloat16)
+    np.testing.assert_array_equal(_bits_of(yh), qo.bf16_bits(np.ascontiguousarray(dense[:, picks].T)).view(np.int16))
