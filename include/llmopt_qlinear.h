@@ -117,6 +117,26 @@ int llmopt_q_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void
                     void* stream);
 
 /*
+ * llmopt_q_linear without a workspace argument and without any allocation: the K-split
+ * partial sums that llmopt_q_linear keeps in the caller's workspace live in a static device
+ * array of the library instead, llmopt_q_linear_noalloc_max_scratch() bytes (32 MiB) per
+ * device, held until the process ends. Results are those of llmopt_q_linear with a workspace
+ * of llmopt_q_linear_workspace(...) bytes, bit for bit. A shape whose plan needs more scratch
+ * than that returns LLMOPT_ERR_WORKSPACE and launches nothing. Calls that overlap on one
+ * device (other streams, other threads) share that device's array and race on it; serialize
+ * them. Run it with the stream's device current.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ */
+int llmopt_q_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                            int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                            void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                            int symmetric, int signed_codes, void* stream);
+
+/* Bytes of the static scratch behind llmopt_q_linear_noalloc (the largest plan it takes). */
+size_t llmopt_q_linear_noalloc_max_scratch(void);
+
+/*
  * llmopt_q_linear with an explicit kernel choice (LLMOPT_ALGO_*). Returns
  * LLMOPT_ERR_UNSUPPORTED when the chosen kernel cannot take these arguments.
  * No counterpart in the reference: lets tests and benchmarks pin one kernel.

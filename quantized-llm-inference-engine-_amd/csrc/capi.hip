@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/llmopt_attention.h"
@@ -195,6 +196,41 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
   return hip_status(err, "linear launch");
 }
 
+// ---- the allocation-free linear's scratch ------------------------------------------------------
+//
+// llmopt_q_linear_noalloc takes its K-split partial sums from this file-scope device array
+// instead of a caller's workspace. Each device the library runs on holds its own copy, of
+// kNoAllocScratchBytes, until the process ends. Host code never uses the array's name as an
+// address (on the host it is only a stand-in for the symbol): the device address of each
+// device's copy comes from hipGetSymbolAddress, once per device, with that device current,
+// and only that address is handed to kernels. Every call on a device shares its copy, so
+// calls that overlap on one device (several streams, several threads) race on it; the
+// kernels write every partial sum they later read, so nothing needs clearing between calls.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) static uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices] = {};
+
+// Device address of the current device's scratch (set up on the first call on that device).
+int current_scratch(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(LLMOPT_ERR_UNSUPPORTED, "device %d beyond the scratch table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[dev] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return hip_status(err, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr) return fail(LLMOPT_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_address[dev] = ptr;
+  }
+  *out = g_scratch_address[dev];
+  return LLMOPT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -323,6 +359,28 @@ int llmopt_q_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void
   return llmopt_q_linear_ex(x, M, K, ldx, qweight, ldq, scales, zeros, bias, y, N, ldy, act_dtype,
                             bits, group_size, symmetric, signed_codes, workspace, workspace_bytes,
                             stream, LLMOPT_ALGO_AUTO);
+}
+
+size_t llmopt_q_linear_noalloc_max_scratch(void) { return kNoAllocScratchBytes; }
+
+int llmopt_q_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                            int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                            void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                            int symmetric, int signed_codes, void* stream) {
+  const size_t need = llmopt_q_linear_workspace(M, N, K, bits, group_size);
+  if (need > kNoAllocScratchBytes)
+    return fail(LLMOPT_ERR_WORKSPACE,
+                "llmopt_q_linear_noalloc: M=%lld N=%lld K=%lld needs %zu bytes of scratch, beyond the %zu "
+                "bytes of the static scratch; call llmopt_q_linear with a workspace",
+                (long long)M, (long long)N, (long long)K, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = current_scratch(&ws);
+    if (rc != LLMOPT_OK) return rc;
+  }
+  return run_linear(x, M, K, ldx, qweight, ldq, scales, zeros, bias, y, N, ldy, act_dtype, bits,
+                    group_size, symmetric, signed_codes, ws, ws ? kNoAllocScratchBytes : 0, stream,
+                    LLMOPT_ALGO_AUTO, llmopt::kEpiNone);
 }
 
 }  // extern "C"

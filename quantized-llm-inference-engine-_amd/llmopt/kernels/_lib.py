@@ -93,6 +93,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _int, _int, _int, _int, _int,
          _p, _size, _p],
     ),
+    "llmopt_q_linear_noalloc": (
+        _int,
+        [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _int, _int, _int, _int, _int, _p],
+    ),
+    "llmopt_q_linear_noalloc_max_scratch": (_size, []),
     "llmopt_q_linear_ex": (
         _int,
         [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _int, _int, _int, _int, _int,
