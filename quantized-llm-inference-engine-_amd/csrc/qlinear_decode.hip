@@ -19,6 +19,7 @@
 // where sum_k x_k comes from one extra MFMA against a ones operand. The codes land in the
 // operand in the order (k0,k4,k1,k5,k2,k6,k3,k7); the activations are permuted to match.
 #include <algorithm>
+#include <utility>
 
 #include "qcommon.hpp"
 #include "qkernels.hpp"
@@ -656,8 +657,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
     xv[e] = *reinterpret_cast<const u32x4*>(xg + m * a.ldx + (c >> 4) * (sstride * 128) + 8 * (c & 15));
   }
   const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
-  const uint32_t qoff = uint32_t(n * a.ldq + kq * 16);
   u32x4 w[C];
+  const uint32_t qoff = uint32_t(n * a.ldq + kq * 16);
 #pragma unroll
   for (int i = 0; i < C; ++i) w[i] = buf_load16(wq, qoff, uint32_t(step0 + i * sstride) * 64);
 
@@ -746,6 +747,508 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
           static_cast<Raw*>(a.y)[m * a.ldy + (nn >> 3) * 4 + (c & 3)] = Act::store(swiglu<Act>(v, up));
       } else {
         static_cast<Raw*>(a.y)[m * a.ldy + nn] = Act::store(v);
+      }
+    }
+  }
+}
+
+
+// ---- line-streaming kernel (M <= 4, nibble codes, group 128) -----------------------------------
+//
+// The one-shot kernel's work split (one workgroup per tile of 16 output features, its waves
+// taking contiguous runs of K), with the codes brought in whole cache lines. The unit is a
+// block of 256 codes: 128 bytes of each of the tile's 16 rows, 2 KB. A wave loads a block with
+// two direct-to-LDS loads, each covering 8 rows x 128 B (every lane 16 bytes), non-temporal,
+// into its own LDS ring of D blocks; the first D blocks are issued before anything else is
+// waited for, and a slot is refilled with the block D further on as soon as it has been read.
+// Inside a load, lane l fetches chunk (l % 8) ^ (l / 8) of row l / 8, so that the MFMA-layout
+// reads that follow (lane (col, kq) reads chunk 4h + kq of row col, one 16-byte read per
+// 128-code step h) hit distinct LDS banks. From there on everything is the one-shot kernel's:
+// the same activation slices, per-step sums, scales and cross-wave reduction.
+template <int I, class F>
+__device__ __forceinline__ void static_for_one(F& f) {
+  f(std::integral_constant<int, I>{});
+}
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (static_for_one<I>(f), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int NB, int D, int MMAX>
+struct LineGeom {
+  static constexpr int kSteps = 2 * NB;                      // 128-code steps per wave
+  static constexpr int kStepPieces = 16;                     // 16-byte x pieces per row and step
+  static constexpr int kRowPieces = kSteps * kStepPieces + 1;  // padded LDS row of a wave's slice
+  static constexpr int kWavePieces = MMAX * kRowPieces + 4;  // + four zero pieces
+  static constexpr int kXPerLane = (MMAX * kSteps * kStepPieces + 63) / 64;
+  __host__ __device__ static int meta_stride(int64_t G) { return int(G) + 4; }
+  // [x slices | x sums | scales | zeros | code rings (256-byte aligned)]
+  __host__ __device__ static size_t code_offset(int nw, int64_t G) {
+    const size_t stage = size_t(nw) * (kWavePieces * 16 + kSteps * 16 * 4) + size_t(2) * 16 * meta_stride(G) * 4;
+    return (stage + 255) / 256 * 256;
+  }
+  static size_t lds_bytes(int nw, int64_t G) {
+    const size_t all = code_offset(nw, G) + size_t(nw) * D * 2048;
+    const size_t red = size_t(nw) * 4 * 64 * 4;
+    return all > red ? all : red;
+  }
+};
+
+template <class Act, int NB, int D, int MMAX, int RM>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)))
+    decode_line_kernel(const LinearArgs a) {
+  using Geo = LineGeom<NB, D, MMAX>;
+  using Raw = typename Act::raw;
+  constexpr int NM = 4;
+  constexpr int C = 2 * NB;
+
+  extern __shared__ u32x4 lds[];
+  const int M = int(a.M);
+  const int G = int(a.G);
+  const int nw = int(blockDim.x) >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;
+  const int kq = lane >> 4;
+  const int64_t tile = blockIdx.x;
+  const bool asym = !a.symmetric;
+  const int step0 = wave * C;
+  const int block0 = wave * NB;
+
+  u32x4* const xw = lds + wave * Geo::kWavePieces;
+  u32x4* const zero4 = xw + MMAX * Geo::kRowPieces;
+  float* const xsum = reinterpret_cast<float*>(lds + nw * Geo::kWavePieces) + wave * C * 16;  // [C][16]
+  const int mstride = Geo::meta_stride(G);
+  float* const s_lds = reinterpret_cast<float*>(lds + nw * Geo::kWavePieces) + nw * C * 16;
+  float* const z_lds = s_lds + 16 * mstride;
+  uint8_t* const ring = reinterpret_cast<uint8_t*>(lds) + Geo::code_offset(nw, G) + size_t(wave) * D * 2048;
+
+  // ---- the tile's scales/zeros and the wave's activation slice, into registers ----
+  const int meta_pieces = 16 * G / 4;  // the host guarantees G % 4 == 0
+  const bool meta_loader = tid < meta_pieces;
+  const uint32_t meta_bytes = uint32_t(a.N * a.G * 4);
+  const auto ms = make_rsrc(a.scales, meta_bytes);
+  const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_bytes);
+  const uint32_t mo = uint32_t(tile * 16 * a.G * 4) + uint32_t(meta_loader ? tid : 0) * 16;
+  const u32x4 sv = buf_load16(ms, mo, 0);  // past the end of the tensors: zeros
+  const u32x4 zv = buf_load16(mz, mo, 0);
+  const Raw* xg = static_cast<const Raw*>(a.x) + int64_t(step0) * 128;
+  u32x4 xv[Geo::kXPerLane];
+#pragma unroll
+  for (int e = 0; e < Geo::kXPerLane; ++e) {
+    int idx = lane + 64 * e;
+    idx = idx < M * C * 16 ? idx : 0;
+    const int m = idx / (C * 16);
+    const int c = idx - m * (C * 16);
+    xv[e] = *reinterpret_cast<const u32x4*>(xg + m * a.ldx + (c >> 4) * 128 + 8 * (c & 15));
+  }
+
+  // ---- the first D code blocks, straight into the LDS ring, issued after the loads above so
+  //      that staging those does not wait for the codes ----
+  __builtin_amdgcn_sched_barrier(0);
+  const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
+  const int r8 = lane >> 3;
+  const uint32_t chunk = uint32_t((lane & 7) ^ r8);
+  uint32_t qoff[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    int64_t n = tile * 16 + 8 * h + r8;
+    n = n < a.N ? n : a.N - 1;  // rows past N repeat row N-1; their sums are never stored
+    qoff[h] = uint32_t(n * a.ldq) + chunk * 16;
+  }
+  auto issue = [&](int ib) {
+    uint8_t* dst = ring + (ib % D) * 2048;
+    const uint32_t so = uint32_t(block0 + ib) * 128;
+    load_lds16(wq, dst, qoff[0], so);
+    load_lds16(wq, dst + 1024, qoff[1], so);
+  };
+#pragma unroll
+  for (int ib = 0; ib < (D < NB ? D : NB); ++ib) issue(ib);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- stage scales/zeros and this wave's activation slice in LDS ----
+  if (meta_loader) {
+    const int row = (tid * 4) / G;
+    const int g = tid * 4 - row * G;
+    *reinterpret_cast<u32x4*>(s_lds + row * mstride + g) = sv;
+    *reinterpret_cast<u32x4*>(z_lds + row * mstride + g) = zv;
+  }
+  if (lane < NM) zero4[lane] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = lane; i < C * 16; i += 64)
+    if ((i & 15) >= M) xsum[i] = 0.0f;
+#pragma unroll
+  for (int e = 0; e < Geo::kXPerLane; ++e) {
+    const int idx = lane + 64 * e;
+    const int m = idx / (C * 16);
+    const int c = idx - m * (C * 16);
+    const uint32_t w4[4] = {xv[e].x, xv[e].y, xv[e].z, xv[e].w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) sum += Act::load(Raw(w4[h] & 0xFFFFu)) + Act::load(Raw(w4[h] >> 16));
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+    if (idx < M * C * 16) {
+      xw[m * Geo::kRowPieces + c] = arrange<Act, kNibble>(xv[e]);
+      if ((c & 15) == 0) xsum[(c >> 4) * 16 + m] = sum;
+    }
+  }
+  // A plain barrier once this wave's LDS writes are done: __syncthreads() would also wait for
+  // every outstanding direct-to-LDS load (its release fence covers them), i.e. for the codes.
+  wait_lgkmcnt0();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // ---- compute, block by block as the ring fills ----
+  const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
+  const float z_shift = Act::kNibbleOffset;
+  const float z_const = a.zero_const + z_shift;
+  const u32x4* const xrow = col < M ? xw + col * Geo::kRowPieces + kq * NM : zero4;
+  const int xstep = col < M ? 4 * NM : 0;
+  const float* const srow = s_lds + col * mstride + step0;
+  const float* const zrow = z_lds + col * mstride + step0;
+  // Byte offset, within a block, of chunk 4h + kq of row col.
+  uint32_t rd_off[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    rd_off[h] = uint32_t((col >> 3) * 1024 + ((col & 7) * 8 + ((4 * h + kq) ^ (col & 7))) * 16);
+  f32x4 tot = {0.f, 0.f, 0.f, 0.f};
+  static_for<NB>([&](auto IB) {
+    constexpr int ib = decltype(IB)::value;
+    constexpr int after = 2 * ((ib + D < NB ? ib + D : NB) - 1 - ib);  // loads issued after block ib's
+    wait_vmcnt<after>();
+    const uint8_t* blk = ring + (ib % D) * 2048;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = 2 * ib + h;
+      const u32x4 w = *reinterpret_cast<const u32x4*>(blk + rd_off[h]);
+      u32x4 xa[NM];
+#pragma unroll
+      for (int j = 0; j < NM; ++j) xa[j] = xrow[i * xstep + j];
+      float xs[RM];
+      if constexpr (RM == 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(xsum + i * 16 + 4 * kq);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xs[r] = v[r];
+      } else {
+        xs[0] = xsum[i * 16 + 4 * kq];
+      }
+      const float sc = srow[i];
+      const float zc = asym ? zrow[i] + z_shift : z_const;
+      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NM; ++j) acc = Mfma16<Act>::run(xa[j], nib.operand(words[j]), acc);
+#pragma unroll
+      for (int r = 0; r < RM; ++r) tot[r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], acc[r]), tot[r]);
+    }
+    if constexpr (ib + D < NB) {
+      wait_lgkmcnt0();  // the slot's reads are done before the load overwrites it
+      issue(ib + D);
+    }
+  });
+
+  // ---- fixed-order reduction over the waves (the K runs): red[wave][r][lane] ----
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int r = 0; r < RM; ++r) red[(wave * 4 + r) * 64 + lane] = tot[r];
+  __syncthreads();
+  if (tid < 16 * M) {
+    const int m = tid >> 4;
+    const int c = tid & 15;
+    const int src_lane = c + 16 * (m >> 2);
+    const int r = m & 3;
+    float v = 0.0f;
+    for (int w2 = 0; w2 < nw; ++w2) v += red[(w2 * 4 + r) * 64 + src_lane];
+    const int64_t nn = tile * 16 + c;
+    if (nn < a.N) {
+      if (a.bias) v += Act::load(static_cast<const Raw*>(a.bias)[nn]);
+      if (a.epilogue == kEpiSwiglu) {
+        // Gate rows 8p .. 8p+3 and up rows 8p+4 .. 8p+7 sit four lanes apart (N % 8 == 0).
+        const float up = __shfl_xor(v, 4, 64);
+        if ((c & 4) == 0)
+          static_cast<Raw*>(a.y)[m * a.ldy + (nn >> 3) * 4 + (c & 3)] = Act::store(swiglu<Act>(v, up));
+      } else {
+        static_cast<Raw*>(a.y)[m * a.ldy + nn] = Act::store(v);
+      }
+    }
+  }
+}
+
+
+// ---- persistent line-streaming kernel (M <= 4, nibble codes, group 128, many tiles) -------------
+//
+// For grids of thousands of 16-feature tiles (gate_up: 1792) one workgroup per tile pays, for
+// every tile, a workgroup launch and a first-data latency that nothing overlaps: measured on
+// MI355X, workgroups of such a grid live ~2.3 us of which ~1.9 us is the wait for their first
+// bytes, and the grid's launches spread over the whole kernel. Here one workgroup per CU walks a
+// strided list of tiles (tile blockIdx.x + j * gridDim.x). Its 8 waves split K (NB blocks of 256
+// codes each per tile). Each wave's LDS ring holds R tiles of its blocks; a slot is refilled with
+// the block R tiles ahead as soon as it has been read, so R tiles stream in while one is
+// computed. The activations and the workgroup's bias values are staged once. Each tile's scales
+// and zeros come in one tile ahead, by direct-to-LDS 4-byte loads laid out [group][row] (so the
+// 16 rows of one group are 16 consecutive floats: conflict-free reads), double-buffered. The
+// per-wave partial sums go to a double-buffered reduction area; one barrier per tile publishes
+// them and the next tile's metadata. Inside the tile loop the only memory loads are these
+// direct-to-LDS loads, issued by every wave in the same order, so every wait is a static count
+// (near the end of the list, where nothing more is loaded ahead, the waits are for everything).
+template <int NB, int R, int MMAX>
+struct PLineGeom {
+  static constexpr int kStepPieces = 16;  // 16-byte x pieces per row and step
+  // LDS: [x: MMAX rows x (steps*16 + 1) pieces][zero pieces: 4][xsum: steps x 16 floats]
+  //      [meta: 2 buffers x (s, z) x G x 16 floats][red: 2 x S x 4 x 64 floats][bias: 16 x tiles]
+  //      [rings: S x R*NB x 2 KB, 256-byte aligned]
+  __host__ __device__ static int row_pieces(int steps) { return steps * kStepPieces + 1; }
+  __host__ __device__ static size_t x_bytes(int steps) { return size_t(MMAX * row_pieces(steps) + 4) * 16; }
+  __host__ __device__ static size_t xsum_bytes(int steps) { return size_t(steps) * 16 * 4; }
+  __host__ __device__ static size_t meta_bytes(int64_t G) { return size_t(2) * 2 * 16 * G * 4; }
+  __host__ __device__ static size_t red_bytes(int nw) { return size_t(2) * nw * 4 * 64 * 4; }
+  __host__ __device__ static size_t bias_bytes(int ntiles) { return size_t(ntiles) * 16 * 4; }
+  __host__ __device__ static size_t ring_offset(int nw, int steps, int64_t G, int ntiles) {
+    const size_t head = x_bytes(steps) + xsum_bytes(steps) + meta_bytes(G) + red_bytes(nw) + bias_bytes(ntiles);
+    return (head + 255) / 256 * 256;
+  }
+  static size_t lds_bytes(int nw, int steps, int64_t G, int ntiles) {
+    return ring_offset(nw, steps, G, ntiles) + size_t(nw) * R * NB * 2048;
+  }
+};
+
+template <class Act, int NB, int R, int MMAX, int RM>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2)))
+    decode_pline_kernel(const LinearArgs a, int ntiles_max) {
+  using Geo = PLineGeom<NB, R, MMAX>;
+  using Raw = typename Act::raw;
+  constexpr int NM = 4;
+  constexpr int NW = 8;      // waves per workgroup
+  constexpr int D = R * NB;  // ring slots per wave
+  static_assert(R == 2, "the wait counts below are written for two tiles ahead");
+
+  extern __shared__ u32x4 lds[];
+  uint8_t* const base = reinterpret_cast<uint8_t*>(lds);
+  const int M = int(a.M);
+  const int G = int(a.G);
+  const int steps = int(a.K / 128);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;
+  const int kq = lane >> 4;
+  const bool asym = !a.symmetric;
+  const int64_t tiles = (a.N + 15) / 16;
+  const int64_t first = blockIdx.x;
+  const int64_t stride = gridDim.x;
+  const int ntiles = int((tiles - first + stride - 1) / stride);  // 1 .. ntiles_max (grid <= tiles)
+
+  const int rp = Geo::row_pieces(steps);
+  u32x4* const xl = lds;                                     // [MMAX][rp] arranged x pieces
+  u32x4* const zero4 = xl + MMAX * rp;                       // 4 zero pieces
+  float* const xsum = reinterpret_cast<float*>(zero4 + 4);   // [steps][16]
+  float* const meta = xsum + steps * 16;                     // [2 buffers][s, z][G][16 rows]
+  float* const red = meta + 2 * 2 * G * 16;                  // [2][NW][4][64]
+  float* const bias_lds = red + 2 * NW * 256;                // [ntiles][16]
+  uint8_t* const ring = base + Geo::ring_offset(NW, steps, G, ntiles_max) + size_t(wave) * D * 2048;
+
+  // ---- activations and bias into registers ----
+  const int x_pieces = M * steps * 16;
+  const Raw* xg = static_cast<const Raw*>(a.x);
+  u32x4 xv[4];  // the host checks x_pieces <= 4 * 512
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    int idx = tid + e * NW * 64;
+    idx = idx < x_pieces ? idx : 0;
+    const int m = idx / (steps * 16);
+    const int c = idx - m * (steps * 16);
+    xv[e] = *reinterpret_cast<const u32x4*>(xg + m * a.ldx + (c >> 4) * 128 + 8 * (c & 15));
+  }
+  // Bias of feature (tile j, c) for tid = 16 * j + c (the host checks 16 * ntiles_max <= 512),
+  // through a buffer resource so that a missing bias or a feature past N reads zero, unbranched.
+  const auto br = make_rsrc(a.bias ? a.bias : a.x, a.bias ? uint32_t(a.N * sizeof(Raw)) : 0u);
+  const int64_t bn = (first + int64_t(tid >> 4) * stride) * 16 + (tid & 15);
+  static_assert(sizeof(Raw) == 2, "16-bit activations");
+  const uint16_t braw = __builtin_amdgcn_raw_buffer_load_b16(
+      br, int(tid < 16 * ntiles && bn < a.N ? uint32_t(bn) * 2u : 0x7FFFFFF0u), 0, kLoadPolicy);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- direct-to-LDS loads: a tile's metadata (MW 4-byte loads per wave) and code blocks ----
+  const uint32_t meta_total = uint32_t(a.N * a.G * 4);
+  const auto ms = make_rsrc(a.scales, meta_total);
+  const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_total);
+  // Metadata loads per wave and tile: 2 arrays x G/4 loads of 64 floats over 8 waves, G / 16 = NB
+  // (default cache policy: each load takes 16 bytes of 16 rows, the other loads of the tile the
+  // rest of those lines)
+  // (the host checks G == 16 * NB). Load q of this wave covers array p / (G/4), 64-float piece
+  // p % (G/4), p = wave * NB + q; lane l takes row l % 16 and group l / 16 + 4 * piece, which
+  // lands at [group][row] in LDS.
+  const uint32_t meta_lane_off = uint32_t(col) * uint32_t(G) * 4 + uint32_t(kq) * 4;
+  auto issue_meta = [&](int j) {
+    const int64_t tile = first + int64_t(j) * stride;
+    float* dstbase = meta + (j & 1) * 2 * G * 16;
+    const uint32_t so = uint32_t(tile * 16 * a.G * 4);  // rows past N: past the tensors, zeros
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int p = wave * NB + q;
+      const int arr = p / (G / 4);
+      const int piece = p - arr * (G / 4);
+      float* dst = dstbase + arr * G * 16 + piece * 64;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arr ? mz : ms, (__attribute__((address_space(3))) void*)dst, 4,
+                                               meta_lane_off + uint32_t(piece) * 16, so, 0, kLoadPolicy);
+    }
+  };
+  const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
+  const int r8 = lane >> 3;
+  const uint32_t chunk_off = uint32_t((lane & 7) ^ r8) * 16;
+  const int block0 = wave * NB;
+  // Block ib of the j-th tile of this workgroup goes to slot (j % R) * NB + ib. Tiles past the
+  // workgroup's list (only when it holds fewer than R) read the last row, and are never used.
+  auto issue = [&](int j, int ib) {
+    const int64_t tile = first + int64_t(j) * stride;
+    uint32_t qo[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int64_t n = tile * 16 + 8 * h + r8;
+      n = n < a.N ? n : a.N - 1;  // rows past N repeat row N-1; their sums are never stored
+      qo[h] = uint32_t(n * a.ldq) + chunk_off;
+    }
+    uint8_t* dst = ring + ((j % R) * NB + ib) * 2048;
+    const uint32_t so = uint32_t(block0 + ib) * 128;
+    load_lds16(wq, dst, qo[0], so);
+    load_lds16(wq, dst + 1024, qo[1], so);
+  };
+  issue_meta(0);
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+#pragma unroll
+    for (int ib = 0; ib < NB; ++ib) issue(j, ib);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- stage the activations (arranged) with per-step sums, and the bias ----
+  for (int i = tid; i < steps * 16; i += NW * 64)
+    if ((i & 15) >= M) xsum[i] = 0.0f;
+  if (tid < 4) zero4[tid] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int idx = tid + e * NW * 64;
+    const int m = idx / (steps * 16);
+    const int c = idx - m * (steps * 16);
+    const uint32_t w4[4] = {xv[e].x, xv[e].y, xv[e].z, xv[e].w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) sum += Act::load(Raw(w4[h] & 0xFFFFu)) + Act::load(Raw(w4[h] >> 16));
+    // The 16 pieces of one step and row sit in 16 consecutive lanes.
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+    if (idx < x_pieces) {
+      xl[m * rp + c] = arrange<Act, kNibble>(xv[e]);
+      if ((c & 15) == 0) xsum[(c >> 4) * 16 + m] = sum;
+    }
+  }
+  if (tid < 16 * ntiles) bias_lds[tid] = Act::load(Raw(braw));
+  wait_vmcnt<2 * D>();  // this wave's metadata loads of tile 0 (the code blocks may still fly)
+  wait_lgkmcnt0();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  // ---- per lane, constant over tiles ----
+  const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
+  const float z_shift = Act::kNibbleOffset;
+  const float z_const = a.zero_const + z_shift;
+  const int step0 = 2 * block0;
+  const u32x4* const xrow = col < M ? xl + col * rp + step0 * 16 + kq * NM : zero4;
+  const int xstep = col < M ? 16 : 0;
+  uint32_t rd_off[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    rd_off[h] = uint32_t((col >> 3) * 1024 + ((col & 7) * 8 + ((4 * h + kq) ^ (col & 7))) * 16);
+  Raw* y = static_cast<Raw*>(a.y);
+
+  for (int j = 0; j < ntiles; ++j) {
+    const int64_t tile = first + int64_t(j) * stride;
+    const int buf = j & 1;
+    const bool more = j + 1 < ntiles;   // load the next tile's metadata
+    const bool ahead = j + R < ntiles;  // refill with the blocks of tile j + R
+    // Loads issued after block ib of this tile, while tiles are still loaded ahead: the D - 1
+    // blocks behind it in the ring and the metadata of the tiles j + 2 - R .. j + 1 that exist
+    // (tile 0's was loaded before any block).
+    const int phase = !ahead ? 0 : (j == 0 ? 1 : 2);
+    if (more) issue_meta(j + 1);
+    const float* sg = meta + buf * 2 * G * 16 + step0 * 16 + col;  // [group][row]
+    const float* zg = sg + G * 16;
+    f32x4 tot = {0.f, 0.f, 0.f, 0.f};
+    const uint8_t* slots = ring + (j % R) * NB * 2048;
+    static_for<NB>([&](auto IB) {
+      constexpr int ib = decltype(IB)::value;
+      if (phase == 2) {
+        wait_vmcnt<2 * (D - 1) + R * NB>();  // R tiles of metadata, NB loads per wave each
+      } else if (phase == 1) {
+        wait_vmcnt<2 * (D - 1) + NB>();      // tile 0: only tile 1's metadata came after its blocks
+      } else {
+        wait_vmcnt<0>();
+      }
+      const uint8_t* blk = slots + ib * 2048;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int i = 2 * ib + h;
+        const u32x4 w = *reinterpret_cast<const u32x4*>(blk + rd_off[h]);
+        u32x4 xa[NM];
+#pragma unroll
+        for (int jj = 0; jj < NM; ++jj) xa[jj] = xrow[i * xstep + jj];
+        float xs[RM];
+        if constexpr (RM == 4) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(xsum + (step0 + i) * 16 + 4 * kq);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xs[r] = v[r];
+        } else {
+          xs[0] = xsum[(step0 + i) * 16 + 4 * kq];
+        }
+        const float sc = sg[i * 16];
+        const float zc = asym ? zg[i * 16] + z_shift : z_const;
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jj = 0; jj < NM; ++jj) acc = Mfma16<Act>::run(xa[jj], nib.operand(words[jj]), acc);
+#pragma unroll
+        for (int r = 0; r < RM; ++r) tot[r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], acc[r]), tot[r]);
+      }
+      if (ahead) {
+        wait_lgkmcnt0();  // the slot's reads are done before the load overwrites it
+        issue(j + R, ib);
+      }
+    });
+    float* rb = red + buf * NW * 256;
+#pragma unroll
+    for (int r = 0; r < RM; ++r) rb[(wave * 4 + r) * 64 + lane] = tot[r];
+    // This wave's metadata loads of tile j + 1 have landed before the barrier publishes them.
+    if (ahead) {
+      wait_vmcnt<2 * NB>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // Fixed-order sum over the waves (the K runs) of this tile's outputs.
+    if (tid < 16 * M) {
+      const int m = tid >> 4;
+      const int c = tid & 15;
+      const int src_lane = c + 16 * (m >> 2);
+      const int r = m & 3;
+      float v = 0.0f;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) v += rb[(w2 * 4 + r) * 64 + src_lane];
+      v += bias_lds[j * 16 + c];
+      const int64_t nn = tile * 16 + c;
+      if (a.epilogue == kEpiSwiglu) {
+        // Gate rows 8p .. 8p+3 and up rows 8p+4 .. 8p+7 sit four lanes apart (N % 8 == 0).
+        const float up = __shfl_xor(v, 4, 64);
+        if ((c & 4) == 0 && nn < a.N) y[m * a.ldy + (nn >> 3) * 4 + (c & 3)] = Act::store(swiglu<Act>(v, up));
+      } else if (nn < a.N) {
+        y[m * a.ldy + nn] = Act::store(v);
       }
     }
   }
@@ -1361,6 +1864,139 @@ bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   return true;
 }
 
+template <class Act, int NB, int D, int MMAX, int RM>
+hipError_t launch_line_cfg(const LinearArgs& a, int nw, hipStream_t stream) {
+  const size_t lds = LineGeom<NB, D, MMAX>::lds_bytes(nw, a.G);
+  auto kernel = decode_line_kernel<Act, NB, D, MMAX, RM>;
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kernel, dim3(unsigned((a.N + 15) / 16)), dim3(unsigned(nw * 64)), lds, stream, a);
+  return hipGetLastError();
+}
+
+template <class Act, int NB, int D>
+hipError_t launch_line_m(const LinearArgs& a, int nw, hipStream_t stream) {
+  if (a.M == 1) return launch_line_cfg<Act, NB, D, 1, 1>(a, nw, stream);
+  return launch_line_cfg<Act, NB, D, 4, 4>(a, nw, stream);
+}
+
+template <class Act>
+hipError_t launch_line(const LinearArgs& a, int nb, int d, int nw, hipStream_t stream) {
+  if (nb == 2) return launch_line_m<Act, 2, 2>(a, nw, stream);
+  if (nb == 4) return d == 4 ? launch_line_m<Act, 4, 4>(a, nw, stream) : launch_line_m<Act, 4, 2>(a, nw, stream);
+  if (nb == 8) return d == 4 ? launch_line_m<Act, 8, 4>(a, nw, stream) : launch_line_m<Act, 8, 2>(a, nw, stream);
+  return d == 4 ? launch_line_m<Act, 16, 4>(a, nw, stream) : launch_line_m<Act, 16, 2>(a, nw, stream);
+}
+
+// One token, 2/4-bit codes, group 128, rows of at least 8192 codes: the line-streaming kernel.
+// Measured on MI355X at one token: down (K 14336) 11.4 -> 9.2 us against the one-shot kernel;
+// on K = 4096 the two are within 2 %, and at 2-4 tokens the one-shot kernel leads.
+bool try_line(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
+  if (a.M != 1 || a.K < 8192) return false;
+  if (a.fmt != kNibble || a.M > 4 || a.group != 128 || a.K % 256 != 0 || a.G % 4 != 0) return false;
+  if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
+  if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
+  if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
+  if ((a.N + 15) / 16 > 0x7FFFFFFF) return false;
+  const int64_t blocks = a.K / 256;
+  // Blocks per wave: the fewest that keep a tile within 16 waves (short runs spread the
+  // per-wave arithmetic over more waves, which finish as their data lands).
+  int nb = 0;
+  for (int c : {2, 4, 8}) {
+    if (c == 8 && a.M > 1) continue;
+    if (blocks % c != 0 || blocks / c > 16) continue;
+    nb = c;
+    break;
+  }
+  if (nb == 0) return false;
+  const int nw = int(blocks / nb);
+  if (16 * a.G / 4 > int64_t(nw) * 64) return false;  // one scale piece per thread
+  // Ring depth: every block of the wave up front when LDS allows, else two.
+  const int mmax = a.M == 1 ? 1 : 4;
+  auto lds_for = [&](int d) {
+    if (mmax == 1) {
+      if (nb == 2) return LineGeom<2, 2, 1>::lds_bytes(nw, a.G);
+      if (nb == 4) return d == 4 ? LineGeom<4, 4, 1>::lds_bytes(nw, a.G) : LineGeom<4, 2, 1>::lds_bytes(nw, a.G);
+      return d == 4 ? LineGeom<8, 4, 1>::lds_bytes(nw, a.G) : LineGeom<8, 2, 1>::lds_bytes(nw, a.G);
+    }
+    if (nb == 2) return LineGeom<2, 2, 4>::lds_bytes(nw, a.G);
+    return d == 4 ? LineGeom<4, 4, 4>::lds_bytes(nw, a.G) : LineGeom<4, 2, 4>::lds_bytes(nw, a.G);
+  };
+  int d = nb == 2 ? 2 : 4;
+  if (lds_for(d) > 96 * 1024) d = 2;
+  if (lds_for(d) > 160 * 1024) return false;
+  *err = a.act == kDtBf16 ? launch_line<ActBf16>(a, nb, d, nw, stream) : launch_line<ActF16>(a, nb, d, nw, stream);
+  return true;
+}
+
+// Tiles of code blocks each wave keeps in flight ahead of the one it computes.
+constexpr int kPlineAhead = 2;
+// Workgroups of the persistent kernel: one per CU of the MI355X.
+constexpr int kPlineGrid = 256;
+
+template <int NB, int MMAX>
+size_t pline_lds(int steps, int64_t G, int ntiles) {
+  return PLineGeom<NB, kPlineAhead, MMAX>::lds_bytes(8, steps, G, ntiles);
+}
+
+template <class Act, int NB, int MMAX, int RM>
+hipError_t launch_pline_cfg(const LinearArgs& a, int grid, int ntiles, hipStream_t stream) {
+  const size_t lds = pline_lds<NB, MMAX>(int(a.K / 128), a.G, ntiles);
+  auto kernel = decode_pline_kernel<Act, NB, kPlineAhead, MMAX, RM>;
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kernel, dim3(unsigned(grid)), dim3(512), lds, stream, a, ntiles);
+  return hipGetLastError();
+}
+
+template <class Act, int NB>
+hipError_t launch_pline_nb(const LinearArgs& a, int grid, int ntiles, hipStream_t stream) {
+  if (a.M == 1) return launch_pline_cfg<Act, NB, 1, 1>(a, grid, ntiles, stream);
+  return launch_pline_cfg<Act, NB, 4, 4>(a, grid, ntiles, stream);
+}
+
+// M <= 4, 2/4-bit codes, group 128, at least four tiles of 16 features per CU: the persistent
+// line-streaming kernel (8 waves per workgroup, K = 4096 or 8192).
+bool try_pline(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
+  // Measured on MI355X (gate_up, N 28672): at one token the one-shot kernel stays ahead (13.4
+  // against 15.5 us); at 2-4 tokens this kernel leads it (15.5-16.2 against 17.8 us).
+  if (a.fmt != kNibble || a.M < 2 || a.M > 4 || a.group != 128 || a.K % 256 != 0) return false;
+  if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
+  if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
+  if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
+  const int64_t tiles = (a.N + 15) / 16;
+  if (tiles < 4 * kPlineGrid) return false;
+  const int64_t blocks = a.K / 256;
+  if (blocks % 8 != 0) return false;
+  const int nb = int(blocks / 8);
+  if (nb != 2 && nb != 4) return false;
+  const int steps = int(a.K / 128);
+  if (a.G != 16 * nb) return false;                 // metadata: G / 16 = NB loads per wave and tile
+  if (a.M * steps * 16 > 4 * 512) return false;     // activations: four pieces per thread
+  const int grid = kPlineGrid;
+  const int64_t ntiles = (tiles + grid - 1) / grid;
+  if (16 * ntiles > 512) return false;              // bias: one value per thread
+  const int mmax = a.M == 1 ? 1 : 4;
+  const size_t lds = mmax == 1 ? (nb == 2 ? pline_lds<2, 1>(steps, a.G, int(ntiles)) : pline_lds<4, 1>(steps, a.G, int(ntiles)))
+                               : (nb == 2 ? pline_lds<2, 4>(steps, a.G, int(ntiles)) : pline_lds<4, 4>(steps, a.G, int(ntiles)));
+  if (lds > 160 * 1024) return false;
+  if (a.act == kDtBf16)
+    *err = nb == 2 ? launch_pline_nb<ActBf16, 2>(a, grid, int(ntiles), stream)
+                   : launch_pline_nb<ActBf16, 4>(a, grid, int(ntiles), stream);
+  else
+    *err = nb == 2 ? launch_pline_nb<ActF16, 2>(a, grid, int(ntiles), stream)
+                   : launch_pline_nb<ActF16, 4>(a, grid, int(ntiles), stream);
+  return true;
+}
+
 // Small M: the streaming kernel, when the step geometry fits and x[M, K] fits in LDS.
 bool try_stream(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.M > 16 || a.epilogue != kEpiNone) return false;
@@ -1603,7 +2239,8 @@ hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* f
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
   if (a.M < 1 || a.M > 64) return hipSuccess;
   hipError_t err = hipSuccess;
-  if (try_oneshot(a, stream, &err) || try_mt(a, stream, &err) || try_stream(a, stream, &err)) {
+  if (try_pline(a, stream, &err) || try_line(a, stream, &err) || try_oneshot(a, stream, &err) ||
+      try_mt(a, stream, &err) || try_stream(a, stream, &err)) {
     *fits = true;
     return err;
   }

@@ -465,3 +465,19 @@ def test_gptq_down_projection_through_the_kernels(gptq_down, symmetric, m):
     hot[torch.arange(len(picks)), torch.from_numpy(picks)] = 1.0
     yh = ops.quant_linear(hot.to(DEV), qt, None, torch.bfloat16)
     np.testing.assert_array_equal(_bits_of(yh), qo.bf16_bits(np.ascontiguousarray(dense[:, picks].T)).view(np.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n, k, symmetric, with_bias", [(16400, 4096, False, True), (28672, 4096, True, False),
+                                                        (16384, 2048, False, False), (20480, 6144, False, True)])
+def test_linear_persistent_line_decode(dtype, m, n, k, symmetric, with_bias):
+    # 1-4 tokens over at least 1024 tiles of 16 features: one workgroup per CU walks a strided
+    # list of tiles (N = 16400: 1025 tiles, the last one partial; K 2048 / 4096 / 6144 give
+    # 1, 2 and 3 blocks of 256 codes per wave, the first and last taken by other kernels).
+    qt = _host_qt(n, k, 4, 128, symmetric, seed=m + n + k)
+    gen = torch.Generator().manual_seed(m)
+    x = torch.randn(m, k, generator=gen).to(dtype)
+    bias = torch.randn(n, generator=gen).to(dtype) if with_bias else None
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None if bias is None else bias.to(DEV), dtype)
+    assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), bias, dtype)) <= TOL[dtype]
