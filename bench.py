@@ -28,10 +28,18 @@ e2e            that workload end to end (config 5): the Llama-3-8B model, every 
                W4 g128 asymmetric, 32 prompts of 512 tokens, one prefill forward, then 128
                greedy decode steps through the paged cache, each step one HIP-graph replay;
                decode and prefill tokens/s (reported, not a roofline figure)
-cpu_baseline   the reference's host sequence (dequantize once, cache the dense bf16 weight,
-               F.linear) on this host's cores, for a bounded number of the same decode steps
+shapes         every projection (qkv, o, gate_up, down) at M in {1, 8, 32, 64} (decode: GB/s and
+               fraction of HBM) and {256, 2048, 8192} (prefill: TFLOP/s and fraction of the dense
+               bf16 MFMA peak), W4 g128 asymmetric, bf16
+bits_sweep     the down projection at 8-bit, 4-bit and 2-bit RTN and 4-bit GPTQ (asymmetric and
+               symmetric; calibrated on 128 seeded embedding rows), M in {1, 32, 2048}
+cpu_baseline   the reference's host sequence (dequantize once, cache the dense weight, F.linear)
+               on this host's cores: `value` is the decode step at M = 1 (bf16, warm); `configs`
+               holds a bounded sample of the reference's CPU configurations -- one fp32 linear
+               (K = N = 4096, M = 1), the four projections at M in {1, 8, 32, 64, 256, 2048}, the
+               bit-width sweep -- warm (dense weight cached) and cold (dequantize + F.linear)
 
-Every single-projection timing (roofline, prefill, --sweep, --bits-sweep) rotates over at least
+Every single-projection timing (roofline, prefill, shapes, bits_sweep) rotates over at least
 512 MiB of that projection's own weight copies.
 
 Modes: default prints the JSON line. `--e2e-only` runs only the end-to-end generation (for a
@@ -39,7 +47,7 @@ kernel trace of it). `--pmc-workload` runs only the dominant kernel and a
 256 MiB copy (for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`); `--traffic-from DIR`
 turns two such rocprofv3 CSV outputs into profiles/traffic_decode_gate_up_m1.json.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--bits-sweep] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-shapes] [--no-cpu]
        [--no-prefill] [--no-e2e] [--e2e-only]
 """
 
@@ -82,9 +90,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=40)
     p.add_argument("--m", type=int, default=1, help="tokens per decode step")
     p.add_argument("--kernel-launches", type=int, default=60, help="timed launches of the dominant kernel")
-    p.add_argument("--sweep", action="store_true", help="also time every projection at M in {1..8192}")
-    p.add_argument("--bits-sweep", action="store_true",
-                   help="also time the down projection at 8/4/2 bits, M in {1, 32, 2048}")
+    p.add_argument("--no-shapes", action="store_true",
+                   help="skip the per-shape block and the bit-width sweep")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-prefill", action="store_true", help="skip the prefill measurement")
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Llama-3-8B generation")
@@ -259,13 +266,15 @@ def main() -> int:
     kernel_us = statistics.mean(times)
     kernel_bytes = algorithmic_bytes(args.m, n, k)
     achieved = kernel_bytes / (kernel_us * 1e-6) / 1e9
+    traffic, traffic_note = _measured_traffic(args.m)
     roofline = {
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": _measured_traffic(args.m),
+        "traffic": traffic,
+        "traffic_source": traffic_note,
         "kernel": f"quantized-linear decode, gate_up M={args.m} (K 4096, N 28672, W4 g128 asym)",
         "algorithmic_bytes": kernel_bytes,
         "mean_launch_us": round(kernel_us, 3),
@@ -307,24 +316,43 @@ def main() -> int:
         result["e2e"] = end_to_end(torch)
     if not args.no_prefill:
         result["prefill"] = prefill(torch, ops, rotations)
-    if args.sweep:
-        result["sweep"] = sweep(torch, ops, rotations)
-    if args.bits_sweep:
-        result["bits_sweep"] = bits_sweep(torch, ops)
+    gptq = None
+    if not args.no_shapes:
+        result["shapes"] = shapes(torch, ops, rotations)
+        result["bits_sweep"], gptq = bits_sweep(torch, ops)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(torch, base, args.m, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(torch, base, args.m, args.cpu_seconds, gptq)
     print(json.dumps(result), flush=True)
     return 0
 
 
+def source_digest() -> str:
+    """sha256 (16 hex digits) of the kernel sources the library is built from: names the build
+    a counter measurement belongs to."""
+    import hashlib
+
+    h = hashlib.sha256()
+    csrc = REPO / "quantized-llm-inference-engine-_amd" / "csrc"
+    for path in sorted(list(csrc.glob("*.hip")) + list(csrc.glob("*.hpp"))):
+        h.update(path.name.encode())
+        h.update(path.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def _measured_traffic(m: int):
-    """HBM bytes per launch of the dominant kernel, from rocprofv3 counters, if recorded."""
+    """HBM bytes per launch of the dominant kernel, from rocprofv3 counters, when they were
+    measured on the kernels of this build; otherwise None and a note naming the build they
+    came from."""
     if not TRAFFIC_FILE.exists() or m != 1:
-        return None
+        return None, "no counter measurement recorded for this workload"
     try:
-        return json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+        rec = json.loads(TRAFFIC_FILE.read_text())
     except (OSError, ValueError):
-        return None
+        return None, "unreadable counter record"
+    if rec.get("build") != source_digest():
+        return None, (f"counters were measured on kernel sources {rec.get('build')}, not on this build "
+                      f"({source_digest()}): {rec.get('hbm_bytes_per_launch')} B per launch then")
+    return rec.get("hbm_bytes_per_launch"), f"rocprofv3 FETCH_SIZE + WRITE_SIZE on this build ({rec.get('build')})"
 
 
 def prefill(torch, ops, rotations):
@@ -374,7 +402,18 @@ def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128, r
     ref_res = ref_gen.generate(prompts, ref_steps)
     # Random-init weights give nearly flat logits, so greedy tokens part ways on rounding noise;
     # the logits themselves are what to compare.
-    diff = float((res.prefill_logits - ref_res.prefill_logits).abs().max() / ref_res.prefill_logits.abs().max())
+    def rel(a, b):
+        a, b = a.double(), b.double()
+        return float((a - b).abs().max() / b.abs().max())
+
+    diff = rel(res.prefill_logits, ref_res.prefill_logits)
+    # The same reference computation in float32 (the dequantized bf16 weights, every activation in
+    # fp32): how far each bf16 computation -- this build's and the reference's -- drifts from it.
+    ref32 = ref.float()
+    exact = GreedyGenerator(ref32, block_size=16, use_graph=False).generate(prompts, 2).prefill_logits
+    del ref32, ref
+    torch.cuda.empty_cache()
+    e_hip, e_ref = rel(res.prefill_logits, exact), rel(ref_res.prefill_logits, exact)
     out = {
         "workload": f"llama3-8b, {seqs} prompts x {prompt_len} tokens, then {steps} greedy steps, W4 g128 asym "
                     "RTN linears (fused qkv and gate_up), bf16, paged KV block 16",
@@ -392,12 +431,23 @@ def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128, r
             "prefill_tokens_per_s": round(seqs * prompt_len / ref_res.prefill_seconds, 1),
             "prefill_logits_max_abs_rel_diff": round(diff, 5),
         },
+        "drift_vs_fp32": {
+            "how": "prefill last-position logits against the reference computation run in float32 "
+                   "(max|a - b| / max|b|)",
+            "this_build_bf16": round(e_hip, 5),
+            "reference_way_bf16": round(e_ref, 5),
+            # The bound the deep-model parity test holds the HIP path to: no more than twice the
+            # reference's own bf16 drift.
+            "within_bound": bool(e_hip <= 2 * e_ref + 2e-3),
+        },
     }
     print(f"# e2e llama3-8b: prefill {out['prefill_ms']} ms ({out['prefill_tokens_per_s']:.0f} tok/s), decode "
           f"{step_ms:.2f} ms/step ({out['decode_tokens_per_s']:.0f} tok/s); the reference's way: decode "
           f"{out['reference_way']['decode_step_ms']:.2f} ms/step, prefill "
           f"{out['reference_way']['prefill_tokens_per_s']:.0f} tok/s", file=sys.stderr, flush=True)
-    del model, ref, gen, ref_gen, res, ref_res
+    print(f"# e2e drift from the fp32 reference: this build {e_hip:.4f}, the reference's bf16 way {e_ref:.4f}",
+          file=sys.stderr, flush=True)
+    del model, gen, ref_gen, res, ref_res
     torch.cuda.empty_cache()
     return out
 
@@ -545,23 +595,51 @@ def dense_comparator(torch, qt, m: int):
     return out
 
 
+def gptq_down(torch, symmetric: bool):
+    """The down projection (K 14336, N 4096) quantized by GPTQQuantizer(4 bits, group 128, damping
+    0.01, activation order) on the GPU, calibrated on H = (2/128) X^T X of 128 rows gathered from a
+    seeded N(0, 1) token-embedding table of width 14336 (seed 2) at seeded random ids (seed 3);
+    weights 0.02 N(0, 1), seed 0."""
+    from llmopt.quantization import GPTQQuantizer
+
+    name, n, k = PROJECTIONS[3]
+    dev = torch.device("cuda:0")
+    table = torch.randn(1024, k, generator=torch.Generator().manual_seed(2))
+    ids = torch.randint(0, 1024, (128,), generator=torch.Generator().manual_seed(3))
+    x_cal = table[ids].to(dev)
+    hessian = (2.0 / 128) * (x_cal.t() @ x_cal)
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(0)) * 0.02).to(dev)
+    return GPTQQuantizer(bits=4, group_size=GROUP, symmetric=symmetric).quantize(w, hessian)
+
+
 def bits_sweep(torch, ops):
-    """The bit-width sweep on the down projection (K 14336, N 4096): asymmetric RTN, group 128,
-    8-bit (one code per byte), 4-bit and 2-bit (two codes per byte), M in {1, 32, 2048}.
-    A GPTQ-quantized 4-bit weight has the 4-bit RTN layout, so it runs the same kernels."""
+    """The bit-width sweep on the down projection (K 14336, N 4096): RTN at 8 bits (one code per
+    byte), 4 and 2 bits (two codes per byte), asymmetric, group 128; and 4-bit GPTQ (asymmetric
+    and symmetric), which has the 4-bit layout. M in {1, 32, 2048}. Returns the rows and the
+    asymmetric GPTQ weight (for the CPU baseline)."""
     from llmopt.quantization import QuantizedTensor, RoundToNearestQuantizer
 
     name, n, k = PROJECTIONS[3]
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(4)
-    rows = []
+    weights = []
     for bits in (8, 4, 2):
         w = torch.randn(n, k, generator=gen, device=dev) * 0.02
-        qt = RoundToNearestQuantizer(bits, GROUP, symmetric=False).quantize(w)
+        weights.append((f"rtn{bits}", RoundToNearestQuantizer(bits, GROUP, symmetric=False).quantize(w)))
         del w
+    t0 = time.perf_counter()
+    gptq_asym = gptq_down(torch, False)
+    weights.append(("gptq4", gptq_asym))
+    weights.append(("gptq4_sym", gptq_down(torch, True)))
+    torch.cuda.synchronize()
+    print(f"# GPTQ quantization of down (asymmetric and symmetric) on the GPU: {time.perf_counter() - t0:.1f} s",
+          file=sys.stderr, flush=True)
+    rows = []
+    for label, qt in weights:
+        bits = qt.bits
         copies = max(2, -(-MIN_ROTATION_BYTES // qt.qweight.numel()))
-        qts = [QuantizedTensor(qt.qweight.clone(), qt.scales.clone(), qt.zeros.clone(), bits, GROUP, False, qt.shape)
-               for _ in range(copies)]
+        qts = [QuantizedTensor(qt.qweight.clone(), qt.scales.clone(), qt.zeros.clone(), bits, GROUP, qt.symmetric,
+                               qt.shape) for _ in range(copies)]
         for m in (1, 32, 2048):
             x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
             ops.quant_linear(x, qts[0], None, torch.bfloat16)
@@ -569,21 +647,22 @@ def bits_sweep(torch, ops):
                 torch, lambda i: ops.quant_linear(x, qts[i % copies], None, torch.bfloat16), 2 * copies, 3
             )
             us = statistics.median(times)
-            gbs = algorithmic_bytes(m, n, k, bits=bits) / (us * 1e-6) / 1e9
+            gbs = algorithmic_bytes(m, n, k, bits=bits, asym=not qt.symmetric) / (us * 1e-6) / 1e9
             tflops = 2 * m * n * k / (us * 1e-6) / 1e12
-            rows.append({"proj": name, "bits": bits, "M": m, "us": round(us, 2), "GB/s": round(gbs, 1),
-                         "hbm_frac": round(gbs / HBM_PEAK_GBS, 3), "TFLOP/s": round(tflops, 2),
-                         "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)})
-            print(f"# bits {name} {bits}-bit M={m:5d} {us:9.2f} us {gbs:8.1f} GB/s {tflops:8.2f} TFLOP/s",
+            rows.append({"proj": name, "weights": label, "bits": bits, "symmetric": qt.symmetric, "M": m,
+                         "us": round(us, 2), "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
+                         "TFLOP/s": round(tflops, 2), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)})
+            print(f"# bits {name} {label:9s} M={m:5d} {us:9.2f} us {gbs:8.1f} GB/s {tflops:8.2f} TFLOP/s",
                   file=sys.stderr, flush=True)
             del x
-        del qts, qt
-    return rows
+        del qts
+    return rows, gptq_asym
 
 
-def sweep(torch, ops, rotations):
-    """Per-projection kernel times for decode and prefill batch sizes, each rotating over at
-    least 512 MiB of that projection's weight copies."""
+def shapes(torch, ops, rotations):
+    """Per-projection kernel times at the decode (M <= 64: HBM-bound, GB/s) and prefill
+    (M >= 256: MFMA-bound, TFLOP/s) batch sizes, each rotating over at least 512 MiB of that
+    projection's weight copies; per-launch medians of graph replays of back-to-back launches."""
     bf16 = torch.bfloat16
     rows = []
     for m in (1, 8, 32, 64, 256, 2048, 8192):
@@ -598,39 +677,109 @@ def sweep(torch, ops, rotations):
             us = statistics.median(times)
             gbs = algorithmic_bytes(m, n, k) / (us * 1e-6) / 1e9
             tflops = 2 * m * n * k / (us * 1e-6) / 1e12
+            decode = m <= 64
             rows.append({
-                "proj": name, "M": m, "us": round(us, 2), "GB/s": round(gbs, 1),
-                "hbm_frac": round(gbs / HBM_PEAK_GBS, 3), "TFLOP/s": round(tflops, 2),
-                "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                "proj": name, "N": n, "K": k, "M": m, "us": round(us, 2), "bound": "hbm" if decode else "mfma",
+                "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 3),
+                "TFLOP/s": round(tflops, 2), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                "frac": round(gbs / HBM_PEAK_GBS if decode else tflops / BF16_PEAK_TFLOPS, 4),
             })
-            print(f"# sweep {name:8s} M={m:5d} {us:9.2f} us {gbs:8.1f} GB/s {tflops:8.2f} TFLOP/s",
-                  file=sys.stderr, flush=True)
+            print(f"# shape {name:8s} M={m:5d} {us:9.2f} us {gbs:8.1f} GB/s ({gbs / HBM_PEAK_GBS:6.1%}) "
+                  f"{tflops:8.2f} TFLOP/s ({tflops / BF16_PEAK_TFLOPS:6.1%})", file=sys.stderr, flush=True)
             del x
     return rows
 
 
-def cpu_baseline(torch, base, m: int, seconds: float):
-    """The reference's host sequence on this machine's cores, on a bounded sample."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(torch, base, m: int, seconds: float, gptq=None):
+    """The reference's host sequence on this machine's cores (`oracle.cpu_reference`, the
+    build's restatement of QuantLinear.forward: dequantize once, cache, F.linear), on a bounded
+    sample. `value`: the decode step (4 projections, M = `m`, bf16, dense weight cached) for
+    `seconds`. `configs`: the reference's CPU configurations, warm (cached weight, median of a
+    few calls) and cold (dequantize + F.linear, once per weight; M does not change its cost)."""
+    from llmopt.quantization import RoundToNearestQuantizer
     from oracle.cpu_reference import ReferenceLinear
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(1)
-    mods = {}
-    for name, n, k in PROJECTIONS:
-        qt = base[name]
-        mods[name] = ReferenceLinear(
-            qt.qweight.cpu(), qt.scales.cpu(), qt.zeros.cpu(), 4, GROUP, False, qt.shape, torch.bfloat16
-        )
-    xs = {name: torch.randn(m, k, generator=gen).to(torch.bfloat16) for name, _, k in PROJECTIONS}
-    step_bytes = sum(algorithmic_bytes(m, n, k) for _, n, k in PROJECTIONS)
+    bf16 = torch.bfloat16
 
-    # Cold: one full step that dequantizes every weight (the reference's first call).
-    t0 = time.perf_counter()
+    def module(qt, dtype):
+        return ReferenceLinear(qt.qweight.cpu(), qt.scales.cpu(), qt.zeros.cpu(), qt.bits, qt.group_size,
+                               qt.symmetric, qt.shape, dtype)
+
+    def timed(fn, reps):
+        out = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            out.append(time.perf_counter() - t0)
+        return statistics.median(out)
+
+    rows = []
+
+    def record(config, label, n, k, mm, bits, asym, warm_s, cold_s, dtype):
+        es = 4 if dtype == torch.float32 else 2
+        nbytes = algorithmic_bytes(mm, n, k, bits=bits, asym=asym) + (es - 2) * (mm * k + mm * n)
+        row = {"config": config, "weights": label, "N": n, "K": k, "M": mm, "dtype": str(dtype).split(".")[-1],
+               "warm_ms": round(warm_s * 1e3, 3), "warm_GB/s": round(nbytes / warm_s / 1e9, 2),
+               "warm_TFLOP/s": round(2 * mm * n * k / warm_s / 1e12, 4)}
+        if cold_s is not None:
+            row["cold_ms"] = round(cold_s * 1e3, 2)
+            row["cold_GB/s"] = round(nbytes / cold_s / 1e9, 3)
+        rows.append(row)
+
+    def run_weight(config, label, qt, ms, dtype):
+        mod = module(qt, dtype)
+        n, k = qt.shape
+        x1 = torch.randn(1, k, generator=gen).to(dtype)
+        t0 = time.perf_counter()
+        mod(x1)  # cold: the first call dequantizes, then multiplies
+        cold = time.perf_counter() - t0
+        for i, mm in enumerate(ms):
+            x = torch.randn(mm, k, generator=gen).to(dtype)
+            reps = 10 if mm <= 64 else 3
+            mod(x)
+            record(config, label, n, k, mm, qt.bits, not qt.symmetric, timed(lambda: mod(x), reps),
+                   cold if i == 0 else None, dtype)
+        del mod
+
+    t_start = time.perf_counter()
+    # Config 1: one fp32 QuantLinear, K = N = 4096, M = 1, RTN b4 asymmetric g128 (weights seed 0).
+    w1 = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0)) * 0.02
+    run_weight("1: fp32 linear", "rtn4", RoundToNearestQuantizer(4, GROUP, symmetric=False).quantize(w1), [1],
+               torch.float32)
+    # Configs 2 and 3: the four projections, decode and prefill batch sizes (M = 8192 skipped:
+    # one such call is ~1 TFLOP of dense bf16 on the host).
+    for name, n, k in PROJECTIONS:
+        run_weight("2+3: projection", name, base[name], [1, 8, 32, 64, 256, 2048], bf16)
+    # Config 4: the bit-width sweep on down.
+    dn, dk = PROJECTIONS[3][1], PROJECTIONS[3][2]
+    gen_w = torch.Generator().manual_seed(4)
+    for bits in (8, 2):
+        w = torch.randn(dn, dk, generator=gen_w) * 0.02
+        run_weight("4: bit width", f"rtn{bits}", RoundToNearestQuantizer(bits, GROUP, symmetric=False).quantize(w),
+                   [1, 32, 2048], bf16)
+    if gptq is not None:
+        run_weight("4: bit width", "gptq4", gptq, [1, 32, 2048], bf16)
+    configs_s = time.perf_counter() - t_start
+
+    # The headline-shaped sample: warm decode steps over the four projections.
+    mods = {name: module(base[name], bf16) for name, _, _ in PROJECTIONS}
+    xs = {name: torch.randn(m, k, generator=gen).to(bf16) for name, _, k in PROJECTIONS}
+    step_bytes = sum(algorithmic_bytes(m, n, k) for _, n, k in PROJECTIONS)
     for name, _, _ in PROJECTIONS:
         mods[name](xs[name])
-    cold_s = time.perf_counter() - t0
-    # Warm: the reference's steady state (cached dense bf16 weight, F.linear only).
     steps = 0
     t0 = time.perf_counter()
     while True:
@@ -641,16 +790,18 @@ def cpu_baseline(torch, base, m: int, seconds: float):
         if elapsed >= seconds or steps >= 10000:
             break
     warm = step_bytes * steps / elapsed / 1e9
+    print(f"# cpu baseline: {warm:.1f} GB/s warm decode step on {threads} threads ({_cpu_model()}); "
+          f"{len(rows)} config rows in {configs_s:.1f} s", file=sys.stderr, flush=True)
     return {
         "value": round(warm, 2),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{steps} warm decode steps (4 projections, M={m}, bf16, dense weight cached) "
-                  f"in {elapsed:.1f} s; cold first step (dequantize + F.linear) {cold_s:.2f} s "
-                  f"= {step_bytes / cold_s / 1e9:.3f} GB/s",
-        "cold_value": round(step_bytes / cold_s / 1e9, 3),
+        "sample": f"{steps} warm decode steps (4 projections, M={m}, bf16, dense weight cached) in {elapsed:.1f} s; "
+                  f"plus {len(rows)} configuration rows in {configs_s:.1f} s",
+        "cpu_model": _cpu_model(),
         "torch": torch.__version__,
+        "configs": rows,
     }
 
 
@@ -664,7 +815,7 @@ def _counter_per_dispatch(csv_path: Path, counter: str):
             name = row["Kernel_Name"]
             value = float(row["Counter_Value"])
             grid = int(row["Grid_Size"])
-            if "decode_oneshot_kernel" in name or "decode_stream_kernel" in name:
+            if "llmopt" in name and "decode_" in name:
                 kern.append(value)
             elif "copy" in name.lower() and grid > 0:
                 copy.append(value)
@@ -697,6 +848,7 @@ def traffic_summary(pmc_dir: Path) -> int:
         "write_scale": round(w_scale, 4),
         "copy_bytes": COPY_BYTES,
         "samples": {"kernel_fetch": len(kf), "kernel_write": len(kw), "copy_fetch": len(cf), "copy_write": len(cw)},
+        "build": source_digest(),
     }
     TRAFFIC_FILE.parent.mkdir(exist_ok=True)
     TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
