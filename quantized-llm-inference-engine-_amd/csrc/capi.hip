@@ -28,7 +28,13 @@ constexpr int64_t kDecodeMaxTokens = 32;
 // Whether the split-K GEMM takes a plain product of this size: every batch above
 // kDecodeMaxTokens, and from 24 tokens the long rows (K >= 8192, down: 40.7 -> 33.8 us at
 // M = 32), where the decode kernels' per-workgroup metadata outgrows them.
-bool gemm_first(int64_t M, int64_t K) { return M > kDecodeMaxTokens || (M >= 24 && K >= 8192); }
+// Batches of 33-64 tokens over at least 1024 tiles of 16 features (gate_up) stay on the decode
+// path, whose N-split kernel streams them faster than the split-K GEMM (gate_up at M = 64: 36.5
+// against 43 us).
+bool gemm_first(int64_t M, int64_t K, int64_t N) {
+  if (M > kDecodeMaxTokens && M <= 64 && N >= 16 * 1024 && K < 8192) return false;
+  return M > kDecodeMaxTokens || (M >= 24 && K >= 8192);
+}
 
 thread_local std::string g_last_error;
 
@@ -136,8 +142,9 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
   if (epilogue != llmopt::kEpiNone) {
     // Kernels with the fused epilogue first.
     if (K > 0 && algo == LLMOPT_ALGO_AUTO) {
-      if (M <= kDecodeMaxTokens) {
+      if (M <= kDecodeMaxTokens || !gemm_first(M, K, N)) {
         err = llmopt::launch_linear_decode(a, s, &fits);
+        if (!fits && M > kDecodeMaxTokens) err = llmopt::launch_linear_gemm(a, s, &fits);
       } else {
         err = llmopt::launch_linear_gemm(a, s, &fits);
         if (!fits && M <= 64) err = llmopt::launch_linear_decode(a, s, &fits);
@@ -159,7 +166,7 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
 
   switch (algo) {
     case LLMOPT_ALGO_AUTO: {
-      bool gemm = gemm_first(M, K);
+      bool gemm = gemm_first(M, K, N);
       if (gemm && M <= kDecodeMaxTokens) {
         // The decode path's K-split kernel first, then the GEMM, which is worth it only with
         // its own K split; each needs its workspace.
@@ -311,7 +318,7 @@ size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int 
   if (M <= 0 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
   const int64_t g = group_size <= 0 ? K : group_size;
   const size_t nx = M <= kDecodeMaxTokens ? llmopt::nx_split_workspace_bytes(M, N, K, g, bits) : 0;
-  if (!gemm_first(M, K)) return nx;
+  if (!gemm_first(M, K, N)) return nx;
   return std::max(nx, llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble));
 }
 
@@ -330,8 +337,8 @@ size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bit
   const int64_t g = group_size <= 0 ? K : group_size;
   const bool nibble = bits == 2 || bits == 4;
   // Sizes whose kernels apply the activation themselves (assuming aligned, contiguous tensors).
-  if (nibble && M <= kDecodeMaxTokens && g % 128 == 0 && K % 128 == 0 && (K / g) % 4 == 0 &&
-      (M <= 4 || K <= 8192))
+  if (nibble && (M <= kDecodeMaxTokens || !gemm_first(M, K, N)) && g % 128 == 0 && K % 128 == 0 &&
+      (K / g) % 4 == 0 && (M <= 4 || K <= 8192))
     return 0;
   if (M > kDecodeMaxTokens && bits >= 1 && bits <= 8 && g % 32 == 0 && K % 64 == 0)
     return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);

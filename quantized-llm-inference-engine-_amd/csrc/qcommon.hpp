@@ -87,6 +87,57 @@ __device__ __forceinline__ float swiglu(float g, float u) {
   return s * ur;
 }
 
+// ---- exact MFMA operands from packed nibbles ------------------------------------------------------
+//
+// A 4-bit code q becomes an exact bf16 (fp16) operand without float math: OR-ing it into the
+// mantissa of 128.0 (1024.0) gives OFF + q. One 32-bit word of eight codes (k0 .. k7, low nibble
+// first) yields four operand words holding the pairs (k0,k4) (k1,k5) (k2,k6) (k3,k7).
+// The mask sits in a VGPR and the magic in an SGPR, so each pair is a single v_and_or_b32 (gfx9
+// VOP3 takes no literal and one scalar operand): 7 VALU ops per 8 codes.
+struct NibbleConsts {
+  uint32_t mask;   // 0x000F000F, VGPR
+  uint32_t magic;  // Act::kNibbleMagic2, SGPR
+  template <class Act>
+  __device__ static NibbleConsts make(uint32_t opaque_zero) {
+    NibbleConsts c;
+    c.mask = 0x000F000Fu | opaque_zero;
+    c.magic = Act::kNibbleMagic2 | opaque_zero;
+    asm("" : "+v"(c.mask));
+    asm("" : "+s"(c.magic));
+    return c;
+  }
+  __device__ u32x4 operand(uint32_t d) const {
+    u32x4 r;
+    r.x = (d & mask) | magic;
+    r.y = ((d >> 4) & mask) | magic;
+    r.z = ((d >> 8) & mask) | magic;
+    r.w = ((d >> 12) & mask) | magic;
+    return r;
+  }
+};
+
+// Eight consecutive activations (x0..x7 in d) rearranged into the code order of the operand
+// above (nibbles) or of the byte-code operands of the decode kernels.
+template <class Act, int FMT>
+__device__ __forceinline__ u32x4 arrange(u32x4 d) {
+  u32x4 o;
+  if constexpr (FMT == kNibble) {  // (x0,x4) (x1,x5) (x2,x6) (x3,x7)
+    o.x = (d.x & 0xFFFFu) | (d.z << 16);
+    o.y = (d.x >> 16) | (d.z & 0xFFFF0000u);
+    o.z = (d.y & 0xFFFFu) | (d.w << 16);
+    o.w = (d.y >> 16) | (d.w & 0xFFFF0000u);
+  } else if constexpr (Act::id == kDtF16) {  // (x0,x2) (x1,x3) (x4,x6) (x5,x7)
+    o.x = (d.x & 0xFFFFu) | (d.y << 16);
+    o.y = (d.x >> 16) | (d.y & 0xFFFF0000u);
+    o.z = (d.z & 0xFFFFu) | (d.w << 16);
+    o.w = (d.z >> 16) | (d.w & 0xFFFF0000u);
+  } else {  // natural order
+    o = d;
+  }
+  return o;
+}
+
+
 // ---- code access -----------------------------------------------------------------------------
 
 // Numeric value of code k of one weight row, exactly as the reference reads it:

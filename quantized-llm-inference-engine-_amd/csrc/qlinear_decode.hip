@@ -74,31 +74,6 @@ struct Codes<Act, kNibble> {
   }
 };
 
-// The same nibble operand with the mask in a VGPR and the magic in an SGPR, so each pair is a
-// single v_and_or_b32 (gfx9 VOP3 takes no literal and one scalar operand): 7 VALU ops per 8
-// codes instead of 11.
-struct NibbleConsts {
-  uint32_t mask;   // 0x000F000F, VGPR
-  uint32_t magic;  // Act::kNibbleMagic2, SGPR
-  template <class Act>
-  __device__ static NibbleConsts make(uint32_t opaque_zero) {
-    NibbleConsts c;
-    c.mask = 0x000F000Fu | opaque_zero;
-    c.magic = Act::kNibbleMagic2 | opaque_zero;
-    asm("" : "+v"(c.mask));
-    asm("" : "+s"(c.magic));
-    return c;
-  }
-  __device__ u32x4 operand(uint32_t d) const {
-    u32x4 r;
-    r.x = (d & mask) | magic;
-    r.y = ((d >> 4) & mask) | magic;
-    r.z = ((d >> 8) & mask) | magic;
-    r.w = ((d >> 12) & mask) | magic;
-    return r;
-  }
-};
-
 template <>
 struct Codes<ActF16, kByte> {
   static constexpr float kOffset = 1024.0f;
@@ -135,26 +110,6 @@ struct Codes<ActBf16, kByte> {
     return r;
   }
 };
-
-// Eight consecutive activations (x0..x7 in d) rearranged into the code order above.
-template <class Act, int FMT>
-__device__ __forceinline__ u32x4 arrange(u32x4 d) {
-  u32x4 o;
-  if constexpr (FMT == kNibble) {  // (x0,x4) (x1,x5) (x2,x6) (x3,x7)
-    o.x = (d.x & 0xFFFFu) | (d.z << 16);
-    o.y = (d.x >> 16) | (d.z & 0xFFFF0000u);
-    o.z = (d.y & 0xFFFFu) | (d.w << 16);
-    o.w = (d.y >> 16) | (d.w & 0xFFFF0000u);
-  } else if constexpr (Act::id == kDtF16) {  // (x0,x2) (x1,x3) (x4,x6) (x5,x7)
-    o.x = (d.x & 0xFFFFu) | (d.y << 16);
-    o.y = (d.x >> 16) | (d.y & 0xFFFF0000u);
-    o.z = (d.z & 0xFFFFu) | (d.w << 16);
-    o.w = (d.z >> 16) | (d.w & 0xFFFF0000u);
-  } else {  // natural order
-    o = d;
-  }
-  return o;
-}
 
 template <int CB>
 __device__ __forceinline__ void load_codes(uint32_t (&dst)[CB / 4], const uint8_t* p) {
@@ -2147,7 +2102,12 @@ bool try_nx(const LinearArgs& a, int64_t steps, uint32_t magic, hipStream_t stre
                      : launch_nx_cfg<Act, 2, 1, 8, 4, 1>(a, magic, stream, splits);
     return true;
   }
-  if (a.M < kNxMinTokens || a.M > 32 || (a.N + 15) / 16 < 1024) return false;
+  if (a.M < kNxMinTokens || a.M > 64 || (a.N + 15) / 16 < 1024) return false;
+  if (a.M > 32) {
+    if (steps % 2 != 0 || nx_lds_bytes<4, 1, 8, 2>(a.G) > 160 * 1024) return false;
+    *err = launch_nx_cfg<Act, 4, 1, 8, 2, 1>(a, magic, stream);
+    return true;
+  }
   if (a.M <= 16) {
     if (steps % 8 != 0 || nx_lds_bytes<1, 1, 8, 8>(a.G) > 160 * 1024) return false;
     *err = launch_nx_cfg<Act, 1, 1, 8, 8, 1>(a, magic, stream);

@@ -105,7 +105,7 @@ def test_swiglu_bias_and_leading_dims():
         assert _rel_err(y, ref) <= SWIGLU_TOL, m
 
 
-@pytest.mark.parametrize("m", [1, 8, 16, 32, 64, 2048])
+@pytest.mark.parametrize("m", [1, 8, 16, 32, 40, 64, 2048])
 def test_swiglu_llama_gate_up(m):
     dtype = torch.bfloat16
     inter, k = 14336, 4096

@@ -218,7 +218,7 @@ def test_linear_batched_decode_ring_configuration(dtype, m, n):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m", [5, 8, 16, 17, 32])
+@pytest.mark.parametrize("m", [5, 8, 16, 17, 32, 33, 47, 64])
 @pytest.mark.parametrize("n, bits, group, symmetric", [(16400, 4, 128, False), (16384, 4, 256, True),
                                                      (16384, 2, 128, False)])
 def test_linear_n_split_decode(dtype, m, n, bits, group, symmetric):
