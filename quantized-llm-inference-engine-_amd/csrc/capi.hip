@@ -170,7 +170,7 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
       if (gemm && M <= kDecodeMaxTokens) {
         // The decode path's K-split kernel first, then the GEMM, which is worth it only with
         // its own K split; each needs its workspace.
-        const size_t nx = llmopt::nx_split_workspace_bytes(M, N, K, a.group, bits);
+        const size_t nx = llmopt::decode_workspace_bytes(M, N, K, a.group, bits);
         const size_t need = llmopt::gemm_workspace_bytes(M, N, K, a.group, a.fmt);
         const bool ws_nx = nx > 0 && a.workspace != nullptr && a.workspace_bytes >= nx;
         gemm = !ws_nx && need > 0 && a.workspace != nullptr && a.workspace_bytes >= need;
@@ -317,7 +317,7 @@ size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int 
   // than 1024 tiles of 16 features; the other decode kernels reduce in LDS.
   if (M <= 0 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
   const int64_t g = group_size <= 0 ? K : group_size;
-  const size_t nx = M <= kDecodeMaxTokens ? llmopt::nx_split_workspace_bytes(M, N, K, g, bits) : 0;
+  const size_t nx = M <= kDecodeMaxTokens ? llmopt::decode_workspace_bytes(M, N, K, g, bits) : 0;
   if (!gemm_first(M, K, N)) return nx;
   return std::max(nx, llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble));
 }

@@ -146,8 +146,8 @@ size_t gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int 
 // y = bias + the fixed-order sum of `splits` fp32 partial products [splits][M][N] (with the
 // SwiGLU epilogue when a.epilogue asks for it).
 hipError_t launch_splitk_reduce(const LinearArgs& a, const float* partials, int splits, hipStream_t stream);
-// Workspace the decode path's K-split N-split kernel uses for these sizes (0 when it does not
-// split); with less, the decode path takes its other kernels.
-size_t nx_split_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
+// Workspace the decode path's K-split kernels (N-split, K-sliced) use for these sizes (0 when
+// they do not split); with less, the decode path takes its other kernels.
+size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
 
 }  // namespace llmopt

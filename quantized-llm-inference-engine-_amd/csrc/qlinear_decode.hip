@@ -1533,14 +1533,31 @@ __global__ void __launch_bounds__(NW * 64)
   const float z_shift = Act::kNibbleOffset;
   const float z_const = a.zero_const + z_shift;
   if (partials) {
-    // The slice's groups: a run of gs floats per row, not 16-byte aligned in general.
-    for (int i = tid; i < 16 * NT * NW * gs; i += NW * 64) {
-      const int row = i / gs;
-      const int gg = i - row * gs;
-      const uint32_t off = uint32_t(((n0 + row) * a.G + g0 + gg) * 4);  // rows past N: zeros
-      const float sc = buf_load_f32(ms, off, 0);
-      const float zr = buf_load_f32(mz, off, 0);
-      sz_lds[row * mstride + gg] = f32x2{sc, asym ? zr + z_shift : z_const};
+    // The slice's groups: a run of gs floats per row, not 16-byte aligned in general. Four
+    // elements per thread are loaded before any is stored, so their round trips overlap.
+    constexpr int kBatch = 4;
+    const int total = 16 * NT * NW * gs;
+    for (int i0 = tid; i0 < total; i0 += kBatch * NW * 64) {
+      float sc[kBatch], zr[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int i = i0 + u * NW * 64;
+        const int row = i / gs;
+        const int gg = i - row * gs;
+        // Rows past N, and elements past the slice's (a repeat of element 0), read past the
+        // end of the tensors or in bounds; only elements of the slice are stored.
+        const uint32_t off = i < total ? uint32_t(((n0 + row) * a.G + g0 + gg) * 4) : 0u;
+        sc[u] = buf_load_f32(ms, off, 0);
+        zr[u] = buf_load_f32(mz, off, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int i = i0 + u * NW * 64;
+        if (i < total) {
+          const int row = i / gs;
+          sz_lds[row * mstride + (i - row * gs)] = f32x2{sc[u], asym ? zr[u] + z_shift : z_const};
+        }
+      }
     }
   }
   for (int p = partials ? pieces : tid; p < pieces; p += NW * 64) {
@@ -1651,6 +1668,208 @@ __global__ void __launch_bounds__(NW * 64)
           y[m * a.ldy + nn] = Act::store(v);
         }
       }
+  }
+}
+
+// ---- K-sliced persistent kernel (2..32 tokens, group a multiple of 128) -----------------------
+//
+// For grids of a few hundred tiles of 16 output features (qkv, o, down) a workgroup per tile
+// reads the whole activation matrix for 16 rows of codes: at 32 tokens over K = 4096 that is
+// 256 KB of activations against 32 KB of codes, and the kernels that split K over the waves of
+// such a workgroup spend most of their time bringing activations in. Here the activations are
+// brought in once per workgroup and reused over many tiles.
+//
+// Workgroup (s, p) of an S x P grid owns the K slice of blocks s * NW .. s * NW + NW - 1 (256
+// codes each) and the tiles p, p + P, p + 2P, ...; wave w owns block b = s * NW + w of each of
+// those tiles. The wave's activations (2 steps x MB token blocks, in MFMA operand order as in
+// the multi-tile kernel, with their per-step sums) are loaded once into registers. The codes of
+// a block come in whole cache lines (two direct-to-LDS loads of 8 rows x 128 bytes, swizzled as
+// in the line-streaming kernel), together with the scales and zeros of its two steps (two
+// 4-byte direct-to-LDS loads), into a per-wave ring of R tiles; a slot is refilled with the tile
+// R further on as soon as it has been read. Every load inside the tile loop goes to LDS, four
+// per tile and wave in one fixed order, so the waits are static counts of the loads issued
+// after a tile's. Per tile the waves' sums meet in LDS (double-buffered, one barrier per tile)
+// and are added in wave order; with S > 1 they go to partials[s][m][n] for the fixed-order
+// reduction kernel, otherwise to y with bias and epilogue.
+//
+// Measured on MI355X (down, K = 14336, at 8 tokens): the workgroups' activations are in after
+// ~1.8 us, the first tile completes at ~4.3 us (the first R tiles of every workgroup arrive as
+// one burst) and the others every ~0.8 us, i.e. ~5.2 TB/s of codes in the steady state. Two
+// other ways of bringing in the scales and zeros measured slower: staging those of all the
+// workgroup's tiles once, along whole rows, behind a barrier (+0.4 us), and each wave loading
+// its own for all its tiles ahead of the codes (+2.4 us). Deeper rings were slower too (R = 4:
+// +1 us, R = 6: +2.6 us), as they lengthen the initial burst.
+template <int NW, int R, int MB>
+struct KsGeom {
+  static constexpr int kCodeBytes = 2048;          // 16 rows x 128 bytes
+  static constexpr int kSlot = kCodeBytes + 512;   // + scales and zeros: 64 floats each
+  static constexpr size_t ring_bytes() { return size_t(NW) * R * kSlot; }
+  static constexpr size_t red_bytes() { return size_t(2) * NW * MB * 4 * 64 * 4; }
+  static constexpr size_t lds_bytes() { return ring_bytes() + red_bytes(); }
+};
+
+template <class Act, int NW, int R, int MB>
+__global__ void __launch_bounds__(NW * 64)
+    decode_ks_kernel(const LinearArgs a, int per_slice, uint32_t group_magic, float* partials) {
+  using Geo = KsGeom<NW, R, MB>;
+  using Raw = typename Act::raw;
+  constexpr int kLoadsPerTile = 4;
+  extern __shared__ u32x4 lds[];
+  uint8_t* const base = reinterpret_cast<uint8_t*>(lds);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;
+  const int kq = lane >> 4;
+  const bool asym = !a.symmetric;
+  const int slice = int(blockIdx.x) / per_slice;
+  const int first = int(blockIdx.x) - slice * per_slice;
+  const int64_t tiles = (a.N + 15) / 16;
+  if (first >= tiles) return;  // the host sizes the grid so that this does not happen
+  const int ntiles = int((tiles - first + per_slice - 1) / per_slice);
+  const int blk = slice * NW + wave;  // this wave's block of 256 codes
+  uint8_t* const ring = base + size_t(wave) * R * Geo::kSlot;
+  float* const red = reinterpret_cast<float*>(base + Geo::ring_bytes());
+
+  // ---- the wave's activations: lane (col, kq), step i, token block mb, MFMA j takes
+  //      x[16 mb + col][256 b + 128 i + 32 kq + 8 j .. + 8]; token rows past M read zeros ----
+  const uint32_t xbytes = uint32_t(a.M * a.ldx * 2);
+  const auto xr = make_rsrc(a.x, xbytes);
+  u32x4 xa[2][MB][4];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int64_t m = 16 * mb + col;
+    const uint32_t row = m < a.M ? uint32_t(m * a.ldx * 2 + (int64_t(blk) * 256 + 32 * kq) * 2) : xbytes;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xa[i][mb][j] = buf_load16(xr, row, uint32_t(128 * i + 8 * j) * 2);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- direct-to-LDS loads of tile j's block into slot j % R ----
+  const uint32_t meta_total = uint32_t(a.N * a.G * 4);
+  const auto ms = make_rsrc(a.scales, meta_total);
+  const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_total);
+  // Metadata: lane l loads row l % 16 of step (l / 16) % 2 of the block (lanes 32..63 repeat
+  // lanes 0..31), landing at float l of the slot's scale (zero) area.
+  const uint32_t mgroup = div_small(uint32_t(2 * blk + ((lane >> 4) & 1)), group_magic);
+  const uint32_t meta_lane = (uint32_t(lane & 15) * uint32_t(a.G) + mgroup) * 4;
+  const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
+  const int r8 = lane >> 3;
+  const uint32_t chunk_off = uint32_t((lane & 7) ^ r8) * 16;
+  const uint32_t code_so = uint32_t(blk) * 128;
+  auto issue = [&](int j) {
+    const int64_t tile = first + int64_t(j) * per_slice;
+    uint8_t* slot = ring + (j % R) * Geo::kSlot;
+    // Rows past N: the metadata reads past the tensors (zeros), the codes repeat row N - 1.
+    const uint32_t mo = uint32_t(tile * 16 * a.G * 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ms, (__attribute__((address_space(3))) void*)(slot + Geo::kCodeBytes),
+                                             4, meta_lane, mo, 0, kLoadPolicy);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(mz, (__attribute__((address_space(3))) void*)(slot + Geo::kCodeBytes + 256),
+                                             4, meta_lane, mo, 0, kLoadPolicy);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int64_t n = tile * 16 + 8 * h + r8;
+      n = n < a.N ? n : a.N - 1;
+      load_lds16(wq, slot + 1024 * h, uint32_t(n * a.ldq) + chunk_off, code_so);
+    }
+  };
+  // The first R tiles (the last one again where the list is shorter: those slots are never read).
+#pragma unroll
+  for (int j = 0; j < R; ++j) issue(j < ntiles ? j : ntiles - 1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- activations into operand order, and their per-step sums (one MFMA chain against ones) ----
+  const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 xs[2][MB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xa[i][mb][j] = arrange<Act, kNibble>(xa[i][mb][j]);
+      xs[i][mb] = Mfma16<Act>::run(xa[i][mb][0], ones, zero4);
+#pragma unroll
+      for (int j = 1; j < 4; ++j) xs[i][mb] = Mfma16<Act>::run(xa[i][mb][j], ones, xs[i][mb]);
+    }
+
+  const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
+  const float z_shift = Act::kNibbleOffset;
+  const float z_const = a.zero_const + z_shift;
+  // Byte offset, within a block, of chunk 4i + kq of row col.
+  uint32_t rd_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    rd_off[i] = uint32_t((col >> 3) * 1024 + ((col & 7) * 8 + ((4 * i + kq) ^ (col & 7))) * 16);
+  const Raw* bias = static_cast<const Raw*>(a.bias);
+  Raw* y = static_cast<Raw*>(a.y);
+  const int M = int(a.M);
+
+  for (int j = 0; j < ntiles; ++j) {
+    const int64_t tile = first + int64_t(j) * per_slice;
+    // Tile j's loads are done once at most those of the tiles after it that were issued, up to
+    // R - 1 of them, are outstanding.
+    const int after = ntiles - 1 - j < R - 1 ? ntiles - 1 - j : R - 1;
+    static_for<R>([&](auto K) {
+      if (after == decltype(K)::value) wait_vmcnt<kLoadsPerTile * decltype(K)::value>();
+    });
+    const uint8_t* slot = ring + (j % R) * Geo::kSlot;
+    const float* sm = reinterpret_cast<const float*>(slot + Geo::kCodeBytes);
+    f32x4 tot[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) tot[mb] = zero4;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(slot + rd_off[i]);
+      const float sc = sm[16 * i + col];
+      const float zc = asym ? sm[64 + 16 * i + col] + z_shift : z_const;
+      const u32x4 b[4] = {nib.operand(w.x), nib.operand(w.y), nib.operand(w.z), nib.operand(w.w)};
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        f32x4 acc = Mfma16<Act>::run(xa[i][mb][0], b[0], zero4);
+#pragma unroll
+        for (int jj = 1; jj < 4; ++jj) acc = Mfma16<Act>::run(xa[i][mb][jj], b[jj], acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          tot[mb][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[i][mb][r], acc[r]), tot[mb][r]);
+      }
+    }
+    if (j + R < ntiles) {
+      wait_lgkmcnt0();  // the slot's reads are done before the loads overwrite it
+      issue(j + R);
+    }
+    // ---- red[buf][wave][mb][r][lane]; one barrier, then the sum over the waves in order ----
+    float* rb = red + (j & 1) * (NW * MB * 256);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rb[((wave * MB + mb) * 4 + r) * 64 + lane] = tot[mb][r];
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (tid < 16 * M) {  // the host checks 16 * M <= NW * 64
+      const int m = tid >> 4;
+      const int c = tid & 15;
+      const int src = ((m >> 4) * 4 + (m & 3)) * 64 + c + 16 * ((m >> 2) & 3);
+      float v = 0.0f;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) v += rb[w2 * MB * 256 + src];
+      const int64_t n = tile * 16 + c;
+      if (partials) {
+        if (n < a.N) partials[(int64_t(slice) * a.M + m) * a.N + n] = v;
+      } else {
+        if (bias && n < a.N) v += Act::load(bias[n]);
+        if (a.epilogue == kEpiSwiglu) {
+          // Gate rows 8p .. 8p+3 and up rows 8p+4 .. 8p+7 sit four lanes apart (N % 8 == 0).
+          const float up = __shfl_xor(v, 4, 64);
+          if (n < a.N && (c & 4) == 0) y[m * a.ldy + (n >> 3) * 4 + (c & 3)] = Act::store(swiglu<Act>(v, up));
+        } else if (n < a.N) {
+          y[m * a.ldy + n] = Act::store(v);
+        }
+      }
+    }
   }
 }
 
@@ -2118,6 +2337,88 @@ bool try_nx(const LinearArgs& a, int64_t steps, uint32_t magic, hipStream_t stre
   return true;
 }
 
+// ---- K-sliced persistent kernel dispatch ----
+
+constexpr int kKsWaves = 8;   // waves per workgroup: a K slice of 8 blocks, 2048 codes
+constexpr int kKsAhead = 3;   // tiles each wave keeps in flight
+constexpr int kKsGrid = 256;  // workgroups: one per CU
+
+struct KsPlan {
+  int slices = 0;     // 0: the kernel does not take the shape
+  int per_slice = 0;  // workgroups per slice
+};
+
+// Token counts and grids where the kernel leads (measured on MI355X against the multi-tile,
+// one-shot and streaming kernels over the Llama-3-8B projections): long rows (K >= 8192) from 5
+// tokens (down at 8 / 16 / 32 tokens: 21.2 / 22.4 / 25.3 -> 14.1 / 15.2 / 19.8 us), K = 4096
+// from 17 (qkv at 24 / 32: 13.2 / 14.4 -> 12.1 / 13.0 us; o: 11.1 / 12.3 -> 10.8 / 11.7 us);
+// below those the activations are small enough for the per-tile kernels. Grids of 1024 tiles
+// or more (gate_up) are faster on the N-split kernel (gate_up at 32 tokens: 24.6 against 28 us).
+// 8 waves, slices of 2048 codes; 16 waves with K = 4096 in one slice and no reduction kernel
+// measured no faster at 2..16 tokens (qkv at 8 tokens: 9.3 against 9.1 us).
+KsPlan plan_ks(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
+  KsPlan p;
+  if (bits != 2 && bits != 4) return p;
+  if (M > 32 || M < (K >= 8192 ? 5 : 17) || group % 128 != 0) return p;
+  const int64_t tiles = (N + 15) / 16;
+  if (tiles >= 1024 || tiles < 1) return p;
+  if (K % (256 * kKsWaves) != 0) return p;
+  const int64_t slices = K / (256 * kKsWaves);
+  if (slices > kKsGrid) return p;
+  p.slices = int(slices);
+  p.per_slice = int(std::min<int64_t>(tiles, std::max<int64_t>(1, kKsGrid / slices)));
+  return p;
+}
+
+size_t ks_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
+  const KsPlan p = plan_ks(M, N, K, group, bits);
+  return p.slices > 1 ? size_t(p.slices) * size_t(M) * size_t(N) * 4 : 0;
+}
+
+template <class Act, int MB>
+hipError_t launch_ks_cfg(const LinearArgs& a, const KsPlan& p, uint32_t magic, hipStream_t stream) {
+  using Geo = KsGeom<kKsWaves, kKsAhead, MB>;
+  static_assert(Geo::lds_bytes() <= 160 * 1024, "LDS of one CU");
+  static_assert(16 * 16 * MB <= kKsWaves * 64, "one reduction thread per output of a tile");
+  auto kern = decode_ks_kernel<Act, kKsWaves, kKsAhead, MB>;
+  const size_t lds = Geo::lds_bytes();
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (e != hipSuccess) return e;
+  }
+  float* partials = p.slices > 1 ? static_cast<float*>(a.workspace) : nullptr;
+  hipLaunchKernelGGL(kern, dim3(unsigned(p.slices * p.per_slice)), dim3(kKsWaves * 64), lds, stream, a,
+                     p.per_slice, magic, partials);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.slices == 1) return e;
+  return launch_splitk_reduce(a, partials, p.slices, stream);
+}
+
+bool try_ks(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
+  if (a.fmt != kNibble) return false;
+  const KsPlan p = plan_ks(a.M, a.N, a.K, a.group, a.bits);
+  if (p.slices == 0) return false;
+  if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
+  if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
+  if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
+  if (a.M * a.ldx * 2 >= (int64_t(1) << 31)) return false;
+  if (p.slices > 1) {
+    const size_t need = size_t(p.slices) * size_t(a.M) * size_t(a.N) * 4;
+    if (!a.workspace || a.workspace_bytes < need || reinterpret_cast<uintptr_t>(a.workspace) % 16 != 0)
+      return false;
+  }
+  const uint32_t per_group = uint32_t(a.group / 128);
+  const uint32_t magic = per_group == 1 ? 0u
+      : uint32_t((uint64_t(1) << 32) / per_group + ((uint64_t(1) << 32) % per_group != 0));
+  if (a.M <= 16)
+    *err = a.act == kDtBf16 ? launch_ks_cfg<ActBf16, 1>(a, p, magic, stream) : launch_ks_cfg<ActF16, 1>(a, p, magic, stream);
+  else
+    *err = a.act == kDtBf16 ? launch_ks_cfg<ActBf16, 2>(a, p, magic, stream) : launch_ks_cfg<ActF16, 2>(a, p, magic, stream);
+  return true;
+}
+
 // M <= 64, 2/4-bit codes, groups of a multiple of 128 codes: the multi-tile kernel.
 bool try_mt(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.fmt != kNibble || a.M < 1 || a.M > 64) return false;
@@ -2187,11 +2488,12 @@ hipError_t launch_skinny(const LinearArgs& a, hipStream_t stream, bool* fits) {
 
 }  // namespace
 
-size_t nx_split_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
+size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   if (bits != 2 && bits != 4) return 0;
-  if (group % 128 != 0 || K % 128 != 0 || (K / group) % 4 != 0) return 0;
+  const size_t ks = ks_workspace_bytes(M, N, K, group, bits);
+  if (group % 128 != 0 || K % 128 != 0 || (K / group) % 4 != 0) return ks;
   const int splits = nx_splits(M, N, K / 128);
-  return splits > 0 ? size_t(splits) * size_t(M) * size_t(N) * 4 : 0;
+  return std::max(ks, splits > 0 ? size_t(splits) * size_t(M) * size_t(N) * 4 : size_t(0));
 }
 
 hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* fits) {
@@ -2199,8 +2501,8 @@ hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* f
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
   if (a.M < 1 || a.M > 64) return hipSuccess;
   hipError_t err = hipSuccess;
-  if (try_pline(a, stream, &err) || try_line(a, stream, &err) || try_oneshot(a, stream, &err) ||
-      try_mt(a, stream, &err) || try_stream(a, stream, &err)) {
+  if (try_pline(a, stream, &err) || try_line(a, stream, &err) || try_ks(a, stream, &err) ||
+      try_oneshot(a, stream, &err) || try_mt(a, stream, &err) || try_stream(a, stream, &err)) {
     *fits = true;
     return err;
   }

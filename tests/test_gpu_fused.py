@@ -105,6 +105,21 @@ def test_swiglu_bias_and_leading_dims():
         assert _rel_err(y, ref) <= SWIGLU_TOL, m
 
 
+@pytest.mark.parametrize("m", [2, 9, 24, 32])
+def test_swiglu_k_sliced_single_slice(m):
+    # K = 2048 over 128 fused tiles: the K-sliced kernel with one slice applies the activation
+    # in its own epilogue.
+    dtype = torch.bfloat16
+    gate = _host_qt(1024, 2048, 4, 128, False, seed=m + 11)
+    up = _host_qt(1024, 2048, 4, 128, False, seed=m + 12)
+    fused = _to_device(interleave_gate_up(gate, up))
+    x = torch.randn(m, 2048, generator=torch.Generator().manual_seed(m)).to(dtype)
+    y = ops.quant_linear_swiglu(x.to(DEV), fused, None, dtype)
+    ref = torch.nn.functional.silu(_ref_linear(x, _oracle_dense(gate), dtype)) * _ref_linear(x, _oracle_dense(up), dtype)
+    assert y.shape == (m, 1024)
+    assert _rel_err(y, ref) <= SWIGLU_TOL, m
+
+
 @pytest.mark.parametrize("m", [1, 8, 16, 32, 40, 64, 2048])
 def test_swiglu_llama_gate_up(m):
     dtype = torch.bfloat16

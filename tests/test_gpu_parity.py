@@ -236,11 +236,11 @@ def test_linear_n_split_decode(dtype, m, n, bits, group, symmetric):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m", [5, 12, 17, 32])
 @pytest.mark.parametrize("n, k, group, symmetric", [(6144, 4096, 128, False), (4096, 14336, 128, False),
-                                                   (2048, 8192, 256, True)])
+                                                   (2048, 8192, 256, True), (4096, 9216, 128, False)])
 def test_linear_n_split_over_k_slices(dtype, m, n, k, group, symmetric):
-    # Fewer than 1024 tiles and long rows: the N-split kernel over K slices (fp32 partial sums
-    # in the workspace, then the fixed-order reduction, which adds the bias), and the same call
-    # through the C-ABI without a workspace, which takes the other decode kernels.
+    # Fewer than 1024 tiles: the kernels that split K over workgroups (fp32 partial sums in the
+    # workspace, then the fixed-order reduction, which adds the bias), and the same call through
+    # the C-ABI without a workspace, which takes the other decode kernels.
     qt = _host_qt(n, k, 4, group, symmetric, seed=m + k)
     gen = torch.Generator().manual_seed(m)
     x = torch.randn(m, k, generator=gen).to(dtype)
@@ -251,11 +251,12 @@ def test_linear_n_split_over_k_slices(dtype, m, n, k, group, symmetric):
     y = ops.quant_linear(xd, dq, bd, dtype)
     assert _rel_err(y, ref) <= TOL[dtype]
     lib = _lib.load_library()
-    # Slices are taken from 12 tokens with K >= 8192, where they give the grid at least 256
-    # workgroups of 8 tiles: down (K 14336) always, K 8192 on 128 tiles from 17 tokens
-    # (chunks of 4 steps instead of 8).
-    splits = m >= 12 and (k == 14336 or (k == 8192 and m >= 17))
-    assert (lib.llmopt_q_linear_workspace(m, n, k, 4, group) > 0) == splits
+    # The K-sliced kernel takes K a multiple of 2048 from 5 tokens with K >= 8192 and from 17
+    # with shorter rows; the N-split kernel slices K = 9216 from 12 tokens (8 or 4 steps a chunk,
+    # 9 slices give the 32 workgroups of 8 tiles 288 in all).
+    ks = k % 2048 == 0 and m >= (5 if k >= 8192 else 17)
+    nx = k == 9216 and m >= 12
+    assert (lib.llmopt_q_linear_workspace(m, n, k, 4, group) > 0) == (ks or nx)
     y2 = torch.empty(m, n, dtype=dtype, device=DEV)
     qw, ldq, sc, zr, _, _, grp, signed = ops._weight_args(dq, xd.device)
     rc = lib.llmopt_q_linear(xd.data_ptr(), m, k, k, qw.data_ptr(), ldq, sc.data_ptr(),
@@ -269,8 +270,9 @@ def test_linear_n_split_over_k_slices(dtype, m, n, k, group, symmetric):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m", [24, 32])
 def test_linear_long_rows_at_24_to_32_tokens(dtype, m):
-    # K >= 8192 from 24 tokens: the split-K GEMM when the workspace is there (ops passes it),
-    # the decode kernels when it is not (a C-ABI caller without one).
+    # K >= 8192 from 24 tokens: a kernel that splits K over workgroups when the workspace is
+    # there (ops passes it; the K-sliced decode kernel on this grid), the decode kernels that
+    # need none when it is not (a C-ABI caller without one).
     qt = _host_qt(512, 8192, 4, 128, False, seed=m)
     x = torch.randn(m, 8192, generator=torch.Generator().manual_seed(m)).to(dtype)
     ref = _reference_linear(x, _oracle_dense(qt), None, dtype)
@@ -465,6 +467,28 @@ def test_gptq_down_projection_through_the_kernels(gptq_down, symmetric, m):
     hot[torch.arange(len(picks)), torch.from_numpy(picks)] = 1.0
     yh = ops.quant_linear(hot.to(DEV), qt, None, torch.bfloat16)
     np.testing.assert_array_equal(_bits_of(yh), qo.bf16_bits(np.ascontiguousarray(dense[:, picks].T)).view(np.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [2, 5, 16, 17, 31, 32])
+@pytest.mark.parametrize("n, k, bits, group, symmetric, with_bias", [
+    (4100, 14336, 4, 128, False, True),  # 257 tiles, the last partial; 7 K slices, 36 workgroups each
+    (6144, 4096, 4, 128, True, False),   # qkv: 2 slices of 128 workgroups, three tiles each
+    (1000, 2048, 4, 256, False, True),   # one slice (no reduction kernel), groups of two steps
+    (4096, 8192, 2, 128, False, False),  # 2-bit codes, 4 slices
+    (2048, 6144, 4, 384, True, True),    # groups of three steps, 3 slices
+])
+def test_linear_k_sliced_decode(dtype, m, n, k, bits, group, symmetric, with_bias):
+    # Fewer than 1024 tiles of 16 features, 5-32 tokens on rows of at least 8192 codes and 17-32
+    # on shorter ones: workgroups own a K slice of 2048 codes and walk a strided list of tiles,
+    # the slices' sums meeting in the reduction kernel (the other token counts check the kernels
+    # that take them on the same shapes).
+    qt = _host_qt(n, k, bits, group, symmetric, seed=m + n + k)
+    gen = torch.Generator().manual_seed(m)
+    x = torch.randn(m, k, generator=gen).to(dtype)
+    bias = torch.randn(n, generator=gen).to(dtype) if with_bias else None
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None if bias is None else bias.to(DEV), dtype)
+    assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), bias, dtype)) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
