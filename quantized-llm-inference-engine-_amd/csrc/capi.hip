@@ -26,13 +26,16 @@ namespace {
 constexpr int64_t kDecodeMaxTokens = 32;
 
 // Whether the split-K GEMM takes a plain product of this size: every batch above
-// kDecodeMaxTokens, and from 24 tokens the long rows (K >= 8192, down: 40.7 -> 33.8 us at
-// M = 32), where the decode kernels' per-workgroup metadata outgrows them.
-// Batches of 33-64 tokens over at least 1024 tiles of 16 features (gate_up) stay on the decode
-// path, whose N-split kernel streams them faster than the split-K GEMM (gate_up at M = 64: 36.5
-// against 43 us).
-bool gemm_first(int64_t M, int64_t K, int64_t N) {
-  if (M > kDecodeMaxTokens && M <= 64 && N >= 16 * 1024 && K < 8192) return false;
+// kDecodeMaxTokens, and from 24 tokens the long rows (K >= 8192), unless the decode path's
+// kernels that split K themselves take them (given a workspace: the caller checks).
+// Batches of 33-64 tokens stay on the decode path where it streams them faster than the split-K
+// GEMM: over at least 1024 tiles of 16 features (gate_up) its N-split kernel (gate_up at M = 64:
+// 36.5 against 43 us), on smaller grids its K-sliced kernel.
+bool gemm_first(int64_t M, int64_t K, int64_t N, int64_t group, int bits) {
+  if (M > kDecodeMaxTokens && M <= 64) {
+    if (N >= 16 * 1024 && K < 8192) return false;
+    if (llmopt::ks_takes(M, N, K, group, bits)) return false;
+  }
   return M > kDecodeMaxTokens || (M >= 24 && K >= 8192);
 }
 
@@ -142,7 +145,7 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
   if (epilogue != llmopt::kEpiNone) {
     // Kernels with the fused epilogue first.
     if (K > 0 && algo == LLMOPT_ALGO_AUTO) {
-      if (M <= kDecodeMaxTokens || !gemm_first(M, K, N)) {
+      if (M <= kDecodeMaxTokens || !gemm_first(M, K, N, a.group, bits)) {
         err = llmopt::launch_linear_decode(a, s, &fits);
         if (!fits && M > kDecodeMaxTokens) err = llmopt::launch_linear_gemm(a, s, &fits);
       } else {
@@ -166,7 +169,7 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
 
   switch (algo) {
     case LLMOPT_ALGO_AUTO: {
-      bool gemm = gemm_first(M, K, N);
+      bool gemm = gemm_first(M, K, N, a.group, bits);
       if (gemm && M <= kDecodeMaxTokens) {
         // The decode path's K-split kernel first, then the GEMM, which is worth it only with
         // its own K split; each needs its workspace.
@@ -313,12 +316,12 @@ int llmopt_q_quantize_rtn(const void* weight, int w_dtype, int64_t ldw, int64_t 
 }
 
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
-  // The GEMM's K split, and the decode path's K-split kernel at 5-32 tokens on grids of fewer
-  // than 1024 tiles of 16 features; the other decode kernels reduce in LDS.
+  // The GEMM's K split, and the decode path's kernels that split K over workgroups (5-64 tokens
+  // on grids of fewer than 1024 tiles of 16 features); the other decode kernels reduce in LDS.
   if (M <= 0 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
   const int64_t g = group_size <= 0 ? K : group_size;
-  const size_t nx = M <= kDecodeMaxTokens ? llmopt::decode_workspace_bytes(M, N, K, g, bits) : 0;
-  if (!gemm_first(M, K, N)) return nx;
+  const size_t nx = M <= 64 ? llmopt::decode_workspace_bytes(M, N, K, g, bits) : 0;
+  if (!gemm_first(M, K, N, g, bits)) return nx;
   return std::max(nx, llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble));
 }
 
@@ -337,7 +340,7 @@ size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bit
   const int64_t g = group_size <= 0 ? K : group_size;
   const bool nibble = bits == 2 || bits == 4;
   // Sizes whose kernels apply the activation themselves (assuming aligned, contiguous tensors).
-  if (nibble && (M <= kDecodeMaxTokens || !gemm_first(M, K, N)) && g % 128 == 0 && K % 128 == 0 &&
+  if (nibble && (M <= kDecodeMaxTokens || !gemm_first(M, K, N, g, bits)) && g % 128 == 0 && K % 128 == 0 &&
       (K / g) % 4 == 0 && (M <= 4 || K <= 8192))
     return 0;
   if (M > kDecodeMaxTokens && bits >= 1 && bits <= 8 && g % 32 == 0 && K % 64 == 0)

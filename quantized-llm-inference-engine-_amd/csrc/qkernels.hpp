@@ -149,5 +149,7 @@ hipError_t launch_splitk_reduce(const LinearArgs& a, const float* partials, int 
 // Workspace the decode path's K-split kernels (N-split, K-sliced) use for these sizes (0 when
 // they do not split); with less, the decode path takes its other kernels.
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
+// Whether the decode path's K-sliced kernel takes this size (given its workspace).
+bool ks_takes(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
 
 }  // namespace llmopt

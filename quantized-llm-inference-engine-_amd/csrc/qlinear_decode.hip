@@ -1671,7 +1671,7 @@ __global__ void __launch_bounds__(NW * 64)
   }
 }
 
-// ---- K-sliced persistent kernel (2..32 tokens, group a multiple of 128) -----------------------
+// ---- K-sliced persistent kernel (5..64 tokens, group a multiple of 128) -----------------------
 //
 // For grids of a few hundred tiles of 16 output features (qkv, o, down) a workgroup per tile
 // reads the whole activation matrix for 16 rows of codes: at 32 tokens over K = 4096 that is
@@ -1849,9 +1849,9 @@ __global__ void __launch_bounds__(NW * 64)
     wait_lgkmcnt0();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (tid < 16 * M) {  // the host checks 16 * M <= NW * 64
-      const int m = tid >> 4;
-      const int c = tid & 15;
+    for (int e = tid; e < 16 * M; e += NW * 64) {
+      const int m = e >> 4;
+      const int c = e & 15;
       const int src = ((m >> 4) * 4 + (m & 3)) * 64 + c + 16 * ((m >> 2) & 3);
       float v = 0.0f;
 #pragma unroll
@@ -2352,14 +2352,15 @@ struct KsPlan {
 // one-shot and streaming kernels over the Llama-3-8B projections): long rows (K >= 8192) from 5
 // tokens (down at 8 / 16 / 32 tokens: 21.2 / 22.4 / 25.3 -> 14.1 / 15.2 / 19.8 us), K = 4096
 // from 17 (qkv at 24 / 32: 13.2 / 14.4 -> 12.1 / 13.0 us; o: 11.1 / 12.3 -> 10.8 / 11.7 us);
-// below those the activations are small enough for the per-tile kernels. Grids of 1024 tiles
-// or more (gate_up) are faster on the N-split kernel (gate_up at 32 tokens: 24.6 against 28 us).
-// 8 waves, slices of 2048 codes; 16 waves with K = 4096 in one slice and no reduction kernel
-// measured no faster at 2..16 tokens (qkv at 8 tokens: 9.3 against 9.1 us).
+// below those the activations are small enough for the per-tile kernels. Up to 64 tokens (four
+// token blocks). Grids of 1024 tiles or more (gate_up) are faster on the N-split kernel
+// (gate_up at 32 tokens: 24.6 against 28 us). 8 waves, slices of 2048 codes; 16 waves with K =
+// 4096 in one slice and no reduction kernel measured no faster at 2..16 tokens (qkv at 8
+// tokens: 9.3 against 9.1 us).
 KsPlan plan_ks(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   KsPlan p;
   if (bits != 2 && bits != 4) return p;
-  if (M > 32 || M < (K >= 8192 ? 5 : 17) || group % 128 != 0) return p;
+  if (M > 64 || M < (K >= 8192 ? 5 : 17) || group % 128 != 0) return p;
   const int64_t tiles = (N + 15) / 16;
   if (tiles >= 1024 || tiles < 1) return p;
   if (K % (256 * kKsWaves) != 0) return p;
@@ -2379,7 +2380,6 @@ template <class Act, int MB>
 hipError_t launch_ks_cfg(const LinearArgs& a, const KsPlan& p, uint32_t magic, hipStream_t stream) {
   using Geo = KsGeom<kKsWaves, kKsAhead, MB>;
   static_assert(Geo::lds_bytes() <= 160 * 1024, "LDS of one CU");
-  static_assert(16 * 16 * MB <= kKsWaves * 64, "one reduction thread per output of a tile");
   auto kern = decode_ks_kernel<Act, kKsWaves, kKsAhead, MB>;
   const size_t lds = Geo::lds_bytes();
   if (lds > 65536) {
@@ -2414,8 +2414,10 @@ bool try_ks(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
       : uint32_t((uint64_t(1) << 32) / per_group + ((uint64_t(1) << 32) % per_group != 0));
   if (a.M <= 16)
     *err = a.act == kDtBf16 ? launch_ks_cfg<ActBf16, 1>(a, p, magic, stream) : launch_ks_cfg<ActF16, 1>(a, p, magic, stream);
-  else
+  else if (a.M <= 32)
     *err = a.act == kDtBf16 ? launch_ks_cfg<ActBf16, 2>(a, p, magic, stream) : launch_ks_cfg<ActF16, 2>(a, p, magic, stream);
+  else
+    *err = a.act == kDtBf16 ? launch_ks_cfg<ActBf16, 4>(a, p, magic, stream) : launch_ks_cfg<ActF16, 4>(a, p, magic, stream);
   return true;
 }
 
@@ -2487,6 +2489,10 @@ hipError_t launch_skinny(const LinearArgs& a, hipStream_t stream, bool* fits) {
 
 
 }  // namespace
+
+bool ks_takes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
+  return plan_ks(M, N, K, group, bits).slices > 0;
+}
 
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   if (bits != 2 && bits != 4) return 0;

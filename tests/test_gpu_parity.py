@@ -470,7 +470,7 @@ def test_gptq_down_projection_through_the_kernels(gptq_down, symmetric, m):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m", [2, 5, 16, 17, 31, 32])
+@pytest.mark.parametrize("m", [2, 5, 16, 17, 31, 32, 33, 48, 64])
 @pytest.mark.parametrize("n, k, bits, group, symmetric, with_bias", [
     (4100, 14336, 4, 128, False, True),  # 257 tiles, the last partial; 7 K slices, 36 workgroups each
     (6144, 4096, 4, 128, True, False),   # qkv: 2 slices of 128 workgroups, three tiles each
@@ -479,7 +479,7 @@ def test_gptq_down_projection_through_the_kernels(gptq_down, symmetric, m):
     (2048, 6144, 4, 384, True, True),    # groups of three steps, 3 slices
 ])
 def test_linear_k_sliced_decode(dtype, m, n, k, bits, group, symmetric, with_bias):
-    # Fewer than 1024 tiles of 16 features, 5-32 tokens on rows of at least 8192 codes and 17-32
+    # Fewer than 1024 tiles of 16 features, 5-64 tokens on rows of at least 8192 codes and 17-64
     # on shorter ones: workgroups own a K slice of 2048 codes and walk a strided list of tiles,
     # the slices' sums meeting in the reduction kernel (the other token counts check the kernels
     # that take them on the same shapes).
