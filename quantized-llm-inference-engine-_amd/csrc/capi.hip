@@ -320,9 +320,11 @@ size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int 
   // on grids of fewer than 1024 tiles of 16 features); the other decode kernels reduce in LDS.
   if (M <= 0 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
   const int64_t g = group_size <= 0 ? K : group_size;
-  const size_t nx = M <= 64 ? llmopt::decode_workspace_bytes(M, N, K, g, bits) : 0;
-  if (!gemm_first(M, K, N, g, bits)) return nx;
-  return std::max(nx, llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble));
+  // The decode path's K split when it has one for these sizes (a call given that much takes
+  // it), else the GEMM's when the GEMM takes the shape.
+  const size_t dec = M <= 64 ? llmopt::decode_workspace_bytes(M, N, K, g, bits) : 0;
+  if (dec > 0 || !gemm_first(M, K, N, g, bits)) return dec;
+  return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
 }
 
 int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,

@@ -2495,11 +2495,13 @@ bool ks_takes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
 }
 
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
+  // The split of the kernel the decode path tries first: the K-sliced kernel, else the N-split
+  // kernel over K slices.
   if (bits != 2 && bits != 4) return 0;
-  const size_t ks = ks_workspace_bytes(M, N, K, group, bits);
-  if (group % 128 != 0 || K % 128 != 0 || (K / group) % 4 != 0) return ks;
+  if (ks_takes(M, N, K, group, bits)) return ks_workspace_bytes(M, N, K, group, bits);
+  if (group % 128 != 0 || K % 128 != 0 || (K / group) % 4 != 0) return 0;
   const int splits = nx_splits(M, N, K / 128);
-  return std::max(ks, splits > 0 ? size_t(splits) * size_t(M) * size_t(N) * 4 : size_t(0));
+  return splits > 0 ? size_t(splits) * size_t(M) * size_t(N) * 4 : 0;
 }
 
 hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* fits) {

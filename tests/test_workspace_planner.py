@@ -1,0 +1,95 @@
+"""Which shapes split K, and into how many slices, as the C ABI reports it on the host.
+
+``llmopt_q_linear_workspace`` is the host side of the kernel choice: it returns the bytes of
+fp32 partial sums (``slices * M * N * 4``) of the kernel a call of that size would pick when it
+splits K over workgroups, and 0 when it does not. These tests pin that choice for the
+Llama-3-8B projections without a GPU (no kernel is launched):
+
+* the K-sliced decode kernel: fewer than 1024 tiles of 16 output features, 2/4-bit codes in
+  groups of a multiple of 128, K a multiple of 2048, 5-64 tokens when K >= 8192 and 17-64 on
+  shorter rows; one slice per 2048 codes (down: 7, qkv and o: 2);
+* the N-split kernel over K slices, only where the K-sliced kernel does not take the shape
+  (K >= 8192 not a multiple of 2048, 12-32 tokens);
+* nothing for gate_up up to 64 tokens (its N-split kernel keeps all of K per workgroup), nor at
+  1-4 tokens anywhere;
+* the prefill GEMM's own plan above 64 tokens.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch  # noqa: F401 - load torch's HIP runtime before the library
+
+from llmopt.kernels import _lib
+
+QKV, O, GATE_UP, DOWN = (6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.library_path().exists():
+        pytest.fail(f"kernel library not built: {_lib.library_path()} (run __graft_entry__.build())")
+    return _lib.load_library()
+
+
+def _ws(lib, m, shape, bits=4, group=128):
+    n, k = shape
+    return lib.llmopt_q_linear_workspace(m, n, k, bits, group)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("m", [5, 8, 16, 24, 32, 33, 48, 64])
+def test_down_takes_seven_k_slices_from_five_tokens(lib, bits, m):
+    assert _ws(lib, m, DOWN, bits) == 7 * m * 4096 * 4
+
+
+@pytest.mark.parametrize("shape", [QKV, O])
+def test_qkv_and_o_take_two_k_slices_from_seventeen_tokens(lib, shape):
+    n = shape[0]
+    for m in range(1, 17):
+        assert _ws(lib, m, shape) == 0, m
+    for m in (17, 24, 31, 32, 33, 48, 64):
+        assert _ws(lib, m, shape) == 2 * m * n * 4, m
+
+
+def test_no_split_at_one_to_four_tokens(lib):
+    for shape in (QKV, O, GATE_UP, DOWN):
+        for m in range(1, 5):
+            assert _ws(lib, m, shape) == 0, (shape, m)
+
+
+def test_gate_up_keeps_all_of_k_up_to_64_tokens(lib):
+    for m in (1, 5, 8, 16, 32, 33, 48, 64):
+        assert _ws(lib, m, GATE_UP) == 0, m
+
+
+def test_slices_follow_k(lib):
+    # One slice per 2048 codes: K = 2048 runs unsplit, 8192 in four slices.
+    assert _ws(lib, 24, (1000, 2048)) == 0
+    assert _ws(lib, 24, (2048, 8192)) == 4 * 24 * 2048 * 4
+    assert _ws(lib, 24, (2048, 6144), group=384) == 3 * 24 * 2048 * 4
+
+
+def test_n_split_k_slices_where_the_k_sliced_kernel_does_not_fit(lib):
+    # K = 9216 is not a multiple of 2048: 9 slices of the N-split kernel from 12 to 32 tokens.
+    for m in range(5, 12):
+        assert _ws(lib, m, (4096, 9216)) == 0, m
+    for m in (12, 16, 17, 32):
+        assert _ws(lib, m, (4096, 9216)) == 9 * m * 4096 * 4, m
+
+
+def test_groups_below_128_and_8_bit_codes_never_take_the_decode_splits(lib):
+    for m in (5, 8, 16):
+        assert _ws(lib, m, DOWN, group=64) == 0
+        assert _ws(lib, m, DOWN, bits=8) == 0
+
+
+def test_prefill_plans_above_64_tokens(lib):
+    # The GEMM's K split is sized by its own plan: a multiple of one fp32 plane of M x N.
+    for shape in (QKV, O, GATE_UP, DOWN):
+        n = shape[0]
+        for m in (65, 256, 2048):
+            ws = _ws(lib, m, shape)
+            assert ws % (m * n * 4) == 0 and ws // (m * n * 4) in (0, 2, 3, 4, 5, 6, 7, 8), (shape, m, ws)
+    # A full grid of 256-token tiles does not split.
+    assert _ws(lib, 8192, GATE_UP) == 0
