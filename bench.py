@@ -45,7 +45,9 @@ Every single-projection timing (roofline, prefill, shapes, bits_sweep) rotates o
 Modes: default prints the JSON line. `--e2e-only` runs only the end-to-end generation (for a
 kernel trace of it). `--pmc-workload` runs only the dominant kernel and a
 256 MiB copy (for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`); `--traffic-from DIR`
-turns two such rocprofv3 CSV outputs into profiles/traffic_decode_gate_up_m1.json.
+turns two such rocprofv3 CSV outputs into profiles/traffic_decode_gate_up_m1.json;
+`--trace-runs CSV` prints a rocprofv3 kernel trace of this script per timed block (run),
+`--trace-kernels CSV` per kernel and grid.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-shapes] [--no-cpu]
        [--no-prefill] [--no-e2e] [--e2e-only]
@@ -99,6 +101,10 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--pmc-workload", action="store_true", help="only the dominant kernel + a copy")
     p.add_argument("--traffic-from", type=str, default=None, help="rocprofv3 --pmc output dir")
+    p.add_argument("--trace-runs", type=str, default=None,
+                   help="rocprofv3 --kernel-trace CSV: print this library's kernels per run of dispatches")
+    p.add_argument("--trace-kernels", type=str, default=None,
+                   help="rocprofv3 --kernel-trace CSV: print every kernel's count and durations per grid")
     return p.parse_args()
 
 
@@ -176,6 +182,10 @@ def main() -> int:
     args = parse_args()
     if args.traffic_from:
         return traffic_summary(Path(args.traffic_from))
+    if args.trace_runs:
+        return trace_runs(Path(args.trace_runs))
+    if args.trace_kernels:
+        return trace_kernels(Path(args.trace_kernels))
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: the quantized-linear kernels run on one device and this "
@@ -823,6 +833,62 @@ def _counter_per_dispatch(csv_path: Path, counter: str):
     # them), not the smaller copies that set up the weight copies.
     flushes = [v for v in copy if v * 1024 >= COPY_BYTES / 4]
     return kern, flushes
+
+
+def _kernel_short_name(name: str) -> str:
+    import re
+
+    name = name.replace("void llmopt::(anonymous namespace)::", "").replace("llmopt::", "")
+    return name.split(">(")[0] + ">" if ">(" in name else re.sub(r"\(.*$", "", name)[:100]
+
+
+def trace_kernels(trace_csv: Path) -> int:
+    """Summarise a rocprofv3 kernel trace per (kernel, grid, workgroup), every kernel of the run:
+    count, mean, median, min and max kernel-only duration in microseconds, VGPR / AGPR counts and
+    LDS bytes, sorted by total time."""
+    stats: dict[tuple, list[float]] = {}
+    regs: dict[tuple, tuple] = {}
+    with open(trace_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            block = int(r["Workgroup_Size_X"])
+            key = (_kernel_short_name(r["Kernel_Name"]), int(r["Grid_Size_X"]) // block, block)
+            stats.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+            regs[key] = (r.get("VGPR_Count", ""), r.get("Accum_VGPR_Count", ""), r.get("LDS_Block_Size", ""))
+    print("count\tmean\tmedian\tmin\tmax\tgrid x workgroup\tVGPR/AGPR\tLDS\tkernel")
+    for key, v in sorted(stats.items(), key=lambda kv: -sum(kv[1])):
+        vg, ag, lds = regs[key]
+        print(f"{len(v)}\t{statistics.mean(v):.2f}\t{statistics.median(v):.2f}\t{min(v):.2f}\t{max(v):.2f}\t"
+              f"{key[1]}x{key[2]}\t{vg}/{ag}\t{lds}\t{key[0]}")
+    return 0
+
+
+def trace_runs(trace_csv: Path, min_launches: int = 8) -> int:
+    """Summarise a rocprofv3 kernel trace of this script by runs: consecutive dispatches of
+    this library's kernels with the same main kernel (name, grid, workgroup) form one run -- one
+    timed block, e.g. one (projection, M) of the per-shape sweep -- and the split-K reductions
+    that follow a kernel are counted with it. Prints one line per run of at least
+    `min_launches` main-kernel dispatches: kernel, grid x workgroup, count, median and mean
+    kernel-only duration in microseconds."""
+    short = _kernel_short_name
+    with open(trace_csv, newline="") as f:
+        rows = sorted((r for r in csv.DictReader(f) if "llmopt" in r["Kernel_Name"]),
+                      key=lambda r: int(r["Start_Timestamp"]))
+    runs: list[tuple[tuple, dict]] = []
+    for r in rows:
+        block = int(r["Workgroup_Size_X"])
+        key = (short(r["Kernel_Name"]), int(r["Grid_Size_X"]) // block, block)
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        if not key[0].startswith("splitk_reduce") and (not runs or runs[-1][0] != key):
+            runs.append((key, {}))
+        if runs:
+            runs[-1][1].setdefault(key, []).append(dur)
+    for i, (main_key, kernels) in enumerate(runs):
+        if len(kernels[main_key]) < min_launches:
+            continue
+        parts = [f"{k[0]} {k[1]}x{k[2]} n={len(v)} median={statistics.median(v):.2f} mean={statistics.mean(v):.2f}"
+                 for k, v in kernels.items()]
+        print(f"run {i}: " + " | ".join(parts))
+    return 0
 
 
 def traffic_summary(pmc_dir: Path) -> int:
