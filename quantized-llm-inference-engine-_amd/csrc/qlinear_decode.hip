@@ -937,7 +937,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
 }
 
 
-// ---- persistent line-streaming kernel (M <= 4, nibble codes, group 128, many tiles) -------------
+// ---- persistent line-streaming kernel (M <= 8, nibble codes, group 128, many tiles) -------------
 //
 // For grids of thousands of 16-feature tiles (gate_up: 1792) one workgroup per tile pays, for
 // every tile, a workgroup launch and a first-data latency that nothing overlaps: measured on
@@ -1012,9 +1012,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
   // ---- activations and bias into registers ----
   const int x_pieces = M * steps * 16;
   const Raw* xg = static_cast<const Raw*>(a.x);
-  u32x4 xv[4];  // the host checks x_pieces <= 4 * 512
+  constexpr int kXPer = MMAX > 4 ? 8 : 4;  // activation pieces per thread
+  u32x4 xv[kXPer];  // the host checks x_pieces <= kXPer * 512
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < kXPer; ++e) {
     int idx = tid + e * NW * 64;
     idx = idx < x_pieces ? idx : 0;
     const int m = idx / (steps * 16);
@@ -1087,7 +1088,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
     if ((i & 15) >= M) xsum[i] = 0.0f;
   if (tid < 4) zero4[tid] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < kXPer; ++e) {
     const int idx = tid + e * NW * 64;
     const int m = idx / (steps * 16);
     const int c = idx - m * (steps * 16);
@@ -2133,15 +2134,17 @@ hipError_t launch_pline_cfg(const LinearArgs& a, int grid, int ntiles, hipStream
 template <class Act, int NB>
 hipError_t launch_pline_nb(const LinearArgs& a, int grid, int ntiles, hipStream_t stream) {
   if (a.M == 1) return launch_pline_cfg<Act, NB, 1, 1>(a, grid, ntiles, stream);
-  return launch_pline_cfg<Act, NB, 4, 4>(a, grid, ntiles, stream);
+  if (a.M <= 4) return launch_pline_cfg<Act, NB, 4, 4>(a, grid, ntiles, stream);
+  return launch_pline_cfg<Act, NB, 8, 4>(a, grid, ntiles, stream);
 }
 
-// M <= 4, 2/4-bit codes, group 128, at least four tiles of 16 features per CU: the persistent
+// 2 <= M <= 8, 2/4-bit codes, group 128, at least four tiles of 16 features per CU: the persistent
 // line-streaming kernel (8 waves per workgroup, K = 4096 or 8192).
 bool try_pline(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   // Measured on MI355X (gate_up, N 28672): at one token the one-shot kernel stays ahead (13.4
-  // against 15.5 us); at 2-4 tokens this kernel leads it (15.5-16.2 against 17.8 us).
-  if (a.fmt != kNibble || a.M < 2 || a.M > 4 || a.group != 128 || a.K % 256 != 0) return false;
+  // against 15.5 us); at 2-4 tokens this kernel leads it (15.5-16.2 against 17.8 us), and at
+  // 5-8 tokens the N-split kernel (17.5-17.9 against 18.0-18.6 us).
+  if (a.fmt != kNibble || a.M < 2 || a.M > 8 || a.group != 128 || a.K % 256 != 0) return false;
   if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
@@ -2154,13 +2157,14 @@ bool try_pline(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (nb != 2 && nb != 4) return false;
   const int steps = int(a.K / 128);
   if (a.G != 16 * nb) return false;                 // metadata: G / 16 = NB loads per wave and tile
-  if (a.M * steps * 16 > 4 * 512) return false;     // activations: four pieces per thread
+  if (a.M * steps * 16 > (a.M > 4 ? 8 : 4) * 512) return false;  // activations: 4 (8) pieces per thread
   const int grid = kPlineGrid;
   const int64_t ntiles = (tiles + grid - 1) / grid;
   if (16 * ntiles > 512) return false;              // bias: one value per thread
-  const int mmax = a.M == 1 ? 1 : 4;
+  const int mmax = a.M == 1 ? 1 : a.M <= 4 ? 4 : 8;
   const size_t lds = mmax == 1 ? (nb == 2 ? pline_lds<2, 1>(steps, a.G, int(ntiles)) : pline_lds<4, 1>(steps, a.G, int(ntiles)))
-                               : (nb == 2 ? pline_lds<2, 4>(steps, a.G, int(ntiles)) : pline_lds<4, 4>(steps, a.G, int(ntiles)));
+                   : mmax == 4 ? (nb == 2 ? pline_lds<2, 4>(steps, a.G, int(ntiles)) : pline_lds<4, 4>(steps, a.G, int(ntiles)))
+                               : (nb == 2 ? pline_lds<2, 8>(steps, a.G, int(ntiles)) : pline_lds<4, 8>(steps, a.G, int(ntiles)));
   if (lds > 160 * 1024) return false;
   if (a.act == kDtBf16)
     *err = nb == 2 ? launch_pline_nb<ActBf16, 2>(a, grid, int(ntiles), stream)

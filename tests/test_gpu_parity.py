@@ -492,11 +492,11 @@ def test_linear_k_sliced_decode(dtype, m, n, k, bits, group, symmetric, with_bia
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("n, k, symmetric, with_bias", [(16400, 4096, False, True), (28672, 4096, True, False),
                                                         (16384, 2048, False, False), (20480, 6144, False, True)])
 def test_linear_persistent_line_decode(dtype, m, n, k, symmetric, with_bias):
-    # 1-4 tokens over at least 1024 tiles of 16 features: one workgroup per CU walks a strided
+    # 1-8 tokens over at least 1024 tiles of 16 features: one workgroup per CU walks a strided
     # list of tiles (N = 16400: 1025 tiles, the last one partial; K 2048 / 4096 / 6144 give
     # 1, 2 and 3 blocks of 256 codes per wave, the first and last taken by other kernels).
     qt = _host_qt(n, k, 4, 128, symmetric, seed=m + n + k)
