@@ -8,8 +8,8 @@
 // A operand of that instruction gives lane l row l % 32 and eight consecutive k of half l / 32,
 // which is exactly one 32-bit word of packed 4-bit codes. Each wave therefore loads its own
 // weight rows straight from HBM (one 16-byte load per 32-row tile per 64-wide k stage),
-// dequantizes them in registers with the reference's arithmetic -- fp32 (q - z), then * s,
-// each rounded once, then a round-to-nearest-even cast -- and feeds them to the MFMAs. Only
+// dequantizes them in registers to the reference's values -- fp32 (q - z) * s rounded once,
+// then a round-to-nearest-even cast -- and feeds them to the MFMAs. Only
 // the activations go through LDS, so an MFMA costs half a kilobyte of LDS reads instead of a
 // kilobyte (LDS reads and MFMAs compete on this part), and no weight is dequantized twice.
 //
@@ -83,21 +83,36 @@ struct Mfma32x<ActF16> {
 // (8 rows, all chunks).
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
-// Eight packed codes (one 32-bit word) -> the A fragment of one k-slice: four words holding
-// bf16/fp16 pairs (k, k + 1). The nibble mask comes from a kernel argument (its extra bits are
-// always zero), so the compiler cannot tell that only four bits per byte survive and converts
-// each code with one v_cvt_f32_ubyte{0..3}.
+// Per (row, group) constants of the biased dequantization below. For an integer zero point z
+// with 16 - z in [0, 240] and |s| < 2^120, adding b = 16 - z to every code byte (no carry
+// crosses a byte: q + b <= 255) gives f = q + 16 - z exactly, and fma(f, s, -16 s) rounds the
+// exact value (q - z) s once, as the reference's (q - z) * s does (16 s is exact). Any other
+// (s, z) -- fractional or out-of-range zero points, huge or non-finite scales, none of which
+// the quantizers produce -- takes b = 0 and fma(q, s, -z s), within an ulp of the reference.
+struct BiasedMeta {
+  uint32_t bias;  // b replicated into the four bytes
+  float c;        // -16 s, or -z s
+};
+__device__ __forceinline__ BiasedMeta biased_meta(float z, float s) {
+  const bool exact = z == __builtin_rintf(z) && z >= -224.0f && z <= 16.0f && __builtin_fabsf(s) < 0x1p120f;
+  BiasedMeta m;
+  m.bias = exact ? uint32_t(16 - int(z)) * 0x01010101u : 0u;
+  m.c = exact ? -16.0f * s : -(z * s);
+  return m;
+}
+
+// Eight packed codes (one 32-bit word) -> the A fragment of one k-slice with the biased
+// arithmetic above: per 8 codes two masks, a shift, two byte-wise adds, 8 conversions, 8 fmas
+// and 4 packs (3.1 VALU per code against 3.9 for a subtraction and a multiplication each).
 template <class Act>
-__device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t nib_mask, float z, float s) {
-  // Byte lanes of a vector (rather than shifts and masks) make every code one
-  // v_cvt_f32_ubyte{0..3}; a shift-and-mask of byte 2 becomes v_bfe_u32 plus a conversion.
-  const uc4 lo = __builtin_bit_cast(uc4, word & nib_mask);         // codes 0, 2, 4, 6
-  const uc4 hi = __builtin_bit_cast(uc4, (word >> 4) & nib_mask);  // codes 1, 3, 5, 7
+__device__ __forceinline__ u32x4 dequant8_biased(uint32_t word, uint32_t nib_mask, BiasedMeta m, float s) {
+  const uc4 lo = __builtin_bit_cast(uc4, (word & nib_mask) + m.bias);         // codes 0, 2, 4, 6
+  const uc4 hi = __builtin_bit_cast(uc4, ((word >> 4) & nib_mask) + m.bias);  // codes 1, 3, 5, 7
   u32x4 out;
-  out.x = Mfma32x<Act>::pack(dequant_exact(float(lo.x), z, s), dequant_exact(float(hi.x), z, s));
-  out.y = Mfma32x<Act>::pack(dequant_exact(float(lo.y), z, s), dequant_exact(float(hi.y), z, s));
-  out.z = Mfma32x<Act>::pack(dequant_exact(float(lo.z), z, s), dequant_exact(float(hi.z), z, s));
-  out.w = Mfma32x<Act>::pack(dequant_exact(float(lo.w), z, s), dequant_exact(float(hi.w), z, s));
+  out.x = Mfma32x<Act>::pack(__builtin_fmaf(float(lo.x), s, m.c), __builtin_fmaf(float(hi.x), s, m.c));
+  out.y = Mfma32x<Act>::pack(__builtin_fmaf(float(lo.y), s, m.c), __builtin_fmaf(float(hi.y), s, m.c));
+  out.z = Mfma32x<Act>::pack(__builtin_fmaf(float(lo.z), s, m.c), __builtin_fmaf(float(hi.z), s, m.c));
+  out.w = Mfma32x<Act>::pack(__builtin_fmaf(float(lo.w), s, m.c), __builtin_fmaf(float(hi.w), s, m.c));
   return out;
 }
 
@@ -185,6 +200,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   static_assert(GP == 1 || GP == 2, "metadata period of one or two stages");
   u32x4 wring[kRing][2][kCB];
   float sring[kRing][2], zring[kRing][2];
+  // Nibble codes: the biased-dequantization constants of each meta slot, derived from its
+  // loaded scale and zero point once per slot, a stage or more after the loads were issued.
+  BiasedMeta bring[kRing][2];
   auto load_codes = [&](int slot, int kt) {
     const int ktc = kt_base + (kt < ktiles ? kt : ktiles - 1);
 #pragma unroll
@@ -259,14 +277,20 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
       bf[j] = *reinterpret_cast<const u32x4*>(buf + swz(32 * j + frow, 4 * half + ks));
   };
   auto word = [](const u32x4& q, int w) { return w == 0 ? q.x : w == 1 ? q.y : w == 2 ? q.z : q.w; };
+  auto prep_meta = [&](int slot) {
+    if constexpr (FMT == kNibble) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) bring[slot][i] = biased_meta(asym ? zring[slot][i] : z_const, sring[slot][i]);
+    }
+  };
   auto dequant_a = [&](int u, int ks, u32x4* af) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const float z = (asym ? zring[u / GP][i] : z_const) + z_flip;
       if constexpr (FMT == kNibble) {
-        af[i] = dequant8<Act>(word(wring[u][i][0], ks), nib_mask, z, sring[u / GP][i]);
+        af[i] = dequant8_biased<Act>(word(wring[u][i][0], ks), nib_mask, bring[u / GP][i], sring[u / GP][i]);
       } else {
         // Codes 8ks .. 8ks + 7 of the lane's 32: words 2ks and 2ks + 1 of its 32 bytes.
+        const float z = (asym ? zring[u / GP][i] : z_const) + z_flip;
         const u32x4 q = wring[u][i][ks >> 1];
         af[i] = dequant8_bytes<Act>(word(q, (2 * ks) & 3) ^ flip, word(q, (2 * ks + 1) & 3) ^ flip, z,
                                     sring[u / GP][i]);
@@ -275,6 +299,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   };
   u32x4 af[2], bf[TT];
   read_b(xs0, 0, bf);
+  prep_meta(0);
   dequant_a(0, 0, af);
 
   // Stage kt uses LDS buffer kt % 4 and ring slot kt % 4; stages are walked four at a time so
@@ -288,6 +313,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
   auto stage = [&](const int u, const int kt) {
     const uint8_t* cur = xbuf(u);
     const uint8_t* nxt = xbuf((u + 1) % 4);
+    // The next stage opens meta slot ((u + 1) % 4) / GP: its loads were issued at the end of
+    // stage kt + 1 - GP or earlier, and the slot's previous stages were dequantized by now.
+    if (((u + 1) % 4) % GP == 0) prep_meta(((u + 1) % 4) / GP);
     stash_x(xbuf((u + 2) % 4));  // stage kt + 2 (past the end: a clamped stage nobody reads)
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {

@@ -415,6 +415,43 @@ def test_down_projection_bit_width_sweep(bits, symmetric, m):
     assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= 1e-2
 
 
+def _unusual_metadata_qt():
+    """W4 g128 weights whose metadata leaves what the quantizers produce: fractional and
+    negative zero points, zero points of 16, scales of 2^100 and 2^121."""
+    qt = _host_qt(512, 1024, 4, 128, False, seed=7)
+    scales, zeros = qt.scales.clone(), qt.zeros.clone()
+    zeros[0::5] += 0.5
+    zeros[1::5] = -3.0
+    zeros[2::5] = 16.0
+    scales[3::10] *= 2.0 ** 100
+    scales[8::10] *= 2.0 ** 121
+    return QuantizedTensor(qt.qweight, scales, zeros, 4, 128, False, qt.shape)
+
+
+@pytest.mark.parametrize("m", [256, 2048])
+def test_prefill_unusual_zero_points_and_scales(m):
+    # The prefill GEMM's dequantization adds 16 - z to the code bytes when z is an integer in
+    # [-224, 16] and |s| < 2^120 (bit-exact), and falls back to fma(q, s, -z s) otherwise.
+    qt = _unusual_metadata_qt()
+    dqt = _to_device(qt)
+    dense = _oracle_dense(qt)
+    x = torch.randn(m, 1024, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    y = ops.quant_linear(x.to(DEV), dqt, None, torch.bfloat16, algo=ALGO_PREFILL).float().cpu()
+    ref = _reference_linear(x, dense, None, torch.bfloat16).float()
+    # Rows differ in scale by up to 2^121: compare each output feature against its own range.
+    err = (y - ref).abs().amax(dim=0) / ref.abs().amax(dim=0).clamp_min(1e-30)
+    assert float(err.max()) <= 1e-2
+    # One-hot rows return the weight column bit for bit where the zero point is an integer in
+    # range and the scale below 2^120 (every row but the fractional-zero and 2^121-scale ones).
+    picks = np.random.default_rng(m).choice(1024, size=m, replace=True)
+    oh = torch.zeros(m, 1024, dtype=torch.bfloat16)
+    oh[torch.arange(m), torch.from_numpy(picks)] = 1.0
+    y1 = ops.quant_linear(oh.to(DEV), dqt, None, torch.bfloat16, algo=ALGO_PREFILL)
+    exact_rows = np.array([r for r in range(512) if r % 5 != 0 and r % 10 != 8])
+    expect = qo.bf16_bits(np.ascontiguousarray(dense[:, picks].T)).view(np.int16)
+    np.testing.assert_array_equal(_bits_of(y1)[:, exact_rows], expect[:, exact_rows])
+
+
 def test_fp32_compute_single_linear_config():
     # The reference's CPU configuration: K = N = 4096, fp32, M = 1, RTN b4 asym g128.
     qt = _host_qt(4096, 4096, 4, 128, False, seed=0)
