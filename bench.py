@@ -8,7 +8,8 @@ with 4-bit asymmetric round-to-nearest weights, group 128, in the reference's pa
 ~N(0, 0.02), all synthetic and seeded. Steps cycle through enough distinct layer copies
 (>= 512 MiB of packed weights) that the 256 MB Infinity Cache cannot hold them: every step
 streams its weights from HBM, like a decode walking through a model's layers. Inputs are
-resident in HBM before timing; each step is one HIP graph of the four launches.
+resident in HBM before timing; the layer copies' steps (four launches each) are one HIP graph,
+replayed as a whole, as a decode step of a model runs its layers from one graph.
 
 value          algorithmic bytes of all timed steps / timed seconds, where one call moves
                N*K/2 (codes) + 4*N*G*2 (scales, zeros; G = K/128) + 2*M*K + 2*M*N bytes
@@ -237,7 +238,9 @@ def main() -> int:
     outs = {p: torch.empty(args.m, pn, dtype=bf16, device="cuda:0") for p, pn, _ in PROJECTIONS}
     step_bytes = sum(algorithmic_bytes(args.m, pn, pk) for _, pn, pk in PROJECTIONS)
 
-    # One HIP graph per layer copy: the four launches of a step, replayed back to back.
+    # The layer copies in one HIP graph, as a decode step of a model walks through its layers:
+    # `copies` steps (four launches each) per replay. Steps that do not fill a whole replay run
+    # from one-layer graphs of the same launches.
     stream = torch.cuda.Stream()
     graphs = []
     with torch.cuda.stream(stream):
@@ -251,19 +254,29 @@ def main() -> int:
                 for p, _, _ in PROJECTIONS:
                     outs[p] = ops.quant_linear(xs[p], layer[p], None, bf16)
             graphs.append(g)
+        model_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(model_graph, stream=stream):
+            for layer in layers:
+                for p, _, _ in PROJECTIONS:
+                    outs[p] = ops.quant_linear(xs[p], layer[p], None, bf16)
     torch.cuda.synchronize()
 
+    def run_steps(count):
+        for _ in range(count // copies):
+            model_graph.replay()
+        for i in range(count % copies):
+            graphs[i].replay()
+
     print(f"# decode step: 4 projections, M={args.m}, {copies} layer copies "
-          f"({copies * layer_bytes / 2**20:.0f} MiB packed)", file=sys.stderr, flush=True)
-    for i in range(args.warmup):
-        graphs[i % copies].replay()
+          f"({copies * layer_bytes / 2**20:.0f} MiB packed), {copies} steps per graph replay",
+          file=sys.stderr, flush=True)
+    run_steps(args.warmup)
     torch.cuda.synchronize()
     cur = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(cur)
-    for i in range(args.steps):
-        graphs[i % copies].replay()
+    run_steps(args.steps)
     end.record(cur)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
@@ -314,6 +327,7 @@ def main() -> int:
             "group": GROUP,
             "symmetric": False,
             "layer_copies": copies,
+            "steps_per_graph_replay": copies,
             "bytes_per_step": step_bytes,
             "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         },
