@@ -1672,6 +1672,230 @@ __global__ void __launch_bounds__(NW * 64)
   }
 }
 
+// ---- activations in whole lines -------------------------------------------------------------
+//
+// The decode kernels' MFMA layout gives lane (col, kq) the activations x[row col][32 kq + 8 j ..]
+// of a 128-code step as fragment j: one 16-byte load per j puts 16 rows x 4 pieces spaced 64
+// bytes apart in flight, half of every line it touches, and the four loads of a step touch the
+// same 32 lines four times over. Broadcast to every CU, as the decode grids need it, that L2
+// traffic is what costs: at 32 tokens over K = 4096 (256 KB per CU) the fragment-shaped loads
+// took ~6 us of an o projection's 10.6 us. Instead each block of 16 token rows x one step
+// (16 x 256 bytes) comes in as four loads of 4 rows x 256 bytes -- whole lines -- and goes
+// through a per-wave LDS tile (rows padded to kXTileRow bytes, so the column reads below hit
+// 16 distinct bank groups) into the MFMA layout. Token rows past M read zeros.
+constexpr int kXTileRow = 272;
+constexpr int kXTileBytes = 16 * kXTileRow;
+
+// Raw loads of steps [step0, step0 + NS) of token blocks 0 .. MB - 1: piece [i][mb][h] holds
+// row 16 mb + 4 h + lane / 16, bytes 16 (lane % 16) of the step.
+template <int NS, int MB>
+__device__ __forceinline__ void load_x_lines(u32x4 (&raw)[NS][MB][4], const LinearArgs& a, int64_t step0) {
+  const uint32_t xbytes = uint32_t(a.M * a.ldx * 2);
+  const auto xr = make_rsrc(a.x, xbytes);
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int64_t m = 16 * mb + 4 * h + (lane >> 4);
+      const uint32_t row = m < a.M ? uint32_t((m * a.ldx + step0 * 128) * 2 + 16 * (lane & 15)) : xbytes;
+#pragma unroll
+      for (int i = 0; i < NS; ++i) raw[i][mb][h] = buf_load16(xr, row, uint32_t(i) * 256);
+    }
+}
+
+// The same pieces rearranged through the wave's LDS tile into MFMA fragments: frag[i][mb][j] =
+// x[16 mb + col][128 (step0 + i) + 32 kq + 8 j .. + 8] for lane (col, kq). In place.
+template <int NS, int MB>
+__device__ __forceinline__ void lines_to_fragments(u32x4 (&v)[NS][MB][4], uint8_t* tile) {
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int kq = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < NS; ++i)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      wait_lgkmcnt0();  // the previous block's reads are done before its tile is overwritten
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        *reinterpret_cast<u32x4*>(tile + (4 * h + kq) * kXTileRow + 16 * col) = v[i][mb][h];
+      wait_lgkmcnt0();
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        v[i][mb][j] = *reinterpret_cast<const u32x4*>(tile + col * kXTileRow + 64 * kq + 16 * j);
+    }
+  wait_lgkmcnt0();
+}
+
+// ---- resident-activation kernel (5..32 tokens, K = 4096, group 128) ----------------------------
+//
+// One workgroup owns TPW consecutive tiles of 16 output features and all of K. Wave w owns the
+// K range of steps 4 w .. 4 w + 3 (512 codes) of every tile: its activations for that range
+// (4 steps x MB token blocks, 32 / 64 VGPRs per block pair) come in once, in whole lines, and
+// stay in registers while the wave streams the codes of the workgroup's tiles, 16 rows x 64
+// bytes per step, through a ring of kKrRing non-temporal loads. Per tile the wave adds its four
+// steps, s * (sum (OFF + q) x - (OFF + z) sum x) per step as in the other decode kernels, and
+// leaves the sums in LDS; after one barrier the workgroup adds the eight waves' sums in wave
+// order, then bias and epilogue. No K split across workgroups, so no partial sums in memory and
+// no second launch. With TPW = 7, gate_up's 1792 tiles fill 256 workgroups, one per CU.
+constexpr int kKrWaves = 8;
+constexpr int kKrSteps = 4;  // 128-code steps per wave: K = 4096
+constexpr int kKrRing = 8;   // code loads in flight per wave
+constexpr int kKrGrid = 256;
+
+template <int TPW, int MB>
+struct KrGeom {
+  static constexpr size_t red_bytes = size_t(TPW) * kKrWaves * MB * 64 * 16;
+  static constexpr size_t xt_bytes = size_t(kKrWaves) * kXTileBytes;
+  static constexpr size_t xs_bytes = size_t(kKrWaves) * kKrSteps * MB * 16 * 4;
+  static constexpr size_t lds_bytes() { return red_bytes + xt_bytes + xs_bytes; }
+};
+
+template <class Act, int TPW, int MB>
+__global__ void __launch_bounds__(kKrWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    decode_kr_kernel(const LinearArgs a) {
+  using Geo = KrGeom<TPW, MB>;
+  using Raw = typename Act::raw;
+  constexpr int NW = kKrWaves;
+  constexpr int SPW = kKrSteps;
+  constexpr int D = kKrRing;
+  constexpr int NIT = TPW * SPW;  // (tile, step) items per wave
+  extern __shared__ u32x4 lds[];
+  uint8_t* const base = reinterpret_cast<uint8_t*>(lds);
+  f32x4* const red = reinterpret_cast<f32x4*>(base);                        // [TPW][NW][MB][64]
+  float* const xsl = reinterpret_cast<float*>(base + Geo::red_bytes + Geo::xt_bytes);  // [NW][SPW][MB][16]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;
+  const int kq = lane >> 4;
+  const bool asym = !a.symmetric;
+  const int64_t tile0 = int64_t(blockIdx.x) * TPW;
+  const int s0 = SPW * w;
+
+  // ---- activations of the wave's K range, then the first codes and metadata ----
+  u32x4 xa[SPW][MB][4];
+  load_x_lines<SPW, MB>(xa, a, s0);
+  __builtin_amdgcn_sched_barrier(0);
+  const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
+  const uint32_t meta_total = uint32_t(a.N * a.G * 4);
+  const auto ms = make_rsrc(a.scales, meta_total);
+  const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_total);
+  // Item i = (tile t, step s): row 16 (tile0 + t) + col, bytes 64 (s0 + s) + 16 kq. Rows past N
+  // repeat row N - 1; their sums are never stored.
+  auto row_of = [&](int t) {
+    const int64_t n = (tile0 + t) * 16 + col;
+    return n < a.N ? n : a.N - 1;
+  };
+  auto code = [&](int i) {
+    return __builtin_amdgcn_raw_buffer_load_b128(
+        wq, int(uint32_t(row_of(i / SPW) * a.ldq) + 64 * (s0 + i % SPW) + 16 * kq), 0, kStreamPolicy);
+  };
+  // Scales and zeros of a tile row for the wave's four groups: one 16-byte load each (G % 4 == 0).
+  auto meta = [&](const __amdgpu_buffer_rsrc_t& r, int t) {
+    return __builtin_bit_cast(f32x4, buf_load16(r, uint32_t((row_of(t) * a.G + s0) * 4), 0));
+  };
+  f32x4 msc[2], mzc[2];
+  msc[0] = meta(ms, 0);
+  mzc[0] = meta(mz, 0);
+  u32x4 ring[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) ring[i] = code(i < NIT ? i : NIT - 1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- activations into MFMA operand order, with their per-step sums ----
+  lines_to_fragments<SPW, MB>(xa, base + Geo::red_bytes + size_t(w) * kXTileBytes);
+  const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  float* const xs_w = xsl + w * (SPW * MB * 16);
+#pragma unroll
+  for (int s = 0; s < SPW; ++s)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      f32x4 sum = zero4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xa[s][mb][j] = arrange<Act, kNibble>(xa[s][mb][j]);
+        sum = Mfma16<Act>::run(xa[s][mb][j], ones, sum);
+      }
+      // Lane (c, kq) holds the sums of tokens 4 kq .. 4 kq + 3.
+      if (col == 0) *reinterpret_cast<f32x4*>(xs_w + (s * MB + mb) * 16 + 4 * kq) = sum;
+    }
+
+  // ---- stream the tiles ----
+  const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
+  const float z_shift = Act::kNibbleOffset;
+  const float z_const = a.zero_const + z_shift;
+  f32x4 tot[MB];
+#pragma unroll
+  for (int i = 0; i < NIT; ++i) {
+    const int t = i / SPW;
+    const int s = i % SPW;
+    if (s == 0) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) tot[mb] = zero4;
+      if (t + 1 < TPW) {
+        msc[(t + 1) & 1] = meta(ms, t + 1);
+        mzc[(t + 1) & 1] = meta(mz, t + 1);
+      }
+    }
+    const u32x4 q = ring[i % D];
+    if (i + D < NIT) ring[i % D] = code(i + D);
+    const float sc = msc[t & 1][s];
+    const float zc = asym ? mzc[t & 1][s] + z_shift : z_const;
+    const u32x4 b[4] = {nib.operand(q.x), nib.operand(q.y), nib.operand(q.z), nib.operand(q.w)};
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      f32x4 acc = Mfma16<Act>::run(xa[s][mb][0], b[0], zero4);
+#pragma unroll
+      for (int j = 1; j < 4; ++j) acc = Mfma16<Act>::run(xa[s][mb][j], b[j], acc);
+      const f32x4 xs = *reinterpret_cast<const f32x4*>(xs_w + (s * MB + mb) * 16 + 4 * kq);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tot[mb][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], acc[r]), tot[mb][r]);
+    }
+    if (s == SPW - 1) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) red[((t * NW + w) * MB + mb) * 64 + lane] = tot[mb];
+    }
+  }
+  __syncthreads();
+
+  // ---- fixed-order sum over the waves (the K ranges); lane (col, kq) of a tile / token block
+  //      holds tokens 16 mb + 4 kq + r of feature 16 tile + col ----
+  const Raw* bias = static_cast<const Raw*>(a.bias);
+  Raw* y = static_cast<Raw*>(a.y);
+  for (int e = tid; e < TPW * MB * 64; e += NW * 64) {
+    const int ln = e & 63;
+    const int mb = (e >> 6) % MB;
+    const int t = (e >> 6) / MB;
+    const int c = ln & 15;
+    const int64_t n = (tile0 + t) * 16 + c;
+    if (n >= a.N) continue;
+    if (a.epilogue == kEpiSwiglu && (c & 4)) continue;  // the gate lane computes the pair
+    f32x4 v = red[((t * NW) * MB + mb) * 64 + ln];
+    f32x4 u = {0.f, 0.f, 0.f, 0.f};
+    if (a.epilogue == kEpiSwiglu) u = red[((t * NW) * MB + mb) * 64 + ln + 4];
+#pragma unroll
+    for (int w2 = 1; w2 < NW; ++w2) {
+      v += red[((t * NW + w2) * MB + mb) * 64 + ln];
+      if (a.epilogue == kEpiSwiglu) u += red[((t * NW + w2) * MB + mb) * 64 + ln + 4];
+    }
+    const float bv = bias ? Act::load(bias[n]) : 0.0f;
+    const float bu = (bias && a.epilogue == kEpiSwiglu) ? Act::load(bias[n + 4]) : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t m = 16 * mb + 4 * (ln >> 4) + r;
+      if (m >= a.M) continue;
+      if (a.epilogue == kEpiSwiglu) {
+        // Gate rows 8p .. 8p+3 and up rows 8p+4 .. 8p+7 (N % 8 == 0).
+        y[m * a.ldy + (n >> 3) * 4 + (n & 3)] = Act::store(swiglu<Act>(v[r] + bv, u[r] + bu));
+      } else {
+        y[m * a.ldy + n] = Act::store(v[r] + bv);
+      }
+    }
+  }
+}
+
 // ---- K-sliced persistent kernel (5..64 tokens, group a multiple of 128) -----------------------
 //
 // For grids of a few hundred tiles of 16 output features (qkv, o, down) a workgroup per tile
@@ -1706,7 +1930,8 @@ struct KsGeom {
   static constexpr int kSlot = kCodeBytes + 512;   // + scales and zeros: 64 floats each
   static constexpr size_t ring_bytes() { return size_t(NW) * R * kSlot; }
   static constexpr size_t red_bytes() { return size_t(2) * NW * MB * 4 * 64 * 4; }
-  static constexpr size_t lds_bytes() { return ring_bytes() + red_bytes(); }
+  static constexpr size_t xt_bytes() { return size_t(NW) * kXTileBytes; }
+  static constexpr size_t lds_bytes() { return ring_bytes() + red_bytes() + xt_bytes(); }
 };
 
 template <class Act, int NW, int R, int MB>
@@ -1732,20 +1957,9 @@ __global__ void __launch_bounds__(NW * 64)
   uint8_t* const ring = base + size_t(wave) * R * Geo::kSlot;
   float* const red = reinterpret_cast<float*>(base + Geo::ring_bytes());
 
-  // ---- the wave's activations: lane (col, kq), step i, token block mb, MFMA j takes
-  //      x[16 mb + col][256 b + 128 i + 32 kq + 8 j .. + 8]; token rows past M read zeros ----
-  const uint32_t xbytes = uint32_t(a.M * a.ldx * 2);
-  const auto xr = make_rsrc(a.x, xbytes);
+  // ---- the wave's activations, in whole lines: steps 2 b and 2 b + 1 of every token block ----
   u32x4 xa[2][MB][4];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int64_t m = 16 * mb + col;
-    const uint32_t row = m < a.M ? uint32_t(m * a.ldx * 2 + (int64_t(blk) * 256 + 32 * kq) * 2) : xbytes;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xa[i][mb][j] = buf_load16(xr, row, uint32_t(128 * i + 8 * j) * 2);
-  }
+  load_x_lines<2, MB>(xa, a, int64_t(blk) * 2);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- direct-to-LDS loads of tile j's block into slot j % R ----
@@ -1781,7 +1995,10 @@ __global__ void __launch_bounds__(NW * 64)
   for (int j = 0; j < R; ++j) issue(j < ntiles ? j : ntiles - 1);
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- activations into operand order, and their per-step sums (one MFMA chain against ones) ----
+  // ---- activations into operand order (lane (col, kq), step i, token block mb, MFMA j takes
+  //      x[16 mb + col][256 b + 128 i + 32 kq + 8 j .. + 8]), and their per-step sums (one MFMA
+  //      chain against ones) ----
+  lines_to_fragments<2, MB>(xa, base + Geo::ring_bytes() + Geo::red_bytes() + size_t(wave) * kXTileBytes);
   const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
   f32x4 xs[2][MB];
@@ -2425,6 +2642,59 @@ bool try_ks(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   return true;
 }
 
+// ---- resident-activation kernel dispatch ----
+
+template <class Act, int TPW, int MB>
+hipError_t launch_kr_cfg(const LinearArgs& a, int grid, hipStream_t stream) {
+  using Geo = KrGeom<TPW, MB>;
+  static_assert(Geo::lds_bytes() <= 160 * 1024, "LDS of one CU");
+  auto kern = decode_kr_kernel<Act, TPW, MB>;
+  const size_t lds = Geo::lds_bytes();
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(kern, dim3(unsigned(grid)), dim3(kKrWaves * 64), lds, stream, a);
+  return hipGetLastError();
+}
+
+template <class Act, int MB>
+hipError_t launch_kr_mb(const LinearArgs& a, int tpw, int grid, hipStream_t stream) {
+  if (tpw == 1) return launch_kr_cfg<Act, 1, MB>(a, grid, stream);
+  if (tpw == 2) return launch_kr_cfg<Act, 2, MB>(a, grid, stream);
+  if (tpw == 4) return launch_kr_cfg<Act, 4, MB>(a, grid, stream);
+  return launch_kr_cfg<Act, 7, MB>(a, grid, stream);
+}
+
+// Tiles per workgroup of the resident-activation kernel: the fewest of {1, 2, 4, 7} that cover
+// the tiles with at most one workgroup per CU; 0 when even 7 do not.
+int kr_tiles_per_wg(int64_t tiles) {
+  for (int t : {1, 2, 4, 7})
+    if (tiles <= int64_t(t) * kKrGrid) return t;
+  return 0;
+}
+
+// 5..32 tokens, K = 4096, 2/4-bit codes, group 128: the resident-activation kernel.
+bool try_kr(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
+  if (a.fmt != kNibble || (a.bits != 2 && a.bits != 4) || a.group != 128 || a.K != 4096 || a.G != 32) return false;
+  if (a.M < 5 || a.M > 32) return false;
+  if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
+  if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
+  if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
+  if (a.M * a.ldx * 2 >= (int64_t(1) << 31)) return false;
+  const int64_t tiles = (a.N + 15) / 16;
+  const int tpw = kr_tiles_per_wg(tiles);
+  if (tpw == 0) return false;
+  const int grid = int((tiles + tpw - 1) / tpw);
+  if (a.M <= 16)
+    *err = a.act == kDtBf16 ? launch_kr_mb<ActBf16, 1>(a, tpw, grid, stream) : launch_kr_mb<ActF16, 1>(a, tpw, grid, stream);
+  else
+    *err = a.act == kDtBf16 ? launch_kr_mb<ActBf16, 2>(a, tpw, grid, stream) : launch_kr_mb<ActF16, 2>(a, tpw, grid, stream);
+  return true;
+}
+
 // M <= 64, 2/4-bit codes, groups of a multiple of 128 codes: the multi-tile kernel.
 bool try_mt(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.fmt != kNibble || a.M < 1 || a.M > 64) return false;
@@ -2513,7 +2783,7 @@ hipError_t launch_linear_decode(const LinearArgs& a, hipStream_t stream, bool* f
   if (a.act != kDtBf16 && a.act != kDtF16) return hipSuccess;
   if (a.M < 1 || a.M > 64) return hipSuccess;
   hipError_t err = hipSuccess;
-  if (try_pline(a, stream, &err) || try_line(a, stream, &err) || try_ks(a, stream, &err) ||
+  if (try_kr(a, stream, &err) || try_pline(a, stream, &err) || try_line(a, stream, &err) || try_ks(a, stream, &err) ||
       try_oneshot(a, stream, &err) || try_mt(a, stream, &err) || try_stream(a, stream, &err)) {
     *fits = true;
     return err;
