@@ -529,6 +529,40 @@ def test_linear_k_sliced_decode(dtype, m, n, k, bits, group, symmetric, with_bia
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [5, 9, 16, 17, 24, 32])
+@pytest.mark.parametrize("n, bits, symmetric, with_bias, strided", [
+    (4100, 4, False, True, True),     # 257 tiles, two per workgroup, the last one partial; x rows strided
+    (4096, 2, True, False, False),    # 2-bit codes, one tile per workgroup
+    (12288, 4, False, False, False),  # 768 tiles: four per workgroup
+    (28672, 4, True, True, False),    # gate_up: seven tiles per workgroup, 256 workgroups
+])
+def test_linear_resident_activation_decode(dtype, m, n, bits, symmetric, with_bias, strided):
+    # 5-32 tokens over K = 4096 with groups of 128: eight waves per workgroup, each holding the
+    # activations of its 512 codes of K, loaded in whole lines and rearranged through LDS.
+    k = 4096
+    qt = _host_qt(n, k, bits, 128, symmetric, seed=m + n)
+    gen = torch.Generator().manual_seed(m)
+    x = torch.randn(m, k + (64 if strided else 0), generator=gen).to(dtype)[:, :k]
+    bias = torch.randn(n, generator=gen).to(dtype) if with_bias else None
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None if bias is None else bias.to(DEV), dtype)
+    assert _rel_err(y, _reference_linear(x, _oracle_dense(qt), bias, dtype)) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("m", [5, 17, 32])
+def test_linear_resident_activation_one_hot_rows(m):
+    # One-hot activation rows through the resident-activation kernel return dequantized weight
+    # columns bit for bit: every other term of each MFMA sum and step correction is exactly zero.
+    qt = _host_qt(4096, 4096, 4, 128, False, seed=m)
+    dense = _oracle_dense(qt)
+    picks = np.random.default_rng(m).choice(4096, size=m, replace=False)
+    x = torch.zeros(m, 4096, dtype=torch.bfloat16)
+    x[torch.arange(m), torch.from_numpy(picks)] = 1.0
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None, torch.bfloat16)
+    expect = qo.bf16_bits(np.ascontiguousarray(dense[:, picks].T)).view(np.int16)
+    np.testing.assert_array_equal(_bits_of(y), expect)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("n, k, symmetric, with_bias", [(16400, 4096, False, True), (28672, 4096, True, False),
                                                         (16384, 2048, False, False), (20480, 6144, False, True)])
