@@ -2572,7 +2572,8 @@ struct KsPlan {
 // Token counts and grids where the kernel leads (measured on MI355X against the multi-tile,
 // one-shot and streaming kernels over the Llama-3-8B projections): long rows (K >= 8192) from 5
 // tokens (down at 8 / 16 / 32 tokens: 21.2 / 22.4 / 25.3 -> 14.1 / 15.2 / 19.8 us), K = 4096
-// from 17 (qkv at 24 / 32: 13.2 / 14.4 -> 12.1 / 13.0 us; o: 11.1 / 12.3 -> 10.8 / 11.7 us);
+// from 17 (qkv at 24 / 32: 13.2 / 14.4 -> 12.1 / 13.0 us; o: 11.1 / 12.3 -> 10.8 / 11.7 us;
+// at 5-32 tokens over K = 4096 the resident-activation kernel, tried first, leads in turn);
 // below those the activations are small enough for the per-tile kernels. Up to 64 tokens (four
 // token blocks). Grids of 1024 tiles or more (gate_up) are faster on the N-split kernel
 // (gate_up at 32 tokens: 24.6 against 28 us). 8 waves, slices of 2048 codes; 16 waves with K =
