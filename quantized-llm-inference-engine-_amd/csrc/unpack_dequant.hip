@@ -121,6 +121,45 @@ __global__ void __launch_bounds__(256) dequant_chunks_kernel(const LinearArgs a,
   }
 }
 
+// Dense 16-bit weight from nibble codes, whole lines both ways: one wave owns 2048 codes of a
+// row (1 KB of codes, 4 KB of output). Lane l takes codes 512 h + 8 l .. + 7 for h < 4: each of
+// the wave's four code loads reads 256 contiguous bytes and each of its four stores writes 1 KB
+// of whole lines, against the chunk kernel's 16-byte pieces of 64 bytes per lane. Scales and
+// zeros: one 4-byte load each per lane and h (16 lanes share a group of 128). Every load is
+// issued before the first conversion. K % 2048 == 0, group % 8 == 0.
+template <class Out>
+__global__ void __launch_bounds__(256) dequant_lines_kernel(const LinearArgs a, void* out) {
+  using Raw = typename Out::raw;
+  static_assert(sizeof(Raw) == 2, "16-bit outputs");
+  const int lane = threadIdx.x & 63;
+  const int64_t chunks = a.K >> 11;
+  const int64_t task = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (task >= a.N * chunks) return;
+  const int64_t n = task / chunks;
+  const int64_t k0 = (task - n * chunks) * 2048 + 8 * lane;
+  const uint8_t* row = a.qw + n * a.ldq;
+  uint32_t w[4];
+  float sc[4], zr[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int64_t k = k0 + 512 * h;
+    w[h] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(row + k / 2));
+    const int64_t g = n * a.G + k / a.group;
+    sc[h] = a.scales[g];
+    zr[h] = a.symmetric ? a.zero_const : a.zeros[g];
+  }
+  Raw* dst = static_cast<Raw*>(out) + n * a.K + k0;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    Raw v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = Out::store(dequant_exact(float((w[h] >> (4 * j)) & 0xFu), zr[h], sc[h]));
+    u32x4 piece;
+    __builtin_memcpy(&piece, v, 16);
+    *reinterpret_cast<u32x4*>(dst + 512 * h) = piece;
+  }
+}
+
 int grid_for(int64_t work, int per_block) {
   int64_t blocks = (work + per_block - 1) / per_block;
   if (blocks > 65536) blocks = 65536;
@@ -164,6 +203,19 @@ hipError_t launch_dequant(const LinearArgs& a, void* out, int out_dtype, hipStre
   const bool chunked = a.K % 8 == 0 && a.group % 8 == 0 && a.ldq % code_align == 0 &&
                        qa % code_align == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
                        (a.K >> 3) <= int64_t(65535) * 256;
+  // Nibble codes into a 16-bit dense weight, rows of whole 2048-code chunks: the line kernel.
+  const bool lines = a.fmt == kNibble && out_dtype != kDtF32 && a.K % 2048 == 0 && a.group % 8 == 0 &&
+                     a.ldq % 4 == 0 && qa % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                     a.N * (a.K >> 11) <= int64_t(0x7FFFFFFF) * 4;
+  if (lines) {
+    const int64_t tasks = a.N * (a.K >> 11);
+    const dim3 grid(unsigned((tasks + 3) / 4));
+    if (out_dtype == kDtBf16)
+      hipLaunchKernelGGL(dequant_lines_kernel<ActBf16>, grid, dim3(256), 0, stream, a, out);
+    else
+      hipLaunchKernelGGL(dequant_lines_kernel<ActF16>, grid, dim3(256), 0, stream, a, out);
+    return hipGetLastError();
+  }
   if (chunked) {
     switch (out_dtype) {
       case kDtF32: launch_dequant_chunks<ActF32>(a, out, stream); break;
