@@ -2676,10 +2676,16 @@ int kr_tiles_per_wg(int64_t tiles) {
   return 0;
 }
 
+// The shapes the resident-activation kernel takes (alignment aside): 5..32 tokens, K = 4096,
+// 2/4-bit codes in groups of 128, at most 7 tiles per workgroup over 256 workgroups.
+bool kr_shape(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
+  if ((bits != 2 && bits != 4) || group != 128 || K != 4096) return false;
+  return M >= 5 && M <= 32 && N >= 1 && kr_tiles_per_wg((N + 15) / 16) > 0;
+}
+
 // 5..32 tokens, K = 4096, 2/4-bit codes, group 128: the resident-activation kernel.
 bool try_kr(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
-  if (a.fmt != kNibble || (a.bits != 2 && a.bits != 4) || a.group != 128 || a.K != 4096 || a.G != 32) return false;
-  if (a.M < 5 || a.M > 32) return false;
+  if (a.fmt != kNibble || a.G != 32 || !kr_shape(a.M, a.N, a.K, a.group, a.bits)) return false;
   if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
@@ -2770,9 +2776,10 @@ bool ks_takes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
 }
 
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
-  // The split of the kernel the decode path tries first: the K-sliced kernel, else the N-split
-  // kernel over K slices.
+  // The split of the kernel the decode path tries first: none for the resident-activation
+  // kernel, else the K-sliced kernel's, else the N-split kernel's over K slices.
   if (bits != 2 && bits != 4) return 0;
+  if (kr_shape(M, N, K, group, bits)) return 0;
   if (ks_takes(M, N, K, group, bits)) return ks_workspace_bytes(M, N, K, group, bits);
   if (group % 128 != 0 || K % 128 != 0 || (K / group) % 4 != 0) return 0;
   const int splits = nx_splits(M, N, K / 128);

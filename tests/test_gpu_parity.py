@@ -252,9 +252,11 @@ def test_linear_n_split_over_k_slices(dtype, m, n, k, group, symmetric):
     assert _rel_err(y, ref) <= TOL[dtype]
     lib = _lib.load_library()
     # The K-sliced kernel takes K a multiple of 2048 from 5 tokens with K >= 8192 and from 17
-    # with shorter rows; the N-split kernel slices K = 9216 from 12 tokens (8 or 4 steps a chunk,
-    # 9 slices give the 32 workgroups of 8 tiles 288 in all).
-    ks = k % 2048 == 0 and m >= (5 if k >= 8192 else 17)
+    # with shorter rows, except the 5-32 tokens over K = 4096 in groups of 128 that the
+    # resident-activation kernel takes unsplit; the N-split kernel slices K = 9216 from 12 tokens
+    # (8 or 4 steps a chunk, 9 slices give the 32 workgroups of 8 tiles 288 in all).
+    kr = k == 4096 and group == 128 and 5 <= m <= 32
+    ks = k % 2048 == 0 and m >= (5 if k >= 8192 else 17) and not kr
     nx = k == 9216 and m >= 12
     assert (lib.llmopt_q_linear_workspace(m, n, k, 4, group) > 0) == (ks or nx)
     y2 = torch.empty(m, n, dtype=dtype, device=DEV)

@@ -5,9 +5,12 @@ fp32 partial sums (``slices * M * N * 4``) of the kernel a call of that size wou
 splits K over workgroups, and 0 when it does not. These tests pin that choice for the
 Llama-3-8B projections without a GPU (no kernel is launched):
 
+* nothing for the resident-activation decode kernel: 5-32 tokens over K = 4096 with groups of
+  128 (qkv, o, gate_up) keep all of K in each workgroup;
 * the K-sliced decode kernel: fewer than 1024 tiles of 16 output features, 2/4-bit codes in
   groups of a multiple of 128, K a multiple of 2048, 5-64 tokens when K >= 8192 and 17-64 on
-  shorter rows; one slice per 2048 codes (down: 7, qkv and o: 2);
+  shorter rows where the resident-activation kernel does not take them; one slice per 2048
+  codes (down: 7, qkv and o at 33-64 tokens: 2);
 * the N-split kernel over K slices, only where the K-sliced kernel does not take the shape
   (K >= 8192 not a multiple of 2048, 12-32 tokens);
 * nothing for gate_up up to 64 tokens (its N-split kernel keeps all of K per workgroup), nor at
@@ -44,12 +47,22 @@ def test_down_takes_seven_k_slices_from_five_tokens(lib, bits, m):
 
 
 @pytest.mark.parametrize("shape", [QKV, O])
-def test_qkv_and_o_take_two_k_slices_from_seventeen_tokens(lib, shape):
+def test_qkv_and_o_take_two_k_slices_from_thirty_three_tokens(lib, shape):
     n = shape[0]
-    for m in range(1, 17):
+    for m in range(1, 33):
         assert _ws(lib, m, shape) == 0, m
-    for m in (17, 24, 31, 32, 33, 48, 64):
+    for m in (33, 48, 64):
         assert _ws(lib, m, shape) == 2 * m * n * 4, m
+
+
+def test_resident_activation_shapes_keep_all_of_k(lib):
+    # K = 4096, groups of 128, 5-32 tokens: no split, whatever the grid (up to 7 tiles per
+    # workgroup over 256 workgroups); K = 4096 with other groups, or 8192, still splits.
+    for n in (16, 4100, 12288, 28672):
+        for m in (5, 17, 32):
+            assert _ws(lib, m, (n, 4096)) == 0, (n, m)
+    assert _ws(lib, 24, (1000, 4096), group=256) == 2 * 24 * 1000 * 4
+    assert _ws(lib, 24, (2048, 8192)) == 4 * 24 * 2048 * 4
 
 
 def test_no_split_at_one_to_four_tokens(lib):
@@ -64,7 +77,8 @@ def test_gate_up_keeps_all_of_k_up_to_64_tokens(lib):
 
 
 def test_slices_follow_k(lib):
-    # One slice per 2048 codes: K = 2048 runs unsplit, 8192 in four slices.
+    # One slice per 2048 codes: K = 2048 runs unsplit, 8192 in four slices (4096 in two, where
+    # the resident-activation kernel does not take the shape).
     assert _ws(lib, 24, (1000, 2048)) == 0
     assert _ws(lib, 24, (2048, 8192)) == 4 * 24 * 2048 * 4
     assert _ws(lib, 24, (2048, 6144), group=384) == 3 * 24 * 2048 * 4
