@@ -126,6 +126,20 @@ def test_dequant_bit_exact(bits, symmetric, rows, cols, group, dtype):
     np.testing.assert_array_equal(_bits_of(got), _expected_bits(_oracle_dense(qt), dtype))
 
 
+@pytest.mark.parametrize("bits,symmetric", [(4, False), (4, True), (2, False), (2, True)])
+@pytest.mark.parametrize("rows,cols,group", [(33, 2048, 128), (7, 6144, 32), (5, 4096, 2048), (3, 2048, 0)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dequant_whole_line_kernel_bit_exact(bits, symmetric, rows, cols, group, dtype):
+    # Nibble codes into 16-bit weights with rows of whole 2048-code chunks: one wave per chunk,
+    # 256-byte code loads and 1 KB stores (odd row counts, groups smaller and larger than a
+    # wave's 512-code stride, a whole-row group).
+    qt = _host_qt(rows, cols, bits, group if group else cols, symmetric, seed=rows + cols + bits)
+    if group == 0:
+        qt = QuantizedTensor(qt.qweight, qt.scales, qt.zeros, qt.bits, 0, qt.symmetric, qt.shape)
+    got = dequantize(_to_device(qt), dtype)
+    np.testing.assert_array_equal(_bits_of(got), _expected_bits(_oracle_dense(qt), dtype))
+
+
 def test_dequant_more_rows_than_one_grid_dimension():
     # 70000 rows exceed the 65535 workgroups of one grid dimension: rows are strided.
     qt = _host_qt(70000, 16, 4, 8, False, seed=11)
