@@ -97,9 +97,10 @@ int llmopt_q_quantize_rtn(const void* weight, int w_dtype, int64_t ldw, int64_t 
 
 /*
  * Bytes of workspace llmopt_q_linear may use for these sizes (0 if none): fp32 partial sums of
- * a K split, splits * M * N * 4 bytes, for the prefill GEMM and for the decode kernel at 12-32
- * tokens on long rows (K >= 8192) over fewer than 1024 tiles of 16 features. With less, those
- * shapes run on the other kernels: correct, slower.
+ * a K split, splits * M * N * 4 bytes, for the prefill GEMM and for the decode kernels that
+ * split K over fewer than 1024 tiles of 16 features (5-64 tokens on rows of K >= 8192, 33-64 on
+ * shorter rows; none at 5-32 tokens over K = 4096 in groups of 128). With less, those shapes run
+ * on the other kernels: correct, slower.
  */
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size);
 
