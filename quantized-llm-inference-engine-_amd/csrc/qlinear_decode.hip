@@ -1693,15 +1693,17 @@ __device__ __forceinline__ void load_x_lines(u32x4 (&raw)[NS][MB][4], const Line
   const uint32_t xbytes = uint32_t(a.M * a.ldx * 2);
   const auto xr = make_rsrc(a.x, xbytes);
   const int lane = threadIdx.x & 63;
+  // Issued step by step, so the first step's pieces land first.
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int i = 0; i < NS; ++i)
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int64_t m = 16 * mb + 4 * h + (lane >> 4);
-      const uint32_t row = m < a.M ? uint32_t((m * a.ldx + step0 * 128) * 2 + 16 * (lane & 15)) : xbytes;
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int i = 0; i < NS; ++i) raw[i][mb][h] = buf_load16(xr, row, uint32_t(i) * 256);
-    }
+      for (int h = 0; h < 4; ++h) {
+        const int64_t m = 16 * mb + 4 * h + (lane >> 4);
+        const uint32_t row = m < a.M ? uint32_t((m * a.ldx + step0 * 128) * 2 + 16 * (lane & 15)) : xbytes;
+        raw[i][mb][h] = buf_load16(xr, row, uint32_t(i) * 256);
+      }
 }
 
 // The same pieces rearranged through the wave's LDS tile into MFMA fragments: frag[i][mb][j] =
@@ -1747,13 +1749,11 @@ template <int TPW, int MB>
 struct KrGeom {
   static constexpr size_t red_bytes = size_t(TPW) * kKrWaves * MB * 64 * 16;
   static constexpr size_t xt_bytes = size_t(kKrWaves) * kXTileBytes;
-  static constexpr size_t xs_bytes = size_t(kKrWaves) * kKrSteps * MB * 16 * 4;
-  static constexpr size_t lds_bytes() { return red_bytes + xt_bytes + xs_bytes; }
+  static constexpr size_t lds_bytes() { return red_bytes + xt_bytes; }
 };
 
 template <class Act, int TPW, int MB>
-__global__ void __launch_bounds__(kKrWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-    decode_kr_kernel(const LinearArgs a) {
+__global__ void __launch_bounds__(kKrWaves * 64) decode_kr_kernel(const LinearArgs a) {
   using Geo = KrGeom<TPW, MB>;
   using Raw = typename Act::raw;
   constexpr int NW = kKrWaves;
@@ -1762,8 +1762,7 @@ __global__ void __launch_bounds__(kKrWaves * 64) __attribute__((amdgpu_waves_per
   constexpr int NIT = TPW * SPW;  // (tile, step) items per wave
   extern __shared__ u32x4 lds[];
   uint8_t* const base = reinterpret_cast<uint8_t*>(lds);
-  f32x4* const red = reinterpret_cast<f32x4*>(base);                        // [TPW][NW][MB][64]
-  float* const xsl = reinterpret_cast<float*>(base + Geo::red_bytes + Geo::xt_bytes);  // [NW][SPW][MB][16]
+  f32x4* const red = reinterpret_cast<f32x4*>(base);  // [TPW][NW][MB][64]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1807,19 +1806,19 @@ __global__ void __launch_bounds__(kKrWaves * 64) __attribute__((amdgpu_waves_per
   lines_to_fragments<SPW, MB>(xa, base + Geo::red_bytes + size_t(w) * kXTileBytes);
   const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  float* const xs_w = xsl + w * (SPW * MB * 16);
+  // xsum[s][mb][r]: sum of the step's activations of token 16 mb + 4 kq + r -- the product with
+  // a matrix of ones puts it in every column, so each lane holds the four it scales.
+  f32x4 xsum[SPW][MB];
 #pragma unroll
   for (int s = 0; s < SPW; ++s)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      f32x4 sum = zero4;
+      xsum[s][mb] = zero4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         xa[s][mb][j] = arrange<Act, kNibble>(xa[s][mb][j]);
-        sum = Mfma16<Act>::run(xa[s][mb][j], ones, sum);
+        xsum[s][mb] = Mfma16<Act>::run(xa[s][mb][j], ones, xsum[s][mb]);
       }
-      // Lane (c, kq) holds the sums of tokens 4 kq .. 4 kq + 3.
-      if (col == 0) *reinterpret_cast<f32x4*>(xs_w + (s * MB + mb) * 16 + 4 * kq) = sum;
     }
 
   // ---- stream the tiles ----
@@ -1849,9 +1848,9 @@ __global__ void __launch_bounds__(kKrWaves * 64) __attribute__((amdgpu_waves_per
       f32x4 acc = Mfma16<Act>::run(xa[s][mb][0], b[0], zero4);
 #pragma unroll
       for (int j = 1; j < 4; ++j) acc = Mfma16<Act>::run(xa[s][mb][j], b[j], acc);
-      const f32x4 xs = *reinterpret_cast<const f32x4*>(xs_w + (s * MB + mb) * 16 + 4 * kq);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) tot[mb][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], acc[r]), tot[mb][r]);
+      for (int r = 0; r < 4; ++r)
+        tot[mb][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xsum[s][mb][r], acc[r]), tot[mb][r]);
     }
     if (s == SPW - 1) {
 #pragma unroll
