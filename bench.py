@@ -101,6 +101,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--e2e-only", action="store_true", help="only the end-to-end generation (for profiling)")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--pmc-workload", action="store_true", help="only the dominant kernel + a copy")
+    p.add_argument("--roofline-only", action="store_true",
+                   help="only the roofline block (graph replays of the dominant kernel), for rocprofv3 --stats")
     p.add_argument("--traffic-from", type=str, default=None, help="rocprofv3 --pmc output dir")
     p.add_argument("--trace-runs", type=str, default=None,
                    help="rocprofv3 --kernel-trace CSV: print this library's kernels per run of dispatches")
@@ -233,6 +235,14 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"pmc_workload": "gate_up decode", "M": args.m, "launches": args.kernel_launches,
                           "copy_bytes": COPY_BYTES, "algorithmic_bytes": algorithmic_bytes(args.m, n, k)}))
+        return 0
+
+    if args.roofline_only:
+        times = kernel_launch_times(torch, launch_gate_up, 3 * len(gate_up_copies))
+        kernel_us = statistics.mean(times)
+        print(json.dumps({"roofline_only": "gate_up decode", "M": args.m, "mean_launch_us": round(kernel_us, 3),
+                          "median_launch_us": round(statistics.median(times), 3),
+                          "GB/s": round(algorithmic_bytes(args.m, n, k) / (kernel_us * 1e-6) / 1e9, 1)}))
         return 0
 
     outs = {p: torch.empty(args.m, pn, dtype=bf16, device="cuda:0") for p, pn, _ in PROJECTIONS}
