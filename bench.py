@@ -191,8 +191,9 @@ def main() -> int:
         return trace_kernels(Path(args.trace_kernels))
     if args.gpus != 1:
         print(
-            "bench.py measures one GPU: the quantized-linear kernels run on one device and this "
-            "build has no multi-GPU path (DESIGN.md describes how the projections would shard). "
+            "bench.py measures one GPU: the quantized-linear kernels run on one device and there "
+            "is no multi-GPU path (tensor parallelism would split qkv / gate_up along N and o / down "
+            "along K on group boundaries, with one all-reduce per row-parallel projection). "
             "Run with --gpus 1.",
             file=sys.stderr,
         )
@@ -375,8 +376,8 @@ def source_digest() -> str:
 
 def _measured_traffic(m: int):
     """HBM bytes per launch of the dominant kernel, from rocprofv3 counters, when they were
-    measured on the kernels of this build; otherwise None and a note naming the build they
-    came from."""
+    measured on the current kernel sources (same digest); otherwise None and a note naming the
+    sources they came from."""
     if not TRAFFIC_FILE.exists() or m != 1:
         return None, "no counter measurement recorded for this workload"
     try:
@@ -384,9 +385,10 @@ def _measured_traffic(m: int):
     except (OSError, ValueError):
         return None, "unreadable counter record"
     if rec.get("build") != source_digest():
-        return None, (f"counters were measured on kernel sources {rec.get('build')}, not on this build "
+        return None, (f"counters were measured on kernel sources {rec.get('build')}, not on the current ones "
                       f"({source_digest()}): {rec.get('hbm_bytes_per_launch')} B per launch then")
-    return rec.get("hbm_bytes_per_launch"), f"rocprofv3 FETCH_SIZE + WRITE_SIZE on this build ({rec.get('build')})"
+    return rec.get("hbm_bytes_per_launch"), (f"rocprofv3 FETCH_SIZE + WRITE_SIZE on the current kernel sources "
+                                              f"({rec.get('build')})")
 
 
 def prefill(torch, ops, rotations):
@@ -442,7 +444,7 @@ def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128, r
 
     diff = rel(res.prefill_logits, ref_res.prefill_logits)
     # The same reference computation in float32 (the dequantized bf16 weights, every activation in
-    # fp32): how far each bf16 computation -- this build's and the reference's -- drifts from it.
+    # fp32): how far each bf16 computation -- the HIP path's and the reference's -- drifts from it.
     ref32 = ref.float()
     exact = GreedyGenerator(ref32, block_size=16, use_graph=False).generate(prompts, 2).prefill_logits
     del ref32, ref
@@ -468,7 +470,7 @@ def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128, r
         "drift_vs_fp32": {
             "how": "prefill last-position logits against the reference computation run in float32 "
                    "(max|a - b| / max|b|)",
-            "this_build_bf16": round(e_hip, 5),
+            "hip_path_bf16": round(e_hip, 5),
             "reference_way_bf16": round(e_ref, 5),
             # The bound the deep-model parity test holds the HIP path to: no more than twice the
             # reference's own bf16 drift.
@@ -479,7 +481,7 @@ def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128, r
           f"{step_ms:.2f} ms/step ({out['decode_tokens_per_s']:.0f} tok/s); the reference's way: decode "
           f"{out['reference_way']['decode_step_ms']:.2f} ms/step, prefill "
           f"{out['reference_way']['prefill_tokens_per_s']:.0f} tok/s", file=sys.stderr, flush=True)
-    print(f"# e2e drift from the fp32 reference: this build {e_hip:.4f}, the reference's bf16 way {e_ref:.4f}",
+    print(f"# e2e drift from the fp32 reference: HIP path {e_hip:.4f}, the reference's bf16 way {e_ref:.4f}",
           file=sys.stderr, flush=True)
     del model, gen, ref_gen, res, ref_res
     torch.cuda.empty_cache()

@@ -57,7 +57,7 @@ class PagedAttentionConfig:
 class AttentionBackend:
     """Backend names (``paged_attention.py:76-110``). ``"auto"`` (and ``"hip"``) select the gfx950
     decode kernel; ``"sdpa"``/``"math"``/``"eager"`` force the torch sequence. flash-attn and
-    Triton are not part of this build: asking for them gives the torch sequence, with a log line,
+    Triton are not part of this package: asking for them gives the torch sequence, with a log line,
     as the reference does when they are missing."""
 
     @classmethod
