@@ -427,19 +427,36 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1
 
   if (EPI == kEpiSwiglu) {
     // Each wave owns 64 fused rows = 8 gate/up blocks = 32 output features of 32 * TT tokens.
-    // Lanes take consecutive output features of one token, so stores are 64-byte runs.
+    // A lane takes one block: output features 4q .. 4q + 3 of one token, whose gate and up
+    // values are two 8-byte runs of the tile row (fused rows 8q .. 8q + 3 and 8q + 4 .. 8q + 7),
+    // and stores the four results at once; eight lanes cover a token's 64-byte run.
     const Raw* tile = reinterpret_cast<const Raw*>(xbuf(wave));
     const int64_t out0 = (n0 + 64 * wave) / 2;
-    for (int e = lane; e < 32 * TT * 32; e += 64) {
-      const int t = e >> 5;
-      const int o = e & 31;
+    for (int e = lane; e < 32 * TT * 8; e += 64) {
+      const int t = e >> 3;
+      const int q = e & 7;
       const int64_t m = m0 + t;
-      const int64_t f = out0 + o;
+      const int64_t f = out0 + 4 * q;
+      // N % 8 == 0: a block is either wholly inside the output or wholly past it.
       if (m >= a.M || 2 * f >= a.N) continue;
-      const int g = (o >> 2) * 8 + (o & 3);
-      const float gv = Act::load(tile[t * 64 + g]);
-      const float uv = Act::load(tile[t * 64 + g + 4]);
-      y[m * a.ldy + f] = Act::store(swiglu<Act>(gv, uv));
+      const u32x2 gw = *reinterpret_cast<const u32x2*>(tile + t * 64 + 8 * q);
+      const u32x2 uw = *reinterpret_cast<const u32x2*>(tile + t * 64 + 8 * q + 4);
+      const uint32_t gs[4] = {gw.x & 0xFFFFu, gw.x >> 16, gw.y & 0xFFFFu, gw.y >> 16};
+      const uint32_t us[4] = {uw.x & 0xFFFFu, uw.x >> 16, uw.y & 0xFFFFu, uw.y >> 16};
+      Raw out[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        out[r] = Act::store(swiglu<Act>(Act::load(Raw(gs[r])), Act::load(Raw(us[r]))));
+      Raw* dst = y + m * a.ldy + f;
+      if (vec) {
+        u32x2 pk;
+        pk.x = uint32_t(out[0]) | (uint32_t(out[1]) << 16);
+        pk.y = uint32_t(out[2]) | (uint32_t(out[3]) << 16);
+        *reinterpret_cast<u32x2*>(dst) = pk;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[r] = out[r];
+      }
     }
   }
 }
