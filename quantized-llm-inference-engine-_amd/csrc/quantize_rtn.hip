@@ -181,10 +181,12 @@ __device__ __forceinline__ void fold_nan(const float* v, float& lo, float& hi) {
   }
 }
 
-// Groups of T = 2^team_log2 chunks: a team of T lanes per (row, group), one chunk per lane, and
-// each lane serves U teams -- rows r, r + R, ..., r + (U - 1) R of the same group, R = ceil(N / U)
-// -- whose loads are all issued before any is used, so a wave keeps U kilobytes in flight.
-template <class In, int BITS, bool SYM, int U>
+// Groups of T * CPL chunks, T = 2^team_log2: a team of T lanes per (row, group), CPL adjacent
+// chunks per lane, and each lane serves U teams -- rows r, r + R, ..., r + (U - 1) R of the same
+// group, R = ceil(N / U) -- whose loads are all issued before any is used, so a wave keeps
+// U * CPL kilobytes in flight. Two chunks per lane halve the per-weight share of the group's
+// scale and zero point (three divisions per lane) and of the team's shuffles.
+template <class In, int BITS, bool SYM, int U, int CPL>
 __global__ void __launch_bounds__(256) rtn_team_kernel(const RtnArgs a, int team_log2, int64_t rows_per_unit) {
   using Raw = typename In::raw;
   const int T = 1 << team_log2;
@@ -195,16 +197,17 @@ __global__ void __launch_bounds__(256) rtn_team_kernel(const RtnArgs a, int team
   // in the shuffles.
   const int64_t row0 = team0 / a.G;
   const int64_t grp = team0 - row0 * a.G;
-  const int64_t col = grp * a.group + int64_t(tl) * 8;
+  const int64_t col = grp * a.group + int64_t(tl) * (8 * CPL);
   const float inf = __int_as_float(0x7F800000);
 
-  float v[U][8];
+  float v[U][8 * CPL];
   int64_t row[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     row[u] = row0 + u * rows_per_unit;
     const int64_t r = row[u] < a.N ? row[u] : 0;
-    load_chunk<In>(static_cast<const Raw*>(a.w) + r * a.ldw + col, v[u]);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) load_chunk<In>(static_cast<const Raw*>(a.w) + r * a.ldw + col + 8 * c, v[u] + 8 * c);
   }
   // The U reductions run side by side (one basic block); only a team with a NaN or an
   // infinity takes the slow path.
@@ -214,7 +217,8 @@ __global__ void __launch_bounds__(256) rtn_team_kernel(const RtnArgs a, int team
     lo[u] = inf;
     hi[u] = -inf;
     flag[u] = 0.0f;
-    fold(v[u], lo[u], hi[u], flag[u]);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) fold(v[u] + 8 * c, lo[u], hi[u], flag[u]);
   }
   for (int off = T >> 1; off > 0; off >>= 1) {
 #pragma unroll
@@ -233,7 +237,8 @@ __global__ void __launch_bounds__(256) rtn_team_kernel(const RtnArgs a, int team
       if (flag[u] != flag[u]) {
         lo[u] = inf;
         hi[u] = -inf;
-        fold_nan(v[u], lo[u], hi[u]);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) fold_nan(v[u] + 8 * c, lo[u], hi[u]);
       }
       team_reduce_nan(lo[u], hi[u], T);  // every lane joins the shuffles; clean teams are unchanged
     }
@@ -246,7 +251,8 @@ __global__ void __launch_bounds__(256) rtn_team_kernel(const RtnArgs a, int team
         a.scales[row[u] * a.G + grp] = g.s;
         a.zeros[row[u] * a.G + grp] = g.z;
       }
-      store_chunk<BITS, SYM>(a.q + row[u] * a.ldq, col, v[u], g);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) store_chunk<BITS, SYM>(a.q + row[u] * a.ldq, col + 8 * c, v[u] + 8 * c, g);
     }
   }
 }
@@ -336,9 +342,12 @@ hipError_t launch_in(const RtnArgs& a, hipStream_t stream) {
   const bool nibble = a.bits < 8;
   const bool out_aligned = nibble ? (a.ldq % 4 == 0 && reinterpret_cast<uintptr_t>(a.q) % 4 == 0)
                                   : (a.ldq % 8 == 0 && reinterpret_cast<uintptr_t>(a.q) % 8 == 0);
-  int team_log2 = -1, per_lane = 1;
+  int team_log2 = -1, per_lane = 1, cpl = 1;
   if (chunked && out_aligned) {
-    if (chunks <= 64 && (chunks & (chunks - 1)) == 0) {
+    if (chunks <= 128 && chunks >= 2 && (chunks & (chunks - 1)) == 0) {
+      cpl = 2;
+      team_log2 = __builtin_ctzll(uint64_t(chunks / 2));
+    } else if (chunks <= 64 && (chunks & (chunks - 1)) == 0) {
       team_log2 = __builtin_ctzll(uint64_t(chunks));
     } else if (chunks % 64 == 0) {
       team_log2 = 6;
@@ -357,8 +366,11 @@ hipError_t launch_in(const RtnArgs& a, hipStream_t stream) {
   const dim3 wave_grid(unsigned((teams * 64 + 255) / 256));
 #define LLMOPT_RTN(B, S)                                                                           \
   if (a.bits == B && sym == S) {                                                                \
-    if (per_lane == 1)                                                                          \
-      hipLaunchKernelGGL((rtn_team_kernel<In, B, S, kUnits>), team_grid, dim3(256), 0, stream, a, \
+    if (per_lane == 1 && cpl == 2)                                                              \
+      hipLaunchKernelGGL((rtn_team_kernel<In, B, S, kUnits, 2>), team_grid, dim3(256), 0, stream, a, \
+                         team_log2, rows_per_unit);                                             \
+    else if (per_lane == 1)                                                                     \
+      hipLaunchKernelGGL((rtn_team_kernel<In, B, S, kUnits, 1>), team_grid, dim3(256), 0, stream, a, \
                          team_log2, rows_per_unit);                                             \
     else                                                                                        \
       hipLaunchKernelGGL((rtn_wave_kernel<In, B, S>), wave_grid, dim3(256), 0, stream, a,        \
