@@ -360,7 +360,7 @@ hipError_t launch_in(const RtnArgs& a, hipStream_t stream) {
     return hipGetLastError();
   }
   const bool sym = a.symmetric != 0;
-  constexpr int kUnits = 4;
+  constexpr int kUnits = 2;  // rows per lane: with two chunks per lane, 4 KB in flight per wave
   const int64_t rows_per_unit = (a.N + kUnits - 1) / kUnits;
   const dim3 team_grid(unsigned((((rows_per_unit * a.G) << team_log2) + 255) / 256));
   const dim3 wave_grid(unsigned((teams * 64 + 255) / 256));
