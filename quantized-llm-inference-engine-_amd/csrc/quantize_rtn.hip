@@ -19,7 +19,7 @@
 // of the group (one 16-byte load for 2-byte weights, two for fp32), the team reduces min/max
 // with lane shuffles, and every lane writes its chunk's codes (4 bytes of nibbles or 8 bytes)
 // -- one coalesced pass that reads the weight once and writes codes, scales and zeros once.
-// Groups that are not a power-of-two number of chunks up to 64 (or a multiple of 64 chunks)
+// Groups that are not a power-of-two number of chunks up to 256 (or a multiple of 64 chunks)
 // and unaligned tensors take a one-thread-per-group kernel with the same arithmetic.
 #include "qcommon.hpp"
 #include "qkernels.hpp"
@@ -27,13 +27,15 @@
 namespace llmopt {
 namespace {
 
-// torch.amin / amax propagate NaN; IEEE min/max (v_min_f32) would drop it.
-__device__ __forceinline__ float nan_min(float a, float b) { return (b < a || b != b) ? b : a; }
-__device__ __forceinline__ float nan_max(float a, float b) { return (b > a || b != b) ? b : a; }
+// torch.amin / amax propagate NaN, and so do IEEE 754-2019 minimum / maximum, which gfx950
+// executes as v_minimum3_f32 / v_maximum3_f32 (two new weights per instruction). Their choice
+// between -0 and +0 does not reach the results: both grids clamp or take |.| of lo and hi first.
+__device__ __forceinline__ float nan_min(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float nan_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 struct Grid {
   float s, z;
-  float r;  // RN(1 / s), for the quotient shortcut in code_of
+  float r;  // RN(1 / s), for the quotients in rint_quotients
 };
 
 // choose_qparams for one group (quantizers.py:100-142).
@@ -54,25 +56,26 @@ __device__ __forceinline__ Grid group_grid(float lo, float hi, int bits, bool sy
   return {s, z, __fdiv_rn(1.0f, s)};
 }
 
-// rne(RN(w / s)) for the eight weights of a chunk, without a full division in the common case.
-// a = RN(w * RN(1/s)) is within |w/s| * 2^-21 of RN(w / s) (two roundings of 2^-24 each, and
-// RN(w / s) within 2^-24 of w / s). The two round to the same integer unless a half-integer
-// lies between them, so a result is taken from `a` only when a is farther than |a| * 2^-20
-// from every half-integer. Otherwise (about one weight in 30000) the correctly rounded
-// division decides; the test is made wave-wide so that the divisions stay behind a branch
-// that almost every wave skips.
+// rne(RN(w / s)) for the eight weights of a chunk without a division: Markstein's correction.
+// With r = RN(1/s) and q0 = RN(w r), one fma gives the remainder e = RN(w - s q0) and a second
+// q1 = RN(q0 + e r), which is RN(w / s) (Markstein, "Computation of elementary functions on the
+// IBM RISC System/6000 processor", IBM J. Res. Dev. 34(1), 1990; Muller et al., Handbook of
+// Floating-Point Arithmetic, ch. 4). rne(q1) can only differ from rne(w / s) when w / s lies
+// within an ulp of a half-integer; tests/test_quotient_exactness.py checks every fp32 s in
+// [1, 2), every half-integer below 256 and the w within 4 ulps of s times it (all agree), and
+// the steps scale exactly with s and w for 1e-8 <= s <= 2^120. Larger or non-finite scales
+// (r near the subnormal range, or 0) take the correctly rounded division, behind a branch that
+// is wave-uniform in practice.
 __device__ __forceinline__ void rint_quotients(const float* v, const Grid& g, float* ratio) {
-  bool exact = false;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const float a = __fmul_rn(v[j], g.r);
-    const float h = __builtin_rintf(a);
-    const float gap = __fsub_rn(0.5f, fabsf(__fsub_rn(a, h)));  // distance to the nearest half-integer
-    ratio[j] = h;
-    exact |= !(gap > __fmul_rn(fabsf(a), 0x1p-20f));
+    const float q0 = __fmul_rn(v[j], g.r);
+    const float e = __builtin_fmaf(-g.s, q0, v[j]);
+    ratio[j] = __builtin_rintf(__builtin_fmaf(e, g.r, q0));
   }
-  if (__builtin_amdgcn_ballot_w64(exact) != 0) {
-    if (exact) {
+  const bool divide = !(g.s <= 0x1p120f);
+  if (__builtin_amdgcn_ballot_w64(divide) != 0) {
+    if (divide) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) ratio[j] = __builtin_rintf(__fdiv_rn(v[j], g.s));
     }
@@ -144,36 +147,16 @@ __device__ __forceinline__ void store_chunk(uint8_t* qrow, int64_t col, const fl
   }
 }
 
-// min/max of a team's weights (lane values lo, hi already folded over the lane's own weights)
-// with IEEE fminf/fmaxf, which v_min3/v_max3 do two weights at a time, plus a flag that turns
-// NaN when any weight is NaN or infinite (w * 0 + flag). Every lane of the team ends with the
-// team's values.
-__device__ __forceinline__ void team_reduce(float& lo, float& hi, float& flag, int T) {
-  for (int off = T >> 1; off > 0; off >>= 1) {
-    lo = fminf(lo, __shfl_xor(lo, off, 64));
-    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
-    flag += __shfl_xor(flag, off, 64);
-  }
-}
-
-// The same with NaN propagation (torch.amin / amax); used only by teams whose flag is NaN.
-__device__ __forceinline__ void team_reduce_nan(float& lo, float& hi, int T) {
+// min/max of a team's weights (lane values lo, hi already folded over the lane's own weights),
+// NaN-propagating; every lane of the team ends with the team's values.
+__device__ __forceinline__ void team_reduce(float& lo, float& hi, int T) {
   for (int off = T >> 1; off > 0; off >>= 1) {
     lo = nan_min(lo, __shfl_xor(lo, off, 64));
     hi = nan_max(hi, __shfl_xor(hi, off, 64));
   }
 }
 
-__device__ __forceinline__ void fold(const float* v, float& lo, float& hi, float& flag) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    lo = fminf(lo, v[j]);
-    hi = fmaxf(hi, v[j]);
-    flag = __builtin_fmaf(v[j], 0.0f, flag);
-  }
-}
-
-__device__ __forceinline__ void fold_nan(const float* v, float& lo, float& hi) {
+__device__ __forceinline__ void fold(const float* v, float& lo, float& hi) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     lo = nan_min(lo, v[j]);
@@ -184,8 +167,9 @@ __device__ __forceinline__ void fold_nan(const float* v, float& lo, float& hi) {
 // Groups of T * CPL chunks, T = 2^team_log2: a team of T lanes per (row, group), CPL adjacent
 // chunks per lane, and each lane serves U teams -- rows r, r + R, ..., r + (U - 1) R of the same
 // group, R = ceil(N / U) -- whose loads are all issued before any is used, so a wave keeps
-// U * CPL kilobytes in flight. Two chunks per lane halve the per-weight share of the group's
-// scale and zero point (three divisions per lane) and of the team's shuffles.
+// U * CPL kilobytes in flight. Four adjacent chunks per lane (64 bytes of 2-byte weights) cut
+// the per-weight share of the group's scale and zero point (three divisions per lane) and of
+// the team's shuffles; with eight, a lane's loads no longer coalesce with its neighbours'.
 template <class In, int BITS, bool SYM, int U, int CPL>
 __global__ void __launch_bounds__(256) rtn_team_kernel(const RtnArgs a, int team_log2, int64_t rows_per_unit) {
   using Raw = typename In::raw;
@@ -209,38 +193,20 @@ __global__ void __launch_bounds__(256) rtn_team_kernel(const RtnArgs a, int team
 #pragma unroll
     for (int c = 0; c < CPL; ++c) load_chunk<In>(static_cast<const Raw*>(a.w) + r * a.ldw + col + 8 * c, v[u] + 8 * c);
   }
-  // The U reductions run side by side (one basic block); only a team with a NaN or an
-  // infinity takes the slow path.
-  float lo[U], hi[U], flag[U];
+  // The U reductions run side by side (one basic block).
+  float lo[U], hi[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     lo[u] = inf;
     hi[u] = -inf;
-    flag[u] = 0.0f;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) fold(v[u] + 8 * c, lo[u], hi[u], flag[u]);
+    for (int c = 0; c < CPL; ++c) fold(v[u] + 8 * c, lo[u], hi[u]);
   }
   for (int off = T >> 1; off > 0; off >>= 1) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      lo[u] = fminf(lo[u], __shfl_xor(lo[u], off, 64));
-      hi[u] = fmaxf(hi[u], __shfl_xor(hi[u], off, 64));
-      flag[u] += __shfl_xor(flag[u], off, 64);
-    }
-  }
-  bool flagged = false;
-#pragma unroll
-  for (int u = 0; u < U; ++u) flagged |= flag[u] != flag[u];
-  if (flagged) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (flag[u] != flag[u]) {
-        lo[u] = inf;
-        hi[u] = -inf;
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) fold_nan(v[u] + 8 * c, lo[u], hi[u]);
-      }
-      team_reduce_nan(lo[u], hi[u], T);  // every lane joins the shuffles; clean teams are unchanged
+      lo[u] = nan_min(lo[u], __shfl_xor(lo[u], off, 64));
+      hi[u] = nan_max(hi[u], __shfl_xor(hi[u], off, 64));
     }
   }
 #pragma unroll
@@ -273,21 +239,12 @@ __global__ void __launch_bounds__(256) rtn_wave_kernel(const RtnArgs a, int per_
   const Raw* wg = static_cast<const Raw*>(a.w) + row * a.ldw + grp * a.group;
   const float inf = __int_as_float(0x7F800000);
   float v[8];
-  float lo = inf, hi = -inf, flag = 0.0f;
+  float lo = inf, hi = -inf;
   for (int p = 0; p < per_lane; ++p) {
     load_chunk<In>(wg + int64_t(tl + p * 64) * 8, v);
-    fold(v, lo, hi, flag);
+    fold(v, lo, hi);
   }
-  team_reduce(lo, hi, flag, 64);
-  if (flag != flag) {
-    lo = inf;
-    hi = -inf;
-    for (int p = 0; p < per_lane; ++p) {
-      load_chunk<In>(wg + int64_t(tl + p * 64) * 8, v);
-      fold_nan(v, lo, hi);
-    }
-    team_reduce_nan(lo, hi, 64);
-  }
+  team_reduce(lo, hi, 64);
   const Grid g = group_grid(lo, hi, BITS, SYM);
   if (!live) return;
   if (tl == 0) {
@@ -344,9 +301,12 @@ hipError_t launch_in(const RtnArgs& a, hipStream_t stream) {
                                   : (a.ldq % 8 == 0 && reinterpret_cast<uintptr_t>(a.q) % 8 == 0);
   int team_log2 = -1, per_lane = 1, cpl = 1;
   if (chunked && out_aligned) {
-    if (chunks <= 128 && chunks >= 2 && (chunks & (chunks - 1)) == 0) {
+    if (chunks <= 256 && chunks >= 4 && (chunks & (chunks - 1)) == 0) {
+      cpl = 4;
+      team_log2 = __builtin_ctzll(uint64_t(chunks / 4));
+    } else if (chunks == 2) {
       cpl = 2;
-      team_log2 = __builtin_ctzll(uint64_t(chunks / 2));
+      team_log2 = 0;
     } else if (chunks <= 64 && (chunks & (chunks - 1)) == 0) {
       team_log2 = __builtin_ctzll(uint64_t(chunks));
     } else if (chunks % 64 == 0) {
@@ -360,13 +320,19 @@ hipError_t launch_in(const RtnArgs& a, hipStream_t stream) {
     return hipGetLastError();
   }
   const bool sym = a.symmetric != 0;
-  constexpr int kUnits = 2;  // rows per lane: with two chunks per lane, 4 KB in flight per wave
+  // One row per lane: measured on MI355X (gate_up, bf16 -> W4 g128), one row of four chunks
+  // per lane 56 us, two rows of two chunks 61 us, one row of two 57 us, eight chunks (each
+  // lane a whole line, uncoalesced across the wave) 77 us.
+  constexpr int kUnits = 1;
   const int64_t rows_per_unit = (a.N + kUnits - 1) / kUnits;
   const dim3 team_grid(unsigned((((rows_per_unit * a.G) << team_log2) + 255) / 256));
   const dim3 wave_grid(unsigned((teams * 64 + 255) / 256));
 #define LLMOPT_RTN(B, S)                                                                           \
   if (a.bits == B && sym == S) {                                                                \
-    if (per_lane == 1 && cpl == 2)                                                              \
+    if (per_lane == 1 && cpl == 4)                                                              \
+      hipLaunchKernelGGL((rtn_team_kernel<In, B, S, kUnits, 4>), team_grid, dim3(256), 0, stream, a, \
+                         team_log2, rows_per_unit);                                             \
+    else if (per_lane == 1 && cpl == 2)                                                         \
       hipLaunchKernelGGL((rtn_team_kernel<In, B, S, kUnits, 2>), team_grid, dim3(256), 0, stream, a, \
                          team_log2, rows_per_unit);                                             \
     else if (per_lane == 1)                                                                     \
