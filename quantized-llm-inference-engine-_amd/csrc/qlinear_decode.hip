@@ -667,7 +667,8 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
 #pragma unroll
       for (int r = 0; r < 4; ++r) xs[r] = v[r];
     } else {
-      xs[0] = xsum[i * 16 + 4 * kq];
+#pragma unroll
+      for (int r = 0; r < RM; ++r) xs[r] = xsum[i * 16 + 4 * kq + r];
     }
     const float s = srow[i * sstride];
     const float zc = asym ? zrow[i * sstride] + z_shift : z_const;
@@ -2226,6 +2227,12 @@ hipError_t launch_oneshot(const LinearArgs& a, int c, int nw, hipStream_t stream
     if (c == 16) return launch_oneshot_cfg<Act, 16, 1, 1>(a, nw, stream);
     if (c == 8) return launch_oneshot_cfg<Act, 8, 1, 1>(a, nw, stream);
     return launch_oneshot_cfg<Act, 4, 1, 1>(a, nw, stream);
+  }
+  // Two tokens: half the activation loads and accumulator rows of the four-token form; measured
+  // on MI355X, qkv 7.09 -> 6.75 us, o 5.49 -> 5.34, down 12.67 -> 11.65, gate_up level.
+  if (a.M == 2) {
+    if (c == 8) return launch_oneshot_cfg<Act, 8, 2, 2>(a, nw, stream);
+    return launch_oneshot_cfg<Act, 4, 2, 2>(a, nw, stream);
   }
   if (c == 8) return launch_oneshot_cfg<Act, 8, 4, 4>(a, nw, stream);
   return launch_oneshot_cfg<Act, 4, 4, 4>(a, nw, stream);
