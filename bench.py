@@ -737,8 +737,8 @@ def _cpu_model() -> str:
 
 
 def cpu_baseline(torch, base, m: int, seconds: float, gptq=None):
-    """The reference's host sequence on this machine's cores (`oracle.cpu_reference`, the
-    build's restatement of QuantLinear.forward: dequantize once, cache, F.linear), on a bounded
+    """The reference's host sequence on this machine's cores (`oracle.cpu_reference`, a
+    restatement of QuantLinear.forward: dequantize once, cache, F.linear), on a bounded
     sample. `value`: the decode step (4 projections, M = `m`, bf16, dense weight cached) for
     `seconds`. `configs`: the reference's CPU configurations, warm (cached weight, median of a
     few calls) and cold (dequantize + F.linear, once per weight; M does not change its cost)."""
