@@ -75,6 +75,27 @@ def test_rtn_special_groups(bits, symmetric):
     _check(got, weight, bits, g, symmetric)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("bits,symmetric", [(2, False), (2, True), (4, False), (4, True), (8, False), (8, True)])
+def test_rtn_scales_near_the_fp32_limit(dtype, bits, symmetric):
+    # The kernel's division-free quotient holds for scales up to 2^120; larger scales, and
+    # those that overflow to infinity (max - min past the fp32 range), divide instead. Rows
+    # on both sides of that bound, next to an ordinary row, stay bit-exact with the oracle.
+    g = 32
+    rows = [
+        np.linspace(-1e37, 3e37, g),  # s above 2^120 at 2 and 4 bits, below at 8
+        np.linspace(-3e38, 3e38, g),  # max - min overflows: s = inf
+        np.linspace(1e36, 2e38, g),  # all positive, large
+        np.r_[np.zeros(g - 1), 3.3e38],  # one outlier near the top of the range
+        np.linspace(-2e38, -1e35, g),  # all negative
+        np.arange(g) * 0.5 - 7.5,  # ordinary magnitudes in the same launch
+    ]
+    weight = torch.tensor(np.stack(rows), dtype=torch.float32).to(dtype)
+    got = RoundToNearestQuantizer(bits, g, symmetric).quantize(weight.to(DEV))
+    with np.errstate(over="ignore"):  # the oracle's max - min overflows on purpose
+        _check(got, weight, bits, g, symmetric)
+
+
 def test_rtn_full_size_gate_up_bf16():
     gen = torch.Generator(device=DEV).manual_seed(0)
     weight = (torch.randn(28672, 4096, generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
