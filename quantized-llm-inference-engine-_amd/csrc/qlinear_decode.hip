@@ -539,7 +539,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4,
 //   tensors) are loaded once per workgroup with coalesced 16-byte lane loads into LDS; loading
 //   each wave's groups separately costs about as much time again as all the codes' latency.
 // * The activation slice goes through a wave-private LDS region, permuted into the MFMA operand
-//   order, with per-step sums for the zero-point term.
+//   order; the per-step sums for the zero-point term are staged with it for one token and come
+//   from MFMAs against ones for two to four.
 // * One barrier makes the staged data visible; the final cross-wave reduction needs two more.
 template <int C, int MMAX>
 struct OneShotGeom {
@@ -625,24 +626,33 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
     *reinterpret_cast<u32x4*>(z_lds + row * mstride + g) = zv;
   }
   if (lane < NM) zero4[lane] = u32x4{0u, 0u, 0u, 0u};
+  // Per-step activation sums: staged here for one token; from two tokens on, the staging work
+  // grows with the rows while one MFMA against a ones operand per fragment gives every lane its
+  // rows' sums in the compute loop (measured on MI355X at three and four tokens: qkv 7.2 ->
+  // 6.5-6.7 us, o 5.5 -> 5.2; at one token the staged sums stay 0.5-1 % ahead).
+  constexpr bool kMfmaSums = MMAX >= 2;
+  if constexpr (!kMfmaSums) {
 #pragma unroll
-  for (int i = lane; i < C * 16; i += 64)
-    if ((i & 15) >= M) xsum[i] = 0.0f;
+    for (int i = lane; i < C * 16; i += 64)
+      if ((i & 15) >= M) xsum[i] = 0.0f;
+  }
 #pragma unroll
   for (int e = 0; e < Geo::kXPerLane; ++e) {
     const int idx = lane + 64 * e;
     const int m = idx / (C * 16);
     const int c = idx - m * (C * 16);
-    const uint32_t w4[4] = {xv[e].x, xv[e].y, xv[e].z, xv[e].w};
     float sum = 0.0f;
+    if constexpr (!kMfmaSums) {
+      const uint32_t w4[4] = {xv[e].x, xv[e].y, xv[e].z, xv[e].w};
 #pragma unroll
-    for (int h = 0; h < 4; ++h) sum += Act::load(Raw(w4[h] & 0xFFFFu)) + Act::load(Raw(w4[h] >> 16));
-    // The 16 pieces of one step sit in 16 consecutive lanes.
+      for (int h = 0; h < 4; ++h) sum += Act::load(Raw(w4[h] & 0xFFFFu)) + Act::load(Raw(w4[h] >> 16));
+      // The 16 pieces of one step sit in 16 consecutive lanes.
 #pragma unroll
-    for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+      for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+    }
     if (idx < M * C * 16) {
       xw[m * Geo::kRowPieces + c] = arrange<Act, kNibble>(xv[e]);
-      if ((c & 15) == 0) xsum[(c >> 4) * 16 + m] = sum;
+      if (!kMfmaSums && (c & 15) == 0) xsum[(c >> 4) * 16 + m] = sum;
     }
   }
   __syncthreads();
@@ -662,7 +672,14 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
 #pragma unroll
     for (int j = 0; j < NM; ++j) xa[j] = xrow[i * xstep + j];
     float xs[RM];
-    if constexpr (RM == 4) {
+    if constexpr (kMfmaSums) {
+      const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NM; ++j) v = Mfma16<Act>::run(xa[j], ones, v);
+#pragma unroll
+      for (int r = 0; r < RM; ++r) xs[r] = v[r];
+    } else if constexpr (RM == 4) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(xsum + i * 16 + 4 * kq);
 #pragma unroll
       for (int r = 0; r < 4; ++r) xs[r] = v[r];
