@@ -701,7 +701,7 @@ def shapes(torch, ops, rotations):
     projection's weight copies; per-launch medians of graph replays of back-to-back launches."""
     bf16 = torch.bfloat16
     rows = []
-    for m in (1, 8, 32, 64, 256, 2048, 8192):
+    for m in (1, 2, 4, 8, 32, 64, 256, 2048, 8192):
         for name, n, k in PROJECTIONS:
             qts = rotations[name]
             x = torch.randn(m, k, device="cuda:0").to(bf16)
