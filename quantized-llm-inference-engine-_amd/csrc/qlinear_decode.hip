@@ -528,7 +528,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4,
   }
 }
 
-// ---- one-shot kernel (M <= 4, nibble codes, group 128) ------------------------------------------
+// ---- one-shot kernel (M <= 8, nibble codes, group 128) ------------------------------------------
 //
 // One workgroup owns one tile of 16 output features; its waves split K into contiguous chunks of
 // C steps (C*128 codes per row), one chunk per wave. A wave issues every load it needs up front
@@ -2245,6 +2245,7 @@ hipError_t launch_oneshot(const LinearArgs& a, int c, int nw, hipStream_t stream
     if (c == 8) return launch_oneshot_cfg<Act, 8, 1, 1>(a, nw, stream);
     return launch_oneshot_cfg<Act, 4, 1, 1>(a, nw, stream);
   }
+  if (a.M > 4) return launch_oneshot_cfg<Act, 4, 8, 4>(a, nw, stream);
   // Two tokens: half the activation loads and accumulator rows of the four-token form; measured
   // on MI355X, qkv 7.09 -> 6.75 us, o 5.49 -> 5.34, down 12.67 -> 11.65, gate_up level.
   if (a.M == 2) {
@@ -2255,9 +2256,9 @@ hipError_t launch_oneshot(const LinearArgs& a, int c, int nw, hipStream_t stream
   return launch_oneshot_cfg<Act, 4, 4, 4>(a, nw, stream);
 }
 
-// M <= 4, 2/4-bit codes, group 128: the one-shot kernel.
+// M <= 8, 2/4-bit codes, group 128: the one-shot kernel (5-8 tokens in 4-step chunks only).
 bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
-  if (a.fmt != kNibble || a.M > 4 || a.group != 128 || a.K % 128 != 0 || a.G % 4 != 0) return false;
+  if (a.fmt != kNibble || a.M > 8 || a.group != 128 || a.K % 128 != 0 || a.G % 4 != 0) return false;
   if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
@@ -2271,6 +2272,7 @@ bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   int chosen = 0;
   for (int c : {4, 8, 16}) {
     if (c == 16 && a.M > 1) continue;
+    if (a.M > 4 && c != 4) continue;  // eight-row slices of longer chunks overflow the LDS
     if (steps % c != 0 || steps / c > 16) continue;
     chosen = c;
     break;
@@ -2278,6 +2280,7 @@ bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (chosen == 0) return false;
   const int nw = int(steps / chosen);
   if (16 * a.G / 4 > int64_t(nw) * 64) return false;  // one scale piece per thread
+  if (16 * a.M > int64_t(nw) * 64) return false;      // one thread per output of the tile
   *err = a.act == kDtBf16 ? launch_oneshot<ActBf16>(a, chosen, nw, stream)
                           : launch_oneshot<ActF16>(a, chosen, nw, stream);
   return true;
@@ -2707,6 +2710,10 @@ int kr_tiles_per_wg(int64_t tiles) {
 // 2/4-bit codes in groups of 128, at most 7 tiles per workgroup over 256 workgroups.
 bool kr_shape(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   if ((bits != 2 && bits != 4) || group != 128 || K != 4096) return false;
+  // At 5-8 tokens, grids of up to 512 tiles (one or two per workgroup here) go to the one-shot
+  // kernel's eight-row form instead: measured on MI355X, o 6.1 -> 5.3 us at 5-6 tokens and
+  // 6.2 -> 5.6 at 8, qkv 7.7 -> 7.2-7.7; gate_up (1792 tiles) is 7-12 % faster here.
+  if (M <= 8 && (N + 15) / 16 <= 512) return false;
   return M >= 5 && M <= 32 && N >= 1 && kr_tiles_per_wg((N + 15) / 16) > 0;
 }
 
