@@ -2706,8 +2706,9 @@ int kr_tiles_per_wg(int64_t tiles) {
   return 0;
 }
 
-// The shapes the resident-activation kernel takes (alignment aside): 5..32 tokens, K = 4096,
-// 2/4-bit codes in groups of 128, at most 7 tiles per workgroup over 256 workgroups.
+// The shapes the resident-activation kernel takes (alignment aside): 5..32 tokens (9..32 on
+// grids of at most 512 tiles), K = 4096, 2/4-bit codes in groups of 128, at most 7 tiles per
+// workgroup over 256 workgroups.
 bool kr_shape(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   if ((bits != 2 && bits != 4) || group != 128 || K != 4096) return false;
   // At 5-8 tokens, grids of up to 512 tiles (one or two per workgroup here) go to the one-shot
