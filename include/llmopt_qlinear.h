@@ -20,8 +20,10 @@
  *     enqueued asynchronously; nothing synchronises the host.
  *   - Return value: LLMOPT_OK (0) or a negative LLMOPT_ERR_* code. The message of
  *     the last failure on the calling thread is llmopt_q_last_error().
- *   - Reentrant: no mutable global state; calls from several host threads on
- *     different streams are independent.
+ *   - Reentrant: the only mutable global state is the per-thread error text and
+ *     the static device scratch of llmopt_q_linear_noalloc (below); every other
+ *     entry point's calls from several host threads on different streams are
+ *     independent.
  *   - group_size <= 0 means one group spanning the whole row.
  *   - dtype codes: LLMOPT_DTYPE_F32 / F16 / BF16.
  *

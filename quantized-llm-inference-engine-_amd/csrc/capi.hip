@@ -30,10 +30,11 @@ constexpr int64_t kDecodeMaxTokens = 32;
 // kernels that split K themselves take them (given a workspace: the caller checks).
 // Batches of 33-64 tokens stay on the decode path where it streams them faster than the split-K
 // GEMM: over at least 1024 tiles of 16 features (gate_up) its N-split kernel (gate_up at M = 64:
-// 36.5 against 43 us), on smaller grids its K-sliced kernel.
+// 36.5 against 43 us), on smaller grids its K-sliced kernel -- each only for the weight formats
+// it takes (2/4-bit codes, groups of a multiple of 128); other formats stay on the GEMM.
 bool gemm_first(int64_t M, int64_t K, int64_t N, int64_t group, int bits) {
   if (M > kDecodeMaxTokens && M <= 64) {
-    if (N >= 16 * 1024 && K < 8192) return false;
+    if (N >= 16 * 1024 && K < 8192 && llmopt::nx_takes_wide(M, N, K, group, bits)) return false;
     if (llmopt::ks_takes(M, N, K, group, bits)) return false;
   }
   return M > kDecodeMaxTokens || (M >= 24 && K >= 8192);
@@ -180,6 +181,10 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
       }
       if (!gemm) {
         err = llmopt::launch_linear_decode(a, s, &fits);
+        // A batch above the decode threshold that no decode kernel took (an alignment or a
+        // workspace the planner assumed): the GEMMs before the generic kernel.
+        if (!fits && M > kDecodeMaxTokens) err = llmopt::launch_linear_gemm(a, s, &fits);
+        if (!fits && M > kDecodeMaxTokens) err = llmopt::launch_linear_prefill(a, s, &fits);
       } else {
         err = llmopt::launch_linear_gemm(a, s, &fits);
         if (!fits && M <= 64) err = llmopt::launch_linear_decode(a, s, &fits);
@@ -341,10 +346,11 @@ size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bit
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const int64_t g = group_size <= 0 ? K : group_size;
   const bool nibble = bits == 2 || bits == 4;
-  // Sizes whose kernels apply the activation themselves (assuming aligned, contiguous tensors).
+  // Sizes whose kernels apply the activation themselves (assuming aligned, contiguous tensors):
+  // the decode path's partial sums where its plan splits K, else nothing.
   if (nibble && (M <= kDecodeMaxTokens || !gemm_first(M, K, N, g, bits)) && g % 128 == 0 && K % 128 == 0 &&
       (K / g) % 4 == 0 && (M <= 4 || K <= 8192))
-    return 0;
+    return M <= 64 ? llmopt::decode_workspace_bytes(M, N, K, g, bits) : 0;
   if (M > kDecodeMaxTokens && bits >= 1 && bits <= 8 && g % 32 == 0 && K % 64 == 0)
     return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
   // Otherwise: the full [M, N] output in fp32-sized slots, then the combining kernel.

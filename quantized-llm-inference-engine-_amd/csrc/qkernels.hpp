@@ -151,5 +151,7 @@ hipError_t launch_splitk_reduce(const LinearArgs& a, const float* partials, int 
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
 // Whether the decode path's K-sliced kernel takes this size (given its workspace).
 bool ks_takes(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
+// Whether the decode path's N-split kernel takes this 33-64-token size (grids of >= 1024 tiles).
+bool nx_takes_wide(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
 
 }  // namespace llmopt

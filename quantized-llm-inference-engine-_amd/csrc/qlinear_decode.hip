@@ -1063,7 +1063,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
   auto issue_meta = [&](int j) {
     const int64_t tile = first + int64_t(j) * stride;
     float* dstbase = meta + (j & 1) * 2 * G * 16;
-    const uint32_t so = uint32_t(tile * 16 * a.G * 4);  // rows past N: past the tensors, zeros
+    // The tile's offset goes in the per-lane offset, which the buffer range check covers (the
+    // scalar offset is not checked): rows past N then read zeros instead of past the tensors.
+    const uint32_t to = uint32_t(tile * 16 * a.G * 4);
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
       const int p = wave * NB + q;
@@ -1071,7 +1073,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
       const int piece = p - arr * (G / 4);
       float* dst = dstbase + arr * G * 16 + piece * 64;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(arr ? mz : ms, (__attribute__((address_space(3))) void*)dst, 4,
-                                               meta_lane_off + uint32_t(piece) * 16, so, 0, kLoadPolicy);
+                                               to + meta_lane_off + uint32_t(piece) * 16, 0, 0, kLoadPolicy);
     }
   };
   const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
@@ -1998,12 +2000,14 @@ __global__ void __launch_bounds__(NW * 64)
   auto issue = [&](int j) {
     const int64_t tile = first + int64_t(j) * per_slice;
     uint8_t* slot = ring + (j % R) * Geo::kSlot;
-    // Rows past N: the metadata reads past the tensors (zeros), the codes repeat row N - 1.
-    const uint32_t mo = uint32_t(tile * 16 * a.G * 4);
+    // Rows past N: the metadata offset (per lane, so the buffer range check covers it; the
+    // scalar offset is not checked) lies past the tensors and reads zeros; the codes repeat
+    // row N - 1.
+    const uint32_t mo = uint32_t(tile * 16 * a.G * 4) + meta_lane;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(ms, (__attribute__((address_space(3))) void*)(slot + Geo::kCodeBytes),
-                                             4, meta_lane, mo, 0, kLoadPolicy);
+                                             4, mo, 0, 0, kLoadPolicy);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(mz, (__attribute__((address_space(3))) void*)(slot + Geo::kCodeBytes + 256),
-                                             4, meta_lane, mo, 0, kLoadPolicy);
+                                             4, mo, 0, 0, kLoadPolicy);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       int64_t n = tile * 16 + 8 * h + r8;
@@ -2808,6 +2812,15 @@ hipError_t launch_skinny(const LinearArgs& a, hipStream_t stream, bool* fits) {
 
 bool ks_takes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   return plan_ks(M, N, K, group, bits).slices > 0;
+}
+
+bool nx_takes_wide(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
+  // try_nx's 33-64-token form, reached through try_mt (its shape conditions; alignments are
+  // checked at launch, and a refusal there falls back to the GEMM).
+  if (bits != 2 && bits != 4) return false;
+  if (M <= 32 || M > 64 || (N + 15) / 16 < 1024) return false;
+  if (group % 128 != 0 || K % 128 != 0 || (K / group) % 4 != 0) return false;
+  return (K / 128) % 2 == 0 && nx_lds_bytes<4, 1, 8, 2>(K / group) <= 160 * 1024;
 }
 
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {

@@ -63,7 +63,10 @@ __device__ __forceinline__ Grid group_grid(float lo, float hi, int bits, bool sy
 // Floating-Point Arithmetic, ch. 4). rne(q1) can only differ from rne(w / s) when w / s lies
 // within an ulp of a half-integer; tests/test_quotient_exactness.py checks every fp32 s in
 // [1, 2), every half-integer below 256 and the w within 4 ulps of s times it (all agree), and
-// the steps scale exactly with s and w for 1e-8 <= s <= 2^120. Larger or non-finite scales
+// the steps scale exactly with s and w (by powers of two) while the remainder stays exactly
+// representable: for every s from 2^-100 to 2^120 once |w / s| >= 1/4 (below that both sides
+// round to zero). The quantizers' smallest scale is 1e-8 / 127 (about 7.9e-11: the amax floor
+// of an 8-bit symmetric grid), inside that range. Larger or non-finite scales
 // (r near the subnormal range, or 0) take the correctly rounded division, behind a branch that
 // is wave-uniform in practice.
 __device__ __forceinline__ void rint_quotients(const float* v, const Grid& g, float* ratio) {

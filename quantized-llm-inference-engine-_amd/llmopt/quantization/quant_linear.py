@@ -157,18 +157,18 @@ def replace_linear_modules(
     """Put ``replacements[child]`` in place of every child module that is a key (in place).
 
     Behaviour of ``quant_linear.py:122-136``. The slots are found first and filled after,
-    so a replacement that itself contains replaced modules is not visited. A module
-    registered under several parents is replaced in each of them; ``model`` itself is
-    never replaced.
+    so a replacement that itself contains replaced modules is not visited. Each module
+    keeps one slot, the last one the walk over ``model.modules()`` finds: a module
+    registered under several parents is replaced only there, as in the reference.
+    ``model`` itself is never replaced.
     """
-    slots = [
-        (parent, attr)
-        for parent in model.modules()
-        for attr, child in parent.named_children()
-        if child in replacements
-    ]
-    for parent, attr in slots:
-        setattr(parent, attr, replacements[getattr(parent, attr)])
+    slot_of: dict[nn.Module, tuple[nn.Module, str]] = {}
+    for parent in model.modules():
+        for attr, child in parent.named_children():
+            if child in replacements:
+                slot_of[child] = (parent, attr)
+    for child, (parent, attr) in slot_of.items():
+        setattr(parent, attr, replacements[child])
     return model
 
 

@@ -4,8 +4,10 @@
  * every half-integer h = k + 0.5 with k < 256 (|w / s| stays below 256 for 2- to 8-bit codes),
  * and every w within 4 ulps of RN(s h): the only w for which rne(q1) could differ from
  * rne(w / s), since elsewhere both lie within an ulp of w / s and no half-integer is that
- * close. All steps scale exactly with s and w (same power of two) while no value leaves the
- * normal range, which holds for 1e-8 <= s <= 2^120. Prints the case count and the number of
+ * close. All steps scale exactly with s and w (same power of two) while the remainder stays
+ * exactly representable: for every s from 2^-100 to 2^120 once |w / s| >= 1/4 (below that
+ * both sides round to zero); the quantizers' smallest scale, 1e-8 / 127 (8-bit symmetric), is
+ * inside that range. Prints the case count and the number of
  * cases where q1 != RN(w / s); exits 1 if any. argv[1] (optional): significand stride. */
 #include <math.h>
 #include <stdint.h>

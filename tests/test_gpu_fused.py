@@ -120,7 +120,8 @@ def test_swiglu_k_sliced_single_slice(m):
     assert _rel_err(y, ref) <= SWIGLU_TOL, m
 
 
-@pytest.mark.parametrize("m", [1, 8, 16, 32, 40, 64, 2048])
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("m", [1, 8, 16, 32, 40, 64, 2048, 16384])
 def test_swiglu_llama_gate_up(m):
     dtype = torch.bfloat16
     inter, k = 14336, 4096
@@ -178,3 +179,43 @@ def test_swiglu_long_rows_over_k_slices(m):
     u = (x.float() @ dequantize(up, dtype).float().t().contiguous()).to(dtype)
     ref = torch.nn.functional.silu(g.float()).to(dtype).float() * u.float()
     assert _rel_err(y, ref) <= SWIGLU_TOL
+
+
+def _swiglu_of_product(t: torch.Tensor, dtype) -> torch.Tensor:
+    """The reference's SwiGLU (layers.py:44) on a fused [M, 2I] product in the compute dtype:
+    gate row 4p + r is fused column 8p + r, up row 4p + r is fused column 8p + 4 + r."""
+    m, n = t.shape
+    blocks = t.view(m, n // 8, 2, 4)
+    g, u = blocks[:, :, 0, :].reshape(m, n // 2), blocks[:, :, 1, :].reshape(m, n // 2)
+    return (torch.nn.functional.silu(g.float()).to(dtype).float() * u.float()).to(dtype)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("m", [1, 8, 32, 64, 256, 2048, 16384])
+def test_swiglu_epilogue_is_the_reference_activation_of_the_product(m):
+    # The fused output splits into a GEMM output held to the 1e-2 bound of a single quantized
+    # linear and an epilogue that applies the reference's activation to it: the product
+    # without the epilogue (same weight, same kernel family, same summation order) is checked
+    # against the oracle on sampled columns, and the fused output against silu(gate) * up of
+    # that product in the compute dtype, to within one bf16 rounding step (silu's exp in the
+    # kernel and in torch may differ in the last fp32 bits, which can move a rounding).
+    dtype = torch.bfloat16
+    inter, k = 14336, 4096
+    gate = _host_qt(inter, k, 4, 128, False, seed=1)
+    up = _host_qt(inter, k, 4, 128, False, seed=2)
+    fused_host = interleave_gate_up(gate, up)
+    fused = _to_device(fused_host)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(dtype)
+    xd = x.to(DEV)
+    t = ops.quant_linear(xd, fused, None, dtype)
+    y = ops.quant_linear_swiglu(xd, fused, None, dtype)
+    cols = np.sort(np.random.default_rng(m).choice(2 * inter, size=256, replace=False))
+    rows = np.arange(m) if m <= 2048 else np.sort(np.random.default_rng(m + 1).choice(m, size=256, replace=False))
+    ref = _ref_linear(x[torch.from_numpy(rows)], _oracle_dense(fused_host)[cols], dtype)
+    got = t[torch.from_numpy(rows).to(DEV)][:, torch.from_numpy(cols).to(DEV)]
+    assert _rel_err(got, ref) <= 1e-2
+    want = _swiglu_of_product(t, dtype).float()
+    diff = (y.float() - want).abs()
+    step = want.abs() * 2.0 ** -7 + 2.0 ** -133  # one bf16 rounding step at each value
+    assert bool((diff <= step).all()), float((diff / step).max())
+    assert float((diff == 0).float().mean()) >= 0.99

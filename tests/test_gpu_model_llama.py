@@ -86,6 +86,35 @@ def test_llama3_8b_width_decoder_matches_the_oracle_reference(llama_two_layers, 
     assert torch.equal(got.argmax(-1)[sure], want.argmax(-1)[sure])
 
 
+@pytest.mark.timeout(900)
+def test_llama3_8b_width_decoder_end_to_end_prompt_batch(llama_two_layers):
+    # The end-to-end workload's prefill on the GPU: 32 prompts of 512 tokens (16384 rows
+    # through the fused projections and the prefill GEMMs, 512-token contexts in the paged
+    # cache), then two teacher-forced decode steps; one decoder layer. Sequences are
+    # independent, so the host reference runs three of them (first, middle, last) and their
+    # last-position logits are compared (src/llmopt/model/modeling.py:88-131,
+    # model/layers.py:39-44,106-108,142).
+    gpu, twin = llama_two_layers
+    keep_gpu, keep_twin = gpu.layers, twin.layers
+    gpu.layers, twin.layers = keep_gpu[:1], keep_twin[:1]
+    pick = torch.tensor([0, 17, 31])
+    try:
+        g = torch.Generator().manual_seed(11)
+        prompts = torch.randint(0, 128256, (32, 512), generator=g)
+        forced = torch.randint(0, 128256, (32, 2), generator=g)
+        got = forced_logits(gpu, prompts, forced)[:, pick]
+        torch.cuda.empty_cache()
+        want = forced_logits(twin, prompts[pick], forced[pick])
+    finally:
+        gpu.layers, twin.layers = keep_gpu, keep_twin
+    errs = [rel(got[i], want[i]) for i in range(got.shape[0])]
+    print("32 x 512-token prompts, 1 layer: max-abs-rel per step (prefill, decode...):",
+          ["%.2e" % e for e in errs], flush=True)
+    assert max(errs) <= PER_LAYER_BOUND, errs
+    sure = confident_positions(want, 2 * PER_LAYER_BOUND * float(want.abs().max()))
+    assert torch.equal(got.argmax(-1)[sure], want.argmax(-1)[sure])
+
+
 @pytest.fixture(scope="module")
 def deep_narrow():
     cfg = dataclasses.replace(ModelConfig.tiny(), num_hidden_layers=32)

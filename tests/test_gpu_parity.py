@@ -394,6 +394,45 @@ def test_projection_sampled_columns_and_gpu_fp32(projections, name, m):
     assert _rel_err(y, ref_gpu) <= 1e-2
 
 
+def _gpu_rel_err(y: torch.Tensor, ref: torch.Tensor) -> float:
+    """max|y - ref| / max|ref| computed on the device (for outputs of a few GB)."""
+    d = float(ref.float().abs().max())
+    return float((y.float() - ref.float()).abs().max()) / (d if d > 0 else 1.0)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("name", list(PROJECTIONS))
+def test_projection_end_to_end_prefill_batch(projections, name):
+    # The end-to-end workload's prefill: 32 prompts x 512 tokens = 16384 rows through each
+    # projection in one call (src/llmopt/model/layers.py:39-44,106-108,142). Sampled rows x
+    # columns against the CPU reference; every output against a torch fp32 GPU matmul of the
+    # bit-exact dequantized weight; scaling x by 2 scales y by 2 exactly; one-hot activation
+    # rows return the dequantized weight's columns bit for bit.
+    m = 16384
+    qt, dqt, dense = projections[name]
+    n, k = qt.shape
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    xd = x.to(DEV)
+    y = ops.quant_linear(xd, dqt, None, torch.bfloat16)
+    rng = np.random.default_rng(m + n)
+    rows = np.sort(rng.choice(m, size=256, replace=False))
+    cols = np.sort(rng.choice(n, size=256, replace=False))
+    ref = _reference_linear(x[torch.from_numpy(rows)], dense, None, torch.bfloat16, cols=cols)
+    got = y[torch.from_numpy(rows).to(DEV)][:, torch.from_numpy(cols).to(DEV)]
+    assert _rel_err(got, ref) <= 1e-2
+    w = dequantize(dqt, torch.bfloat16)  # bit-exact with the oracle (checked above)
+    ref_gpu = torch.matmul(xd.float(), w.float().t().contiguous())
+    assert _gpu_rel_err(y, ref_gpu) <= 1e-2
+    del ref_gpu
+    assert torch.equal(ops.quant_linear(xd * 2, dqt, None, torch.bfloat16), y * 2)
+    del y
+    picks = torch.from_numpy(rng.choice(k, size=m, replace=True)).to(DEV)
+    one_hot = torch.zeros(m, k, dtype=torch.bfloat16, device=DEV)
+    one_hot[torch.arange(m, device=DEV), picks] = 1.0
+    y1 = ops.quant_linear(one_hot, dqt, None, torch.bfloat16)
+    assert torch.equal(y1.view(torch.int16), w[:, picks].t().contiguous().view(torch.int16))
+
+
 @pytest.mark.parametrize("name", list(PROJECTIONS))
 @pytest.mark.parametrize("m", [1, 64, 2048, 8192])
 def test_projection_one_hot_rows_return_weight_columns(projections, name, m):
@@ -428,6 +467,20 @@ def test_down_projection_bit_width_sweep(bits, symmetric, m):
     y = ops.quant_linear(x.to(DEV), dqt, None, torch.bfloat16)
     cols = np.sort(np.random.default_rng(bits + m).choice(4096, size=128, replace=False))
     ref = _reference_linear(x, dense, None, torch.bfloat16, cols=cols)
+    assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= 1e-2
+
+
+@pytest.mark.parametrize("m", [33, 48, 64])
+@pytest.mark.parametrize("bits, group", [(8, 128), (4, 32), (4, 64), (4, 128)])
+def test_wide_grids_at_33_to_64_tokens_every_format(m, bits, group):
+    # 33-64 tokens over 1024 tiles of 16 features with K = 4096: 2/4-bit codes in groups of a
+    # multiple of 128 run on the N-split decode kernel, other formats on the split-K GEMM.
+    n, k = 16384, 4096
+    qt = _host_qt(n, k, bits, group, False, seed=m + bits + group)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None, torch.bfloat16)
+    cols = np.sort(np.random.default_rng(m + group).choice(n, size=256, replace=False))
+    ref = _reference_linear(x, _oracle_dense(qt), None, torch.bfloat16, cols=cols)
     assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= 1e-2
 
 

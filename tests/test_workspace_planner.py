@@ -107,3 +107,27 @@ def test_prefill_plans_above_64_tokens(lib):
             assert ws % (m * n * 4) == 0 and ws // (m * n * 4) in (0, 2, 3, 4, 5, 6, 7, 8), (shape, m, ws)
     # A full grid of 256-token tiles does not split.
     assert _ws(lib, 8192, GATE_UP) == 0
+
+
+def test_wide_grids_at_33_to_64_tokens_keep_the_gemm_for_other_formats(lib):
+    # 33-64 tokens over >= 1024 tiles (N >= 16384) with K < 8192 leave the split-K GEMM only
+    # for the N-split decode kernel, which takes 2/4-bit codes in groups of a multiple of 128;
+    # 8-bit codes and groups of 32 or 64 stay on the GEMM and its K split.
+    n, k = 16384, 4096
+    for m in (33, 48, 64):
+        assert _ws(lib, m, (n, k)) == 0, m
+        for bits, group in ((8, 128), (4, 32), (4, 64)):
+            ws = _ws(lib, m, (n, k), bits=bits, group=group)
+            assert ws > 0 and ws % (m * n * 4) == 0, (m, bits, group, ws)
+
+
+def test_swiglu_workspace_names_the_decode_k_split(lib):
+    # Where the fused SwiGLU product runs on the K-sliced decode kernel with several slices,
+    # the query returns its partial sums, so a caller sizing by it gets that kernel.
+    ws = lib.llmopt_q_linear_swiglu_workspace
+    assert ws(16, 8192, 8192, 4, 128) == 4 * 16 * 8192 * 4
+    assert ws(48, 8192, 4096, 4, 128) == 2 * 48 * 8192 * 4
+    assert ws(48, 8192, 4096, 4, 128) == _ws(lib, 48, (8192, 4096))
+    # Resident-activation and N-split shapes keep all of K.
+    assert ws(16, 28672, 4096, 4, 128) == 0
+    assert ws(64, 28672, 4096, 4, 128) == 0

@@ -68,9 +68,10 @@ def test_noalloc_refuses_plans_beyond_its_scratch():
     n, k, m = 6144, 8192, 768
     assert lib.llmopt_q_linear_workspace(m, n, k, 4, 128) > cap
     qw, sc, zr = _weight(n, k, 3)
-    x = torch.zeros(m, k, dtype=torch.bfloat16, device=DEV)
-    y = torch.zeros(m, n, dtype=torch.bfloat16, device=DEV)
+    # A non-zero input and a NaN-filled output: any kernel that ran would overwrite the NaNs.
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(DEV)
+    y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
     rc = lib.llmopt_q_linear_noalloc(*_args(x, qw, sc, zr, y, n, k, m), torch.cuda.current_stream().cuda_stream)
     assert rc == -4 and b"static scratch" in lib.llmopt_q_last_error()
     torch.cuda.synchronize()
-    assert int(torch.count_nonzero(y)) == 0  # nothing was launched
+    assert bool(torch.isnan(y).all())  # nothing was launched
