@@ -76,6 +76,7 @@ BF16_PEAK_TFLOPS = 2500.0
 PROJECTIONS = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
 GROUP = 128
 MIN_ROTATION_BYTES = 512 * 2**20
+REPLAYS = 50  # timed graph replays per figure (each of several back-to-back launches); median
 TRAFFIC_FILE = REPO / "profiles" / "traffic_decode_gate_up_m1.json"
 COPY_BYTES = 256 * 2**20
 
@@ -153,10 +154,11 @@ def build_rotations(layers, min_bytes: int = MIN_ROTATION_BYTES):
     return rot
 
 
-def kernel_launch_times(torch, launch, count: int, replays: int = 7) -> list[float]:
+def kernel_launch_times(torch, launch, count: int, replays: int = REPLAYS) -> list[float]:
     """Per-launch times (us) of `count` back-to-back launches captured in one HIP graph and
-    replayed `replays` times, each replay bracketed by HIP events on the replay stream. The
-    figure includes the few-microsecond gap the GPU leaves between two dependent kernels."""
+    replayed `replays` times (after one untimed replay), each replay bracketed by HIP events on
+    the replay stream. The figure includes the few-microsecond gap the GPU leaves between two
+    dependent kernels. Callers report the median over the replays."""
     side = torch.cuda.Stream()
     with torch.cuda.stream(side):
         launch(0)
@@ -355,22 +357,34 @@ def main() -> int:
     if not args.no_shapes:
         result["shapes"] = shapes(torch, ops, rotations)
         result["bits_sweep"], gptq = bits_sweep(torch, ops)
+        result["engine_config"] = engine_config(torch, ops)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(torch, base, args.m, args.cpu_seconds, gptq)
     print(json.dumps(result), flush=True)
     return 0
 
 
+def _code_only(text: str) -> str:
+    """A C++ source without its comments and blank-line or indentation differences: what the
+    compiler sees (no kernel source here has comment markers inside string literals)."""
+    import re
+
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return "\n".join(" ".join(line.split()) for line in text.splitlines() if line.strip())
+
+
 def source_digest() -> str:
-    """sha256 (16 hex digits) of the kernel sources the library is built from: names the build
-    a counter measurement belongs to."""
+    """sha256 (16 hex digits) of the code of the kernel sources the library is built from, comments
+    and layout left out: names the build a counter measurement belongs to, so that a change to a
+    comment does not orphan a measurement and a change to the code does."""
     import hashlib
 
     h = hashlib.sha256()
     csrc = REPO / "quantized-llm-inference-engine-_amd" / "csrc"
     for path in sorted(list(csrc.glob("*.hip")) + list(csrc.glob("*.hpp"))):
         h.update(path.name.encode())
-        h.update(path.read_bytes())
+        h.update(_code_only(path.read_text()).encode())
     return h.hexdigest()[:16]
 
 
@@ -399,9 +413,9 @@ def prefill(torch, ops, rotations):
     x = torch.randn(m, k, device="cuda:0").to(torch.bfloat16)
     ops.quant_linear(x, qts[0], None, torch.bfloat16)
     times = kernel_launch_times(
-        torch, lambda i: ops.quant_linear(x, qts[i % len(qts)], None, torch.bfloat16), len(qts), 3
+        torch, lambda i: ops.quant_linear(x, qts[i % len(qts)], None, torch.bfloat16), len(qts)
     )
-    us = statistics.mean(times)
+    us = statistics.median(times)
     tflops = 2 * m * n * k / (us * 1e-6) / 1e12
     print(f"# prefill gate_up M={m}: {us:.1f} us, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
     dense = dense_comparator(torch, qts[0], m)
@@ -494,7 +508,7 @@ def dequant_rate(torch, ops, rotations):
     name, n, k = PROJECTIONS[2]
     qts = rotations[name]
     count = min(len(qts), 8)
-    times = kernel_launch_times(torch, lambda i: ops.dequantize(qts[i % count], torch.bfloat16), count, 3)
+    times = kernel_launch_times(torch, lambda i: ops.dequantize(qts[i % count], torch.bfloat16), count)
     us = statistics.median(times)
     moved = algorithmic_bytes(0, n, k) + 2 * n * k
     gbs = moved / (us * 1e-6) / 1e9
@@ -514,7 +528,7 @@ def quantize_rate(torch, ops):
     gen = torch.Generator(device="cuda:0").manual_seed(5)
     copies = max(2, -(-MIN_ROTATION_BYTES // (2 * n * k)))
     ws = [(torch.randn(n, k, generator=gen, device="cuda:0") * 0.02).to(torch.bfloat16) for _ in range(copies)]
-    times = kernel_launch_times(torch, lambda i: ops.quantize_rtn(ws[i % copies], 4, GROUP, False), 2 * copies, 3)
+    times = kernel_launch_times(torch, lambda i: ops.quantize_rtn(ws[i % copies], 4, GROUP, False), 2 * copies)
     us = statistics.median(times)
     moved = 2 * n * k + algorithmic_bytes(0, n, k)
     gbs = moved / (us * 1e-6) / 1e9
@@ -562,7 +576,7 @@ def attention_rates(torch):
     lens = ctx.to(torch.int32).to(dev)
     q = torch.randn(seqs, heads, 1, head_dim, device=dev).to(torch.bfloat16)
     attn = PagedAttention(heads, kv_heads, head_dim, config=PagedAttentionConfig(block_size=bs))
-    times = kernel_launch_times(torch, lambda i: attn.forward(q, cache, i % layers, table, lens), 2 * layers, 5)
+    times = kernel_launch_times(torch, lambda i: attn.forward(q, cache, i % layers, table, lens), 2 * layers)
     us = statistics.median(times)
     moved = int(ctx.sum()) * kv_heads * head_dim * 2 * 2 + 2 * q.numel() * 2 + table.numel() * 4
     gbs = moved / (us * 1e-6) / 1e9
@@ -577,7 +591,7 @@ def attention_rates(torch):
     new_k = torch.randn(seqs, kv_heads, head_dim, device=dev).to(torch.bfloat16)
     offsets = (lens - 1).to(torch.int64)
     w_times = kernel_launch_times(torch, lambda i: cache.write_decode(i % layers, table, offsets, new_k, new_k),
-                                  2 * layers, 5)
+                                  2 * layers)
     print(f"# paged decode attention (32 seqs x 512-640 tokens, 32/8 heads): {us:.1f} us, {gbs:.0f} GB/s; "
           f"torch sequence {torch_us:.0f} us; KV write {statistics.median(w_times):.1f} us",
           file=sys.stderr, flush=True)
@@ -588,8 +602,8 @@ def attention_rates(torch):
     head = torch.nn.Linear(hidden_size, vocab, bias=False, device=dev, dtype=torch.bfloat16)
     hidden = torch.randn(seqs * q_len, hidden_size, device=dev).to(torch.bfloat16)
     with torch.no_grad():
-        full = kernel_launch_times(torch, lambda i: head(hidden), 2, 3)
-        last = kernel_launch_times(torch, lambda i: last_token_logits(hidden, head, q_len), 8, 3)
+        full = kernel_launch_times(torch, lambda i: head(hidden), 2, 10)
+        last = kernel_launch_times(torch, lambda i: last_token_logits(hidden, head, q_len), 8)
     full_us, last_us = statistics.median(full), statistics.median(last)
     print(f"# lm_head over a 32 x 512 prefill chunk: all positions {full_us:.0f} us, last positions {last_us:.0f} us",
           file=sys.stderr, flush=True)
@@ -619,7 +633,7 @@ def dense_comparator(torch, qt, m: int):
     ws = [w] + [w.clone() for _ in range(copies - 1)]
     x = torch.randn(m, k, device="cuda:0").to(torch.bfloat16)
     f = torch.nn.functional.linear
-    times = kernel_launch_times(torch, lambda i: f(x, ws[i % copies]), 2 * copies if m <= 64 else copies, 3)
+    times = kernel_launch_times(torch, lambda i: f(x, ws[i % copies]), 2 * copies if m <= 64 else copies)
     us = statistics.median(times)
     dense_bytes = 2 * n * k + 2 * m * k + 2 * m * n
     out = {"op": f"F.linear bf16 [{m}, {k}] x [{n}, {k}]^T", "us": round(us, 2),
@@ -680,7 +694,7 @@ def bits_sweep(torch, ops):
             x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
             ops.quant_linear(x, qts[0], None, torch.bfloat16)
             times = kernel_launch_times(
-                torch, lambda i: ops.quant_linear(x, qts[i % copies], None, torch.bfloat16), 2 * copies, 3
+                torch, lambda i: ops.quant_linear(x, qts[i % copies], None, torch.bfloat16), 2 * copies
             )
             us = statistics.median(times)
             gbs = algorithmic_bytes(m, n, k, bits=bits, asym=not qt.symmetric) / (us * 1e-6) / 1e9
@@ -693,6 +707,61 @@ def bits_sweep(torch, ops):
             del x
         del qts
     return rows, gptq_asym
+
+
+def engine_config(torch, ops):
+    """The reference engine's own quantized configuration: ``LLMEngine.from_pretrained(quantize=
+    True)`` quantizes a float32 model with ``quantize_model_(model, bits=4, group_size=64)``
+    (symmetric), and each QuantLinear computes in float32 (src/llmopt/engine/llm_engine.py:258-264,
+    quantization/quant_linear.py:199-201, model/modeling.py:57-58). Per projection and M in
+    {1, 32, 2048}: the fp32 path (three exact bf16 pieces per activation on the decode kernels,
+    fp32 sums), bf16 activations on the same packed weight, and the reference's way in fp32 on the
+    same GPU (F.linear on the dequantized fp32 weight, dense and cached), each rotating over at
+    least 512 MiB of weight copies. GB/s counts the fp32 (or bf16) activations and outputs."""
+    from llmopt.quantization import QuantizedTensor, RoundToNearestQuantizer, dequantize
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(6)
+    group = 64
+    rows = []
+    f = torch.nn.functional.linear
+    for name, n, k in PROJECTIONS:
+        w = torch.randn(n, k, generator=gen, device=dev) * 0.02
+        qt = RoundToNearestQuantizer(4, group, symmetric=True).quantize(w)
+        del w
+        packed = algorithmic_bytes(0, n, k, group=group, asym=False)
+        copies = max(2, -(-MIN_ROTATION_BYTES // packed))
+        qts = [qt] + [QuantizedTensor(qt.qweight.clone(), qt.scales.clone(), qt.zeros.clone(), 4, group, True,
+                                      qt.shape) for _ in range(copies - 1)]
+        dense = dequantize(qt, torch.float32)
+        dcopies = max(2, -(-MIN_ROTATION_BYTES // (4 * n * k)))
+        dws = [dense] + [dense.clone() for _ in range(dcopies - 1)]
+        for m in (1, 32, 2048):
+            reps = 2 * copies if m <= 64 else copies
+            row = {"proj": name, "N": n, "K": k, "M": m, "bits": 4, "group": group, "symmetric": True}
+            for label, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+                x = torch.randn(m, k, generator=gen, device=dev).to(dt)
+                ops.quant_linear(x, qts[0], None, dt)
+                us = statistics.median(
+                    kernel_launch_times(torch, lambda i: ops.quant_linear(x, qts[i % copies], None, dt), reps))
+                es = 4 if dt == torch.float32 else 2
+                nbytes = packed + es * m * k + es * m * n
+                row[f"{label}_us"] = round(us, 2)
+                row[f"{label}_GB/s"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+                row[f"{label}_TFLOP/s"] = round(2 * m * n * k / (us * 1e-6) / 1e12, 2)
+                if dt == torch.float32:
+                    xr = x
+            ref_us = statistics.median(kernel_launch_times(
+                torch, lambda i: f(xr, dws[i % dcopies]), 2 * dcopies if m <= 64 else dcopies, 20))
+            row["reference_fp32_us"] = round(ref_us, 2)
+            row["fp32_vs_bf16"] = round(row["fp32_us"] / row["bf16_us"], 3)
+            row["reference_fp32_vs_fp32"] = round(ref_us / row["fp32_us"], 3)
+            rows.append(row)
+            print(f"# engine config {name:8s} M={m:5d} fp32 {row['fp32_us']:9.2f} us ({row['fp32_GB/s']:7.1f} GB/s) "
+                  f"bf16 {row['bf16_us']:8.2f} us  reference fp32 way {ref_us:9.2f} us", file=sys.stderr, flush=True)
+            del x, xr
+        del qts, dws, dense
+    return rows
 
 
 def shapes(torch, ops, rotations):
@@ -708,7 +777,7 @@ def shapes(torch, ops, rotations):
             ops.quant_linear(x, qts[0], None, bf16)
             reps = 2 * len(qts) if m <= 2048 else min(len(qts), 16)
             times = kernel_launch_times(
-                torch, lambda i: ops.quant_linear(x, qts[i % len(qts)], None, bf16), reps, 3
+                torch, lambda i: ops.quant_linear(x, qts[i % len(qts)], None, bf16), reps
             )
             us = statistics.median(times)
             gbs = algorithmic_bytes(m, n, k) / (us * 1e-6) / 1e9

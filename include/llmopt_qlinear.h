@@ -107,6 +107,17 @@ int llmopt_q_quantize_rtn(const void* weight, int w_dtype, int64_t ldw, int64_t 
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size);
 
 /*
+ * llmopt_q_linear_workspace for an activation dtype: the same for LLMOPT_DTYPE_BF16 / F16; for
+ * LLMOPT_DTYPE_F32 the bytes of the fp32 path -- each activation split exactly into three bf16
+ * pieces (3 * M * K * 2 bytes), the decode kernels' fp32 sums of a chunk of up to 21 tokens
+ * (3 * chunk * N * 4) and their K-split partial sums. With less, fp32 runs on the generic kernel.
+ * Sizes the workspace of QuantLinear.forward with compute_dtype float32
+ * (src/llmopt/quantization/quant_linear.py:93-113), the reference engine's quantized model
+ * (engine/llm_engine.py:258-264).
+ */
+size_t llmopt_q_linear_workspace_ex(int64_t M, int64_t N, int64_t K, int bits, int group_size, int act_dtype);
+
+/*
  * y = x @ dequant(qweight)^T + bias, without materialising the dense weight.
  * Replaces QuantLinear.forward (src/llmopt/quantization/quant_linear.py:93-113):
  * the reference dequantizes into a cached dense weight and calls F.linear.
@@ -155,6 +166,14 @@ int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const v
  * assuming 16-byte aligned, contiguous tensors (0 if none).
  */
 size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size);
+
+/*
+ * llmopt_q_linear_swiglu_workspace for an activation dtype (LLMOPT_DTYPE_F32: the [M, N] fp32
+ * product and the fp32 path's workspace, as llmopt_q_linear_workspace_ex). Sizes the workspace
+ * of SwiGLUMLP.forward (src/llmopt/model/layers.py:43-44) in a float32 model.
+ */
+size_t llmopt_q_linear_swiglu_workspace_ex(int64_t M, int64_t N, int64_t K, int bits, int group_size,
+                                           int act_dtype);
 
 /*
  * The gated activation of the reference's MLP, silu(gate(x)) * up(x), from one quantized

@@ -159,13 +159,20 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
     const size_t temp = swiglu_temp_bytes(M, N);
     if (!workspace || workspace_bytes < temp || reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
       return fail(LLMOPT_ERR_WORKSPACE, "this shape needs a workspace of at least %zu bytes",
-                  temp + llmopt_q_linear_workspace(M, N, K, bits, group_size));
+                  temp + llmopt_q_linear_workspace_ex(M, N, K, bits, group_size, act_dtype));
     void* t = workspace;
     rc = run_linear(x, M, K, ldx, qweight, ldq, scales, zeros, bias, t, N, N, act_dtype, bits,
                     group_size, symmetric, signed_codes, static_cast<uint8_t*>(workspace) + temp,
                     workspace_bytes - temp, stream, algo, llmopt::kEpiNone);
     if (rc != LLMOPT_OK) return rc;
     return hip_status(llmopt::launch_swiglu_combine(t, N, y, ldy, M, N, act_dtype, s), "swiglu launch");
+  }
+
+  if (act_dtype == LLMOPT_DTYPE_F32 && algo == LLMOPT_ALGO_AUTO) {
+    // fp32 activations: three bf16 pieces per token on the decode kernels (given the workspace
+    // llmopt_q_linear_workspace_ex asks for), else the generic kernel below.
+    err = llmopt::launch_linear_f32_pieces(a, s, &fits);
+    if (fits) return hip_status(err, "linear launch");
   }
 
   switch (algo) {
@@ -332,6 +339,12 @@ size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int 
   return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
 }
 
+size_t llmopt_q_linear_workspace_ex(int64_t M, int64_t N, int64_t K, int bits, int group_size, int act_dtype) {
+  if (act_dtype != LLMOPT_DTYPE_F32) return llmopt_q_linear_workspace(M, N, K, bits, group_size);
+  if (M <= 0 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
+  return llmopt::f32_workspace_bytes(M, N, K, group_size <= 0 ? K : group_size, bits);
+}
+
 int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
                        int64_t ldq, const float* scales, const float* zeros, const void* bias,
                        void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
@@ -355,6 +368,15 @@ size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bit
     return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
   // Otherwise: the full [M, N] output in fp32-sized slots, then the combining kernel.
   return swiglu_temp_bytes(M, N) + llmopt_q_linear_workspace(M, N, K, bits, group_size);
+}
+
+size_t llmopt_q_linear_swiglu_workspace_ex(int64_t M, int64_t N, int64_t K, int bits, int group_size,
+                                           int act_dtype) {
+  if (act_dtype != LLMOPT_DTYPE_F32) return llmopt_q_linear_swiglu_workspace(M, N, K, bits, group_size);
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  // No fp32 kernel applies the activation itself: the product into the workspace, then the
+  // combining kernel.
+  return swiglu_temp_bytes(M, N) + llmopt_q_linear_workspace_ex(M, N, K, bits, group_size, act_dtype);
 }
 
 int llmopt_q_linear_swiglu(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
@@ -397,7 +419,7 @@ int llmopt_q_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, co
     if (rc != LLMOPT_OK) return rc;
   }
   return run_linear(x, M, K, ldx, qweight, ldq, scales, zeros, bias, y, N, ldy, act_dtype, bits,
-                    group_size, symmetric, signed_codes, ws, ws ? kNoAllocScratchBytes : 0, stream,
+                    group_size, symmetric, signed_codes, ws, ws ? need : 0, stream,
                     LLMOPT_ALGO_AUTO, llmopt::kEpiNone);
 }
 

@@ -30,8 +30,24 @@ struct LinearArgs {
   // (fused rows 8p .. 8p+3 = gate features 4p .. 4p+3, rows 8p+4 .. 8p+7 = up features
   // 4p .. 4p+3) and y[m, 4p + r] = silu(gate) * up; y then has N / 2 columns.
   int epilogue;
+  // 1: y is fp32 and takes the sums unrounded (the fp32-activation path's products of its
+  // bf16 pieces); only the decode kernels and the K-split reduction take it, with no bias
+  // and no epilogue.
+  int out_f32;
 };
 enum : int { kEpiNone = 0, kEpiSwiglu = 1 };
+
+#ifdef __HIPCC__
+// Stores output element `idx` of a linear kernel: rounded to the activation dtype, or (out_f32)
+// the fp32 sum itself.
+template <class Act>
+__device__ __forceinline__ void put_y(const LinearArgs& a, int64_t idx, float v) {
+  if (a.out_f32)
+    static_cast<float*>(a.y)[idx] = v;
+  else
+    static_cast<typename Act::raw*>(a.y)[idx] = Act::store(v);
+}
+#endif
 
 // Each launcher returns hipSuccess or the launch error; `why` is set when the arguments do not
 // fit the kernel (then hipErrorInvalidValue is returned and nothing is launched).
@@ -153,5 +169,13 @@ size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, in
 bool ks_takes(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
 // Whether the decode path's N-split kernel takes this 33-64-token size (grids of >= 1024 tiles).
 bool nx_takes_wide(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
+// fp32 activations as three bf16 pieces per token on the decode kernels (chunks of up to 21
+// tokens), then a combining kernel; *fits is false when the workspace is smaller than
+// f32_workspace_bytes (the caller then takes the generic kernel).
+hipError_t launch_linear_f32_pieces(const LinearArgs& a, hipStream_t stream, bool* fits);
+// One or two fp32 tokens on the one-shot kernel with the split into pieces and their sum inside
+// it (no workspace); *fits is false for the shapes it does not take.
+hipError_t launch_linear_oneshot_f32(const LinearArgs& a, hipStream_t stream, bool* fits);
+size_t f32_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
 
 }  // namespace llmopt

@@ -256,7 +256,6 @@ __global__ void __launch_bounds__(NW * 64)
   __syncthreads();
 
   const Raw* bias = static_cast<const Raw*>(a.bias);
-  Raw* y = static_cast<Raw*>(a.y);
   for (int e = threadIdx.x; e < kElems; e += NW * 64) {
     float v = 0.0f;
 #pragma unroll
@@ -270,7 +269,7 @@ __global__ void __launch_bounds__(NW * 64)
     const int64_t n = n_base + 16 * t + (ln & 15);
     if (m < a.M && n < a.N) {
       if (bias) v += Act::load(bias[n]);
-      y[m * a.ldy + n] = Act::store(v);
+      put_y<Act>(a, m * a.ldy + n, v);
     }
   }
 }
@@ -511,7 +510,6 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4,
     }
   __syncthreads();
   const Raw* bias = static_cast<const Raw*>(a.bias);
-  Raw* y = static_cast<Raw*>(a.y);
   const int outs = NTT * M * 16;
   for (int e = tid; e < outs; e += kThreads) {
     float v = 0.0f;
@@ -523,7 +521,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4,
     const int64_t n = (tile0 + t) * 16 + (rem & 15);
     if (n < a.N) {
       if (bias) v += Act::load(bias[n]);
-      y[m * a.ldy + n] = Act::store(v);
+      put_y<Act>(a, m * a.ldy + n, v);
     }
   }
 }
@@ -558,15 +556,33 @@ struct OneShotGeom {
   }
 };
 
-template <class Act, int C, int MMAX, int RM, bool INTER = false>
+// GS: groups per 128-code step, 1 (groups of 128) or 2 (groups of 64). With two, each lane's
+// four code words are transposed across the four 16-lane rows of the wave (two permlane
+// swaps of each kind), so that MFMA e multiplies codes 32e .. 32e + 31 of the step -- within
+// group e / 2 -- and the step's two groups keep accumulators, activation sums and scales of
+// their own; the activation fragments are read in the matching order.
+// F32X: fp32 activations (a.x fp32, a.M tokens) taken as three bf16 pieces per token, rows 3m,
+// 3m + 1, 3m + 2 of the staged slice (hi, mid, lo: x = hi + mid + lo exactly), and each token's
+// output the fp32 sum of its three rows, (t_hi + t_mid) + t_lo + bias, stored in fp32 -- the
+// split and the sum of the fp32 path in one launch.
+// FMT = kByte: 8-bit codes, one per byte. Lane (col, kq) then loads 32 bytes of the step (two
+// 16-byte loads: codes 32kq .. 32kq + 31), and MFMA j takes the exact byte operand of codes
+// 32kq + 8j .. + 8 (bf16: the code itself; fp16: 1024 + code); signed codes are read with the
+// sign bit flipped and 128 added to the zero point. Groups of 128, 16-bit activations.
+template <class Act, int C, int MMAX, int RM, bool INTER = false, int GS = 1, bool F32X = false,
+          int FMT = kNibble>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)))
     decode_oneshot_kernel(const LinearArgs a) {
+  static_assert(GS == 1 || GS == 2, "one or two groups per step");
+  static_assert(!F32X || Act::id == kDtBf16, "fp32 pieces are bf16");
+  static_assert(FMT == kNibble || (GS == 1 && !F32X), "byte codes: groups of 128, 16-bit activations");
+  constexpr int kCB = FMT == kNibble ? 1 : 2;  // 16-byte code loads per lane and step
   using Geo = OneShotGeom<C, MMAX>;
   using Raw = typename Act::raw;
   constexpr int NM = 4;
 
   extern __shared__ u32x4 lds[];
-  const int M = int(a.M);
+  const int M = F32X ? 3 * int(a.M) : int(a.M);  // rows of the staged slice
   const int G = int(a.G);
   const int nw = int(blockDim.x) >> 6;
   const int tid = threadIdx.x;
@@ -602,21 +618,51 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
   const u32x4 sv = buf_load16(ms, mo, 0);  // past the end of the tensors: zeros
   const u32x4 zv = buf_load16(mz, mo, 0);
 
-  const Raw* xg = static_cast<const Raw*>(a.x) + int64_t(step0) * 128;
   u32x4 xv[Geo::kXPerLane];
+  if constexpr (F32X) {
+    // Piece (m % 3) of eight fp32 activations of token m / 3: two 16-byte loads.
+    const float* xg = static_cast<const float*>(a.x) + int64_t(step0) * 128;
 #pragma unroll
-  for (int e = 0; e < Geo::kXPerLane; ++e) {
-    int idx = lane + 64 * e;
-    idx = idx < M * C * 16 ? idx : 0;
-    const int m = idx / (C * 16);
-    const int c = idx - m * (C * 16);
-    xv[e] = *reinterpret_cast<const u32x4*>(xg + m * a.ldx + (c >> 4) * (sstride * 128) + 8 * (c & 15));
+    for (int e = 0; e < Geo::kXPerLane; ++e) {
+      int idx = lane + 64 * e;
+      idx = idx < M * C * 16 ? idx : 0;
+      const int m = idx / (C * 16);
+      const int c = idx - m * (C * 16);
+      const int tok = m / 3;
+      const int piece = m - 3 * tok;
+      const float* src = xg + tok * a.ldx + (c >> 4) * (sstride * 128) + 8 * (c & 15);
+      const f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
+      const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
+      const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      uint32_t h[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint16_t hi = f32_to_bf16_rne(v[j]);
+        const float r1 = v[j] - bf16_to_f32(hi);  // exact
+        const uint16_t mid = f32_to_bf16_rne(r1);
+        const uint16_t lo = f32_to_bf16_rne(r1 - bf16_to_f32(mid));  // exact remainder
+        h[j] = piece == 0 ? hi : piece == 1 ? mid : lo;
+      }
+      xv[e] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+  } else {
+    const Raw* xg = static_cast<const Raw*>(a.x) + int64_t(step0) * 128;
+#pragma unroll
+    for (int e = 0; e < Geo::kXPerLane; ++e) {
+      int idx = lane + 64 * e;
+      idx = idx < M * C * 16 ? idx : 0;
+      const int m = idx / (C * 16);
+      const int c = idx - m * (C * 16);
+      xv[e] = *reinterpret_cast<const u32x4*>(xg + m * a.ldx + (c >> 4) * (sstride * 128) + 8 * (c & 15));
+    }
   }
   const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
-  u32x4 w[C];
-  const uint32_t qoff = uint32_t(n * a.ldq + kq * 16);
+  u32x4 w[C][kCB];
+  const uint32_t qoff = uint32_t(n * a.ldq + kq * 16 * kCB);
 #pragma unroll
-  for (int i = 0; i < C; ++i) w[i] = buf_load16(wq, qoff, uint32_t(step0 + i * sstride) * 64);
+  for (int i = 0; i < C; ++i)
+#pragma unroll
+    for (int c = 0; c < kCB; ++c) w[i][c] = buf_load16(wq, qoff + 16 * c, uint32_t(step0 + i * sstride) * 64 * kCB);
 
   // ---- stage scales/zeros and this wave's activation slice in LDS ----
   if (meta_loader) {
@@ -630,7 +676,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
   // grows with the rows while one MFMA against a ones operand per fragment gives every lane its
   // rows' sums in the compute loop (measured on MI355X at three and four tokens: qkv 7.2 ->
   // 6.5-6.7 us, o 5.5 -> 5.2; at one token the staged sums stay 0.5-1 % ahead).
-  constexpr bool kMfmaSums = MMAX >= 2;
+  constexpr bool kMfmaSums = MMAX >= 2 || GS == 2;
   if constexpr (!kMfmaSums) {
 #pragma unroll
     for (int i = lane; i < C * 16; i += 64)
@@ -651,7 +697,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
       for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
     }
     if (idx < M * C * 16) {
-      xw[m * Geo::kRowPieces + c] = arrange<Act, kNibble>(xv[e]);
+      xw[m * Geo::kRowPieces + c] = arrange<Act, FMT>(xv[e]);
       if (!kMfmaSums && (c & 15) == 0) xsum[(c >> 4) * 16 + m] = sum;
     }
   }
@@ -659,18 +705,50 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
 
   // ---- compute ----
   const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
-  const float z_shift = Act::kNibbleOffset;
+  const bool flipped = FMT == kByte && a.signed_codes;
+  const uint32_t flip = flipped ? 0x80808080u : 0u;
+  const float z_shift = Codes<Act, FMT>::kOffset + (flipped ? 128.0f : 0.0f);
   const float z_const = a.zero_const + z_shift;
-  const u32x4* const xrow = col < M ? xw + col * Geo::kRowPieces + kq * NM : zero4;
+  // Lane (col, kq) reads activation pieces 4 kq + j of a step (GS = 1), or 4 j + kq (GS = 2:
+  // codes 32 j + 8 kq of the transposed words); rows past M read the zero pieces.
+  const u32x4* const xrow = col < M ? xw + col * Geo::kRowPieces + (GS == 1 ? kq * NM : kq) : zero4;
   const int xstep = col < M ? 4 * NM : 0;
-  const float* const srow = s_lds + col * mstride + step0;
-  const float* const zrow = z_lds + col * mstride + step0;
+  const int jstride = GS == 1 ? 1 : (col < M ? 4 : 0);
+  const float* const srow = s_lds + col * mstride + GS * step0;
+  const float* const zrow = z_lds + col * mstride + GS * step0;
   f32x4 tot = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < C; ++i) {
     u32x4 xa[NM];
 #pragma unroll
-    for (int j = 0; j < NM; ++j) xa[j] = xrow[i * xstep + j];
+    for (int j = 0; j < NM; ++j) xa[j] = xrow[i * xstep + j * jstride];
+    if constexpr (GS == 2) {
+      // One step's work at a time: hoisting the swaps and sums of later steps would keep their
+      // values live across the chunk and spill.
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
+      // Words of the step's codes, transposed: T[e] in row kq = word kq of row e.
+      const auto p02 = __builtin_amdgcn_permlane32_swap(w[i][0].x, w[i][0].z, false, false);
+      const auto p13 = __builtin_amdgcn_permlane32_swap(w[i][0].y, w[i][0].w, false, false);
+      const auto r01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+      const auto r23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+      const uint32_t tw[4] = {r01[0], r01[1], r23[0], r23[1]};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 2 * h; j < 2 * h + 2; ++j) {
+          v = Mfma16<Act>::run(xa[j], ones, v);
+          acc = Mfma16<Act>::run(xa[j], nib.operand(tw[j]), acc);
+        }
+        const float s = srow[2 * i * sstride + h];
+        const float zc = asym ? zrow[2 * i * sstride + h] + z_shift : z_const;
+#pragma unroll
+        for (int r = 0; r < RM; ++r) tot[r] = __builtin_fmaf(s, __builtin_fmaf(-zc, v[r], acc[r]), tot[r]);
+      }
+      continue;
+    }
     float xs[RM];
     if constexpr (kMfmaSums) {
       const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
@@ -689,10 +767,17 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
     }
     const float s = srow[i * sstride];
     const float zc = asym ? zrow[i * sstride] + z_shift : z_const;
-    const uint32_t words[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (FMT == kNibble) {
+      const uint32_t words[4] = {w[i][0].x, w[i][0].y, w[i][0].z, w[i][0].w};
 #pragma unroll
-    for (int j = 0; j < NM; ++j) acc = Mfma16<Act>::run(xa[j], nib.operand(words[j]), acc);
+      for (int j = 0; j < NM; ++j) acc = Mfma16<Act>::run(xa[j], nib.operand(words[j]), acc);
+    } else {
+      const uint32_t words[8] = {w[i][0].x, w[i][0].y, w[i][0].z, w[i][0].w,
+                                 w[i][1].x, w[i][1].y, w[i][1].z, w[i][1].w};
+#pragma unroll
+      for (int j = 0; j < NM; ++j) acc = Mfma16<Act>::run(xa[j], Codes<Act, kByte>::operand(words, j, flip), acc);
+    }
 #pragma unroll
     for (int r = 0; r < RM; ++r) tot[r] = __builtin_fmaf(s, __builtin_fmaf(-zc, xs[r], acc[r]), tot[r]);
   }
@@ -703,6 +788,29 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
 #pragma unroll
   for (int r = 0; r < RM; ++r) red[(wave * 4 + r) * 64 + lane] = tot[r];
   __syncthreads();
+  if constexpr (F32X) {
+    // Token m's three rows, each summed over the waves in order, then hi + mid + lo.
+    if (tid < 16 * int(a.M)) {
+      const int m = tid >> 4;
+      const int c = tid & 15;
+      float part[3];
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        const int row = 3 * m + p;
+        const int src_lane = c + 16 * (row >> 2);
+        float v = 0.0f;
+        for (int w2 = 0; w2 < nw; ++w2) v += red[(w2 * 4 + (row & 3)) * 64 + src_lane];
+        part[p] = v;
+      }
+      const int64_t nn = tile * 16 + c;
+      if (nn < a.N) {
+        float v = (part[0] + part[1]) + part[2];
+        if (a.bias) v += static_cast<const float*>(a.bias)[nn];
+        static_cast<float*>(a.y)[m * a.ldy + nn] = v;
+      }
+    }
+    return;
+  }
   if (tid < 16 * M) {
     const int m = tid >> 4;
     const int c = tid & 15;
@@ -719,7 +827,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
         if ((c & 4) == 0)
           static_cast<Raw*>(a.y)[m * a.ldy + (nn >> 3) * 4 + (c & 3)] = Act::store(swiglu<Act>(v, up));
       } else {
-        static_cast<Raw*>(a.y)[m * a.ldy + nn] = Act::store(v);
+        put_y<Act>(a, m * a.ldy + nn, v);
       }
     }
   }
@@ -948,7 +1056,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
         if ((c & 4) == 0)
           static_cast<Raw*>(a.y)[m * a.ldy + (nn >> 3) * 4 + (c & 3)] = Act::store(swiglu<Act>(v, up));
       } else {
-        static_cast<Raw*>(a.y)[m * a.ldy + nn] = Act::store(v);
+        put_y<Act>(a, m * a.ldy + nn, v);
       }
     }
   }
@@ -1224,7 +1332,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))
         const float up = __shfl_xor(v, 4, 64);
         if ((c & 4) == 0 && nn < a.N) y[m * a.ldy + (nn >> 3) * 4 + (c & 3)] = Act::store(swiglu<Act>(v, up));
       } else if (nn < a.N) {
-        y[m * a.ldy + nn] = Act::store(v);
+        put_y<Act>(a, m * a.ldy + nn, v);
       }
     }
   }
@@ -1256,9 +1364,14 @@ constexpr int kMtMetaPer = 2;  // 16-byte metadata pieces per thread of the mult
 
 // REFILL = false: every wave's whole range is in the ring at once (ns == D, checked on the
 // host), so all loads are issued up front and none is repeated past the end.
-template <class Act, int NT, int MB, int D, int NW, int WPE, bool REFILL = true>
+// GS = 2: groups of 64 codes, two per step. As in the one-shot kernel, the lane's code words are
+// transposed across the wave's four 16-lane rows so that MFMA e covers codes 32e .. 32e + 31 of
+// the step, within group 2 step + e / 2; lane (col, kq) then loads the activations of codes
+// 32e + 8kq (16 bytes at 64e + 16kq), and each group keeps its own sums and scale.
+template <class Act, int NT, int MB, int D, int NW, int WPE, bool REFILL = true, int GS = 1>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     decode_mt_kernel(const LinearArgs a, int ns, uint32_t group_magic) {
+  static_assert(GS == 1 || GS == 2, "one or two groups per step");
   using Raw = typename Act::raw;
   extern __shared__ u32x4 lds[];
   const int tid = threadIdx.x;
@@ -1306,7 +1419,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WP
   for (int mb = 0; mb < MB; ++mb) {
     const int64_t m = 16 * mb + col;
     // Token rows past M read past the end of x: the buffer returns zeros.
-    xoff[mb] = m < a.M ? uint32_t(m * a.ldx * 2 + 64 * kq) : xbytes;
+    xoff[mb] = m < a.M ? uint32_t(m * a.ldx * 2 + (GS == 1 ? 64 : 16) * kq) : xbytes;
   }
   const int s_begin = wave * ns;
 
@@ -1319,7 +1432,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WP
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) cx[slot][mb][j] = buf_load16(xr, xoff[mb] + 16 * j, uint32_t(step) * 256);
+      for (int j = 0; j < 4; ++j)
+        cx[slot][mb][j] = buf_load16(xr, xoff[mb] + (GS == 1 ? 16 : 64) * j, uint32_t(step) * 256);
   };
 #pragma unroll
   for (int r = 0; r < D; ++r) load(r, r);
@@ -1356,8 +1470,50 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WP
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) tot[t][mb] = zero4;
 
+  auto compute_two_groups = [&](int slot, int step) {
+    f32x2 sz[NT][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) sz[t][h] = sz_lds[(16 * t + col) * mstride + 2 * step + h];
+    u32x4 xa[MB][4];
+    f32x4 xs[MB][2];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xa[mb][j] = arrange<Act, kNibble>(cx[slot][mb][j]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        xs[mb][h] = Mfma16<Act>::run(xa[mb][2 * h + 1], ones, Mfma16<Act>::run(xa[mb][2 * h], ones, zero4));
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const u32x4 q = cw[slot][t];
+      // T[e] in row kq = word kq of row e: codes 32e + 8kq .. + 8 of the step.
+      const auto p02 = __builtin_amdgcn_permlane32_swap(q.x, q.z, false, false);
+      const auto p13 = __builtin_amdgcn_permlane32_swap(q.y, q.w, false, false);
+      const auto r01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+      const auto r23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+      const u32x4 b[4] = {nib.operand(r01[0]), nib.operand(r01[1]), nib.operand(r23[0]), nib.operand(r23[1])};
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const f32x4 acc =
+              Mfma16<Act>::run(xa[mb][2 * h + 1], b[2 * h + 1], Mfma16<Act>::run(xa[mb][2 * h], b[2 * h], zero4));
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            tot[t][mb][r] = __builtin_fmaf(sz[t][h][0], __builtin_fmaf(-sz[t][h][1], xs[mb][h][r], acc[r]),
+                                           tot[t][mb][r]);
+        }
+    }
+  };
   auto compute = [&](int slot, int i) {
     const int step = s_begin + i;
+    if constexpr (GS == 2) {
+      compute_two_groups(slot, step);
+      return;
+    }
     const int g = int(div_small(uint32_t(step), group_magic));
     f32x2 sz[NT];
 #pragma unroll
@@ -1433,7 +1589,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WP
         const float up = __shfl_xor(v, 4, 64);
         if ((n & 4) == 0) y[m * a.ldy + (n >> 3) * 4 + (n & 3)] = Act::store(swiglu<Act>(v, up));
       } else {
-        y[m * a.ldy + n] = Act::store(v);
+        put_y<Act>(a, m * a.ldy + n, v);
       }
     }
   }
@@ -1686,7 +1842,7 @@ __global__ void __launch_bounds__(NW * 64)
           if (m < a.M && nn < a.N && (nn & 4) == 0)
             y[m * a.ldy + (nn >> 3) * 4 + (nn & 3)] = Act::store(swiglu<Act>(v, up));
         } else if (m < a.M && nn < a.N) {
-          y[m * a.ldy + nn] = Act::store(v);
+          put_y<Act>(a, m * a.ldy + nn, v);
         }
       }
   }
@@ -1913,7 +2069,7 @@ __global__ void __launch_bounds__(kKrWaves * 64) decode_kr_kernel(const LinearAr
         // Gate rows 8p .. 8p+3 and up rows 8p+4 .. 8p+7 (N % 8 == 0).
         y[m * a.ldy + (n >> 3) * 4 + (n & 3)] = Act::store(swiglu<Act>(v[r] + bv, u[r] + bu));
       } else {
-        y[m * a.ldy + n] = Act::store(v[r] + bv);
+        put_y<Act>(a, m * a.ldy + n, v[r] + bv);
       }
     }
   }
@@ -2109,7 +2265,7 @@ __global__ void __launch_bounds__(NW * 64)
           const float up = __shfl_xor(v, 4, 64);
           if (n < a.N && (c & 4) == 0) y[m * a.ldy + (n >> 3) * 4 + (c & 3)] = Act::store(swiglu<Act>(v, up));
         } else if (n < a.N) {
-          y[m * a.ldy + n] = Act::store(v);
+          put_y<Act>(a, m * a.ldy + n, v);
         }
       }
     }
@@ -2229,10 +2385,10 @@ hipError_t launch_stream(const LinearArgs& a, int nw, int steps, int q, uint32_t
   return launch_stream_nw<Act, FMT, 4>(a, steps, q, magic, stream);
 }
 
-template <class Act, int C, int MMAX, int RM>
+template <class Act, int C, int MMAX, int RM, int GS, bool F32X = false, int FMT = kNibble>
 hipError_t launch_oneshot_cfg(const LinearArgs& a, int nw, hipStream_t stream) {
   const size_t lds = OneShotGeom<C, MMAX>::lds_bytes(nw, a.G);
-  auto kernel = decode_oneshot_kernel<Act, C, MMAX, RM>;
+  auto kernel = decode_oneshot_kernel<Act, C, MMAX, RM, false, GS, F32X, FMT>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
@@ -2242,27 +2398,37 @@ hipError_t launch_oneshot_cfg(const LinearArgs& a, int nw, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <class Act>
+template <class Act, int GS, int FMT = kNibble>
 hipError_t launch_oneshot(const LinearArgs& a, int c, int nw, hipStream_t stream) {
+  // (Two groups per step, or byte codes: no sixteen-step chunks, and no eight-step chunks at
+  // 3-4 rows; see try_oneshot.)
+  constexpr bool kLong = GS == 1 && FMT == kNibble;
   if (a.M == 1) {
-    if (c == 16) return launch_oneshot_cfg<Act, 16, 1, 1>(a, nw, stream);
-    if (c == 8) return launch_oneshot_cfg<Act, 8, 1, 1>(a, nw, stream);
-    return launch_oneshot_cfg<Act, 4, 1, 1>(a, nw, stream);
+    if constexpr (kLong) {
+      if (c == 16) return launch_oneshot_cfg<Act, 16, 1, 1, GS, false, FMT>(a, nw, stream);
+    }
+    if (c == 8) return launch_oneshot_cfg<Act, 8, 1, 1, GS, false, FMT>(a, nw, stream);
+    return launch_oneshot_cfg<Act, 4, 1, 1, GS, false, FMT>(a, nw, stream);
   }
-  if (a.M > 4) return launch_oneshot_cfg<Act, 4, 8, 4>(a, nw, stream);
+  if (a.M > 4) return launch_oneshot_cfg<Act, 4, 8, 4, GS, false, FMT>(a, nw, stream);
   // Two tokens: half the activation loads and accumulator rows of the four-token form; measured
   // on MI355X, qkv 7.09 -> 6.75 us, o 5.49 -> 5.34, down 12.67 -> 11.65, gate_up level.
   if (a.M == 2) {
-    if (c == 8) return launch_oneshot_cfg<Act, 8, 2, 2>(a, nw, stream);
-    return launch_oneshot_cfg<Act, 4, 2, 2>(a, nw, stream);
+    if (c == 8) return launch_oneshot_cfg<Act, 8, 2, 2, GS, false, FMT>(a, nw, stream);
+    return launch_oneshot_cfg<Act, 4, 2, 2, GS, false, FMT>(a, nw, stream);
   }
-  if (c == 8) return launch_oneshot_cfg<Act, 8, 4, 4>(a, nw, stream);
-  return launch_oneshot_cfg<Act, 4, 4, 4>(a, nw, stream);
+  if constexpr (kLong) {
+    if (c == 8) return launch_oneshot_cfg<Act, 8, 4, 4, GS, false, FMT>(a, nw, stream);
+  }
+  return launch_oneshot_cfg<Act, 4, 4, 4, GS, false, FMT>(a, nw, stream);
 }
 
-// M <= 8, 2/4-bit codes, group 128: the one-shot kernel (5-8 tokens in 4-step chunks only).
+// M <= 8, 2/4-bit codes in groups of 128 or 64, or 8-bit codes in groups of 128: the one-shot
+// kernel (5-8 tokens in 4-step chunks only).
 bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
-  if (a.fmt != kNibble || a.M > 8 || a.group != 128 || a.K % 128 != 0 || a.G % 4 != 0) return false;
+  const bool bytes = a.fmt == kByte;
+  if (a.M > 8 || a.K % 128 != 0 || a.G % 4 != 0) return false;
+  if (bytes ? a.group != 128 : (a.group != 128 && a.group != 64)) return false;
   if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
@@ -2282,11 +2448,45 @@ bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
     break;
   }
   if (chosen == 0) return false;
+  // Groups of 64 or byte codes with eight-step chunks at three or four rows, or sixteen-step
+  // chunks, exceed the 128 VGPRs of a wave here (other kernels take those shapes).
+  if ((a.group == 64 || bytes) && (chosen == 16 || (chosen == 8 && a.M > 2))) return false;
   const int nw = int(steps / chosen);
   if (16 * a.G / 4 > int64_t(nw) * 64) return false;  // one scale piece per thread
   if (16 * a.M > int64_t(nw) * 64) return false;      // one thread per output of the tile
-  *err = a.act == kDtBf16 ? launch_oneshot<ActBf16>(a, chosen, nw, stream)
-                          : launch_oneshot<ActF16>(a, chosen, nw, stream);
+  if (bytes)
+    *err = a.act == kDtBf16 ? launch_oneshot<ActBf16, 1, kByte>(a, chosen, nw, stream)
+                            : launch_oneshot<ActF16, 1, kByte>(a, chosen, nw, stream);
+  else if (a.group == 64)
+    *err = a.act == kDtBf16 ? launch_oneshot<ActBf16, 2>(a, chosen, nw, stream)
+                            : launch_oneshot<ActF16, 2>(a, chosen, nw, stream);
+  else
+    *err = a.act == kDtBf16 ? launch_oneshot<ActBf16, 1>(a, chosen, nw, stream)
+                            : launch_oneshot<ActF16, 1>(a, chosen, nw, stream);
+  return true;
+}
+
+// fp32 activations of one or two tokens, as three bf16 pieces each (three or six rows), on the
+// one-shot kernel with the split and the pieces' sum inside it: 4-step chunks, groups of 64 or
+// 128, 2/4-bit codes; y and bias fp32.
+bool try_oneshot_f32(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
+  if (a.act != kDtF32 || a.fmt != kNibble || a.M < 1 || a.M > 2 || a.epilogue != kEpiNone) return false;
+  if ((a.group != 128 && a.group != 64) || a.K % 128 != 0 || a.G % 4 != 0) return false;
+  if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 4 != 0) return false;
+  if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
+  const int64_t tiles = (a.N + 15) / 16;
+  if (tiles > 0x7FFFFFFF) return false;
+  const int64_t steps = a.K / 128;
+  if (steps % 4 != 0 || steps / 4 > 16) return false;
+  const int nw = int(steps / 4);
+  if (16 * a.G / 4 > int64_t(nw) * 64) return false;  // one scale piece per thread
+  if (a.M == 1)
+    *err = a.group == 64 ? launch_oneshot_cfg<ActBf16, 4, 4, 4, 2, true>(a, nw, stream)
+                         : launch_oneshot_cfg<ActBf16, 4, 4, 4, 1, true>(a, nw, stream);
+  else
+    *err = a.group == 64 ? launch_oneshot_cfg<ActBf16, 4, 8, 4, 2, true>(a, nw, stream)
+                         : launch_oneshot_cfg<ActBf16, 4, 8, 4, 1, true>(a, nw, stream);
   return true;
 }
 
@@ -2303,10 +2503,11 @@ hipError_t launch_line_cfg(const LinearArgs& a, int nw, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// One token only (try_line): the four-row forms would spill and are not instantiated.
 template <class Act, int NB, int D>
 hipError_t launch_line_m(const LinearArgs& a, int nw, hipStream_t stream) {
-  if (a.M == 1) return launch_line_cfg<Act, NB, D, 1, 1>(a, nw, stream);
-  return launch_line_cfg<Act, NB, D, 4, 4>(a, nw, stream);
+  if (a.M != 1) return hipErrorInvalidValue;
+  return launch_line_cfg<Act, NB, D, 1, 1>(a, nw, stream);
 }
 
 template <class Act>
@@ -2480,14 +2681,14 @@ struct MtConfig {
   bool refill = true;  // false: each wave's whole range is loaded up front (steps == d * nw)
 };
 
-template <class Act, int NT, int MB, int D, int NW, int WPE, bool REFILL = true>
+template <class Act, int NT, int MB, int D, int NW, int WPE, bool REFILL, int GS>
 hipError_t launch_mt_cfg(const LinearArgs& a, int steps, uint32_t magic, hipStream_t stream) {
   if (!REFILL && steps != D * NW) return hipErrorInvalidValue;
   const int64_t blocks = (a.N + 16 * NT - 1) / (16 * NT);
   const size_t meta = size_t(16) * NT * (a.G + 2) * 8;
   const size_t red = size_t(NW) * NT * MB * 4 * 64 * 4;
   const size_t lds = meta > red ? meta : red;
-  auto kern = decode_mt_kernel<Act, NT, MB, D, NW, WPE, REFILL>;
+  auto kern = decode_mt_kernel<Act, NT, MB, D, NW, WPE, REFILL, GS>;
   if (lds > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
@@ -2497,17 +2698,20 @@ hipError_t launch_mt_cfg(const LinearArgs& a, int steps, uint32_t magic, hipStre
   return hipGetLastError();
 }
 
-// The instantiated configurations; `pick_mt` chooses among them.
-template <class Act>
+// The instantiated configurations; `pick_mt` chooses among them. GS: groups per step.
+template <class Act, int GS>
 hipError_t launch_mt(const LinearArgs& a, MtConfig c, int steps, uint32_t magic, hipStream_t stream) {
 #define LLMOPT_MT(NT, MB, D, NW, WPE, R)                                                     \
   if (c.nt == NT && c.mb == MB && c.d == D && c.nw == NW && c.refill == R)                   \
-    return launch_mt_cfg<Act, NT, MB, D, NW, WPE, R>(a, steps, magic, stream);
+    return launch_mt_cfg<Act, NT, MB, D, NW, WPE, R, GS>(a, steps, magic, stream);
   LLMOPT_MT(8, 1, 2, 8, 2, true)
   LLMOPT_MT(2, 1, 4, 8, 2, true)
   LLMOPT_MT(1, 1, 4, 8, 4, true)
   LLMOPT_MT(4, 2, 2, 4, 2, true)
-  LLMOPT_MT(2, 4, 2, 8, 2, true)
+  // Four token blocks with two groups per step would spill inside the main loop.
+  if constexpr (GS == 1) {
+    LLMOPT_MT(2, 4, 2, 8, 2, true)
+  }
   LLMOPT_MT(2, 1, 2, 16, 2, false)
   LLMOPT_MT(1, 2, 4, 8, 2, false)
   LLMOPT_MT(2, 2, 2, 2, 2, true)
@@ -2741,30 +2945,50 @@ bool try_kr(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   return true;
 }
 
-// M <= 64, 2/4-bit codes, groups of a multiple of 128 codes: the multi-tile kernel.
+// M <= 64, 2/4-bit codes, groups of 64 or a multiple of 128 codes: the multi-tile kernel.
 bool try_mt(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.fmt != kNibble || a.M < 1 || a.M > 64) return false;
   if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
-  if (a.group % 128 != 0 || a.K % 128 != 0 || a.G % 4 != 0) return false;
+  const bool g64 = a.group == 64;
+  if ((a.group % 128 != 0 && !g64) || a.K % 128 != 0 || a.G % 4 != 0) return false;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
   if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
   if (a.M * a.ldx * 2 >= (int64_t(1) << 31) || a.K * 2 >= (int64_t(1) << 31)) return false;
   if ((a.N + 15) / 16 > 0x7FFFFFFF) return false;
   const int64_t steps = a.K / 128;
-  const uint32_t per_group = uint32_t(a.group / 128);
+  const uint32_t per_group = g64 ? 1u : uint32_t(a.group / 128);
   const uint32_t magic = per_group == 1 ? 0u
       : uint32_t((uint64_t(1) << 32) / per_group + ((uint64_t(1) << 32) % per_group != 0));
-  if (a.act == kDtBf16 ? try_nx<ActBf16>(a, steps, magic, stream, err)
-                       : try_nx<ActF16>(a, steps, magic, stream, err))
+  if (!g64 && (a.act == kDtBf16 ? try_nx<ActBf16>(a, steps, magic, stream, err)
+                                : try_nx<ActF16>(a, steps, magic, stream, err)))
     return true;
-  const MtConfig c = pick_mt(a, steps);
-  if (c.nt == 0 || steps % c.nw != 0) return false;
   // The metadata block of the workgroup must fit in LDS, and its loads in two per thread.
-  if (size_t(16) * c.nt * (a.G + 2) * 8 > 160 * 1024) return false;
-  if (int64_t(16) * c.nt * a.G / 4 > int64_t(kMtMetaPer) * c.nw * 64) return false;
-  *err = a.act == kDtBf16 ? launch_mt<ActBf16>(a, c, int(steps), magic, stream)
-                          : launch_mt<ActF16>(a, c, int(steps), magic, stream);
+  auto fits = [&](const MtConfig& c) {
+    if (c.nt == 0 || steps % c.nw != 0 || (!c.refill && steps != int64_t(c.d) * c.nw)) return false;
+    if (size_t(16) * c.nt * (a.G + 2) * 8 > 160 * 1024) return false;
+    return int64_t(16) * c.nt * a.G / 4 <= int64_t(kMtMetaPer) * c.nw * 64;
+  };
+  MtConfig c = pick_mt(a, steps);
+  if (g64 && !fits(c)) {
+    // Groups of 64 have twice the metadata per row, and no streaming kernel takes them: the
+    // configurations of the same token blocks with fewer tiles per workgroup, in turn.
+    const MtConfig alt[] = {MtConfig{2, 1, 4, 8}, MtConfig{1, 1, 4, 8}, MtConfig{1, 2, 4, 8, false}};
+    const int mb = a.M <= 16 ? 1 : a.M <= 32 ? 2 : 4;
+    c = MtConfig{0, mb, 0, 0};
+    for (const MtConfig& t : alt)
+      if (t.mb == mb && fits(t)) {
+        c = t;
+        break;
+      }
+  }
+  if (!fits(c) || (g64 && c.mb > 2)) return false;  // 33-64 tokens in groups of 64: the skinny kernel
+  if (g64)
+    *err = a.act == kDtBf16 ? launch_mt<ActBf16, 2>(a, c, int(steps), magic, stream)
+                            : launch_mt<ActF16, 2>(a, c, int(steps), magic, stream);
+  else
+    *err = a.act == kDtBf16 ? launch_mt<ActBf16, 1>(a, c, int(steps), magic, stream)
+                            : launch_mt<ActF16, 1>(a, c, int(steps), magic, stream);
   return true;
 }
 
@@ -2809,6 +3033,12 @@ hipError_t launch_skinny(const LinearArgs& a, hipStream_t stream, bool* fits) {
 
 
 }  // namespace
+
+hipError_t launch_linear_oneshot_f32(const LinearArgs& a, hipStream_t stream, bool* fits) {
+  hipError_t err = hipSuccess;
+  *fits = try_oneshot_f32(a, stream, &err);
+  return err;
+}
 
 bool ks_takes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   return plan_ks(M, N, K, group, bits).slices > 0;

@@ -521,7 +521,6 @@ __global__ void __launch_bounds__(kReduceThreads) splitk_reduce_kernel(const Lin
   const int64_t n = (e - m * n4) * 4;
   const size_t plane = size_t(a.M) * a.N;
   const Raw* bias = static_cast<const Raw*>(a.bias);
-  Raw* y = static_cast<Raw*>(a.y) + m * a.ldy;
   const float* p = partials + size_t(m) * a.N + n;
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   if (n + 3 < a.N && a.N % 4 == 0) {
@@ -549,7 +548,7 @@ __global__ void __launch_bounds__(kReduceThreads) splitk_reduce_kernel(const Lin
     if (n + r >= a.N) break;
     float o = v[r];
     if (bias) o += Act::load(bias[n + r]);
-    y[n + r] = Act::store(o);
+    put_y<Act>(a, m * a.ldy + n + r, o);
   }
 }
 

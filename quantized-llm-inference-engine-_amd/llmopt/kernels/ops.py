@@ -240,7 +240,9 @@ def quant_linear(
         lib = load_library()
         # Scratch for split-K partial sums (only some prefill shapes use it); it comes from
         # torch's caching allocator, so repeated calls reuse the same block.
-        ws_bytes = int(lib.llmopt_q_linear_workspace(m, rows, cols, int(qt.bits), group))
+        ws_bytes = int(
+            lib.llmopt_q_linear_workspace_ex(m, rows, cols, int(qt.bits), group, DTYPE_CODES[compute_dtype])
+        )
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
         call(
             lib.llmopt_q_linear_ex(
@@ -317,7 +319,9 @@ def quant_linear_swiglu(
         if bias is not None:
             bias = bias.contiguous()
         lib = load_library()
-        ws_bytes = int(lib.llmopt_q_linear_swiglu_workspace(m, rows, cols, int(qt.bits), group))
+        ws_bytes = int(
+            lib.llmopt_q_linear_swiglu_workspace_ex(m, rows, cols, int(qt.bits), group, DTYPE_CODES[compute_dtype])
+        )
         for _attempt in range(2):
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
             rc = lib.llmopt_q_linear_swiglu(
@@ -333,7 +337,7 @@ def quant_linear_swiglu(
             # A kernel without the fused activation ran into a short workspace (an unusual
             # alignment): give it room for the full product and try once more.
             ws_bytes = (m * rows * 4 + 255) // 256 * 256 + int(
-                lib.llmopt_q_linear_workspace(m, rows, cols, int(qt.bits), group)
+                lib.llmopt_q_linear_workspace_ex(m, rows, cols, int(qt.bits), group, DTYPE_CODES[compute_dtype])
             )
         call(rc, "llmopt_q_linear_swiglu")
     return y.reshape(*lead_shape, out)

@@ -484,6 +484,75 @@ def test_wide_grids_at_33_to_64_tokens_every_format(m, bits, group):
     assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= 1e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 12, 16, 24, 32, 40, 64])
+@pytest.mark.parametrize("n, k, bits, symmetric, with_bias", [
+    (6144, 4096, 4, True, False), (28672, 4096, 4, True, False), (4100, 4096, 4, False, True),
+    (4096, 14336, 4, True, False), (1000, 2048, 2, False, True)])
+def test_linear_groups_of_64(dtype, m, n, k, bits, symmetric, with_bias):
+    # Groups of 64 codes (the reference engine's quantize_model_(bits=4, group_size=64),
+    # src/llmopt/engine/llm_engine.py:258-264): two groups per 128-code step on the one-shot
+    # (M <= 8) and multi-tile (M <= 32) decode kernels, with the code words transposed across
+    # the wave's rows; ragged N, bias, 2-bit codes, long rows; 33-64 tokens on the skinny kernel.
+    qt = _host_qt(n, k, bits, 64, symmetric, seed=m + n + k)
+    gen = torch.Generator().manual_seed(m)
+    x = torch.randn(m, k, generator=gen).to(dtype)
+    bias = torch.randn(n, generator=gen).to(dtype) if with_bias else None
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None if bias is None else bias.to(DEV), dtype)
+    cols = np.sort(np.random.default_rng(m + k).choice(n, size=min(n, 256), replace=False))
+    ref = _reference_linear(x, _oracle_dense(qt), bias, dtype, cols=cols)
+    assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 32])
+def test_groups_of_64_one_hot_rows_return_weight_columns(m):
+    # One-hot activation rows return the dequantized weight's columns bit for bit: every other
+    # group and step adds exactly zero, and s * ((OFF + q) - (OFF + z)) rounds (q - z) * s once.
+    n, k = 6144, 4096
+    qt = _host_qt(n, k, 4, 64, False, seed=m)
+    dense = _oracle_dense(qt)
+    picks = np.random.default_rng(k + m).choice(k, size=m, replace=False)
+    x = torch.zeros(m, k, dtype=torch.bfloat16)
+    x[torch.arange(m), torch.from_numpy(picks)] = 1.0
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None, torch.bfloat16)
+    expect = qo.bf16_bits(np.ascontiguousarray(dense[:, picks].T)).view(np.int16)
+    np.testing.assert_array_equal(_bits_of(y), expect)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("n, k, symmetric, with_bias", [
+    (6144, 4096, False, False), (4100, 4096, True, True), (4096, 14336, False, False), (4096, 14336, True, False)])
+def test_linear_byte_codes_decode(dtype, m, n, k, symmetric, with_bias):
+    # 8-bit codes (uint8 asymmetric, int8 symmetric, quantizers.py:231-234) at 1-8 tokens: the
+    # one-shot kernel's byte form (32 bytes per lane and step) where it fits, the streaming
+    # kernel for the rest; ragged N, bias, long rows.
+    qt = _host_qt(n, k, 8, 128, symmetric, seed=m + n + k)
+    gen = torch.Generator().manual_seed(m)
+    x = torch.randn(m, k, generator=gen).to(dtype)
+    bias = torch.randn(n, generator=gen).to(dtype) if with_bias else None
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None if bias is None else bias.to(DEV), dtype)
+    cols = np.sort(np.random.default_rng(m + k).choice(n, size=256, replace=False))
+    ref = _reference_linear(x, _oracle_dense(qt), bias, dtype, cols=cols)
+    assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("symmetric", [False, True])
+@pytest.mark.parametrize("m", [1, 2])
+def test_byte_codes_one_hot_rows_return_weight_columns(symmetric, m):
+    # Byte operands are the codes themselves (bf16): a one-hot row returns (q - z) * s rounded
+    # once, then to bf16, bit for bit.
+    n, k = 4096, 14336
+    qt = _host_qt(n, k, 8, 128, symmetric, seed=m + 40)
+    dense = _oracle_dense(qt)
+    picks = np.random.default_rng(k + m).choice(k, size=m, replace=False)
+    x = torch.zeros(m, k, dtype=torch.bfloat16)
+    x[torch.arange(m), torch.from_numpy(picks)] = 1.0
+    y = ops.quant_linear(x.to(DEV), _to_device(qt), None, torch.bfloat16)
+    expect = qo.bf16_bits(np.ascontiguousarray(dense[:, picks].T)).view(np.int16)
+    np.testing.assert_array_equal(_bits_of(y), expect)
+
+
 def _unusual_metadata_qt():
     """W4 g128 weights whose metadata leaves what the quantizers produce: fractional and
     negative zero points, zero points of 16, scales of 2^100 and 2^121."""
