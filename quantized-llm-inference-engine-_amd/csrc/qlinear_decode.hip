@@ -859,9 +859,9 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int NB, int D, int MMAX>
+template <int NB, int D, int MMAX, int SPB = 2>
 struct LineGeom {
-  static constexpr int kSteps = 2 * NB;                      // 128-code steps per wave
+  static constexpr int kSteps = SPB * NB;                    // 128-code steps per wave
   static constexpr int kStepPieces = 16;                     // 16-byte x pieces per row and step
   static constexpr int kRowPieces = kSteps * kStepPieces + 1;  // padded LDS row of a wave's slice
   static constexpr int kWavePieces = MMAX * kRowPieces + 4;  // + four zero pieces
@@ -879,13 +879,17 @@ struct LineGeom {
   }
 };
 
-template <class Act, int NB, int D, int MMAX, int RM>
+// FMT = kByte: 8-bit codes. A block of 128 bytes per row is then one 128-code step, and lane
+// (col, kq) reads its 32 codes of the step as chunks 2kq and 2kq + 1 of row col; the byte
+// operands, flipped signs and zero-point offset are the one-shot kernel's.
+template <class Act, int NB, int D, int MMAX, int RM, int FMT = kNibble>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)))
     decode_line_kernel(const LinearArgs a) {
-  using Geo = LineGeom<NB, D, MMAX>;
+  constexpr int SPB = FMT == kNibble ? 2 : 1;  // 128-code steps per block
+  using Geo = LineGeom<NB, D, MMAX, SPB>;
   using Raw = typename Act::raw;
   constexpr int NM = 4;
-  constexpr int C = 2 * NB;
+  constexpr int C = SPB * NB;
 
   extern __shared__ u32x4 lds[];
   const int M = int(a.M);
@@ -975,7 +979,7 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
     if (idx < M * C * 16) {
-      xw[m * Geo::kRowPieces + c] = arrange<Act, kNibble>(xv[e]);
+      xw[m * Geo::kRowPieces + c] = arrange<Act, FMT>(xv[e]);
       if ((c & 15) == 0) xsum[(c >> 4) * 16 + m] = sum;
     }
   }
@@ -987,17 +991,22 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
 
   // ---- compute, block by block as the ring fills ----
   const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
-  const float z_shift = Act::kNibbleOffset;
+  const bool flipped = FMT == kByte && a.signed_codes;
+  const uint32_t flip = flipped ? 0x80808080u : 0u;
+  const float z_shift = Codes<Act, FMT>::kOffset + (flipped ? 128.0f : 0.0f);
   const float z_const = a.zero_const + z_shift;
   const u32x4* const xrow = col < M ? xw + col * Geo::kRowPieces + kq * NM : zero4;
   const int xstep = col < M ? 4 * NM : 0;
   const float* const srow = s_lds + col * mstride + step0;
   const float* const zrow = z_lds + col * mstride + step0;
-  // Byte offset, within a block, of chunk 4h + kq of row col.
+  // Byte offset, within a block, of chunk 4h + kq of row col (nibbles: step h of the block), or
+  // of chunk 2kq + h (bytes: half h of the lane's 32 codes of the block's one step).
   uint32_t rd_off[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
-    rd_off[h] = uint32_t((col >> 3) * 1024 + ((col & 7) * 8 + ((4 * h + kq) ^ (col & 7))) * 16);
+  for (int h = 0; h < 2; ++h) {
+    const int chunk = FMT == kNibble ? 4 * h + kq : 2 * kq + h;
+    rd_off[h] = uint32_t((col >> 3) * 1024 + ((col & 7) * 8 + (chunk ^ (col & 7))) * 16);
+  }
   f32x4 tot = {0.f, 0.f, 0.f, 0.f};
   static_for<NB>([&](auto IB) {
     constexpr int ib = decltype(IB)::value;
@@ -1005,9 +1014,10 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
     wait_vmcnt<after>();
     const uint8_t* blk = ring + (ib % D) * 2048;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = 2 * ib + h;
+    for (int h = 0; h < SPB; ++h) {
+      const int i = SPB * ib + h;
       const u32x4 w = *reinterpret_cast<const u32x4*>(blk + rd_off[h]);
+      const u32x4 w2 = FMT == kByte ? *reinterpret_cast<const u32x4*>(blk + rd_off[1]) : w;
       u32x4 xa[NM];
 #pragma unroll
       for (int j = 0; j < NM; ++j) xa[j] = xrow[i * xstep + j];
@@ -1021,10 +1031,17 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
       }
       const float sc = srow[i];
       const float zc = asym ? zrow[i] + z_shift : z_const;
-      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (FMT == kNibble) {
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int j = 0; j < NM; ++j) acc = Mfma16<Act>::run(xa[j], nib.operand(words[j]), acc);
+        for (int j = 0; j < NM; ++j) acc = Mfma16<Act>::run(xa[j], nib.operand(words[j]), acc);
+      } else {
+        const uint32_t words[8] = {w.x, w.y, w.z, w.w, w2.x, w2.y, w2.z, w2.w};
+#pragma unroll
+        for (int j = 0; j < NM; ++j)
+          acc = Mfma16<Act>::run(xa[j], Codes<Act, kByte>::operand(words, j, flip), acc);
+      }
 #pragma unroll
       for (int r = 0; r < RM; ++r) tot[r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], acc[r]), tot[r]);
     }
@@ -2490,10 +2507,10 @@ bool try_oneshot_f32(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   return true;
 }
 
-template <class Act, int NB, int D, int MMAX, int RM>
+template <class Act, int NB, int D, int MMAX, int RM, int FMT>
 hipError_t launch_line_cfg(const LinearArgs& a, int nw, hipStream_t stream) {
-  const size_t lds = LineGeom<NB, D, MMAX>::lds_bytes(nw, a.G);
-  auto kernel = decode_line_kernel<Act, NB, D, MMAX, RM>;
+  const size_t lds = LineGeom<NB, D, MMAX, FMT == kNibble ? 2 : 1>::lds_bytes(nw, a.G);
+  auto kernel = decode_line_kernel<Act, NB, D, MMAX, RM, FMT>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
@@ -2504,18 +2521,17 @@ hipError_t launch_line_cfg(const LinearArgs& a, int nw, hipStream_t stream) {
 }
 
 // One token only (try_line): the four-row forms would spill and are not instantiated.
-template <class Act, int NB, int D>
+template <class Act, int NB, int D, int FMT>
 hipError_t launch_line_m(const LinearArgs& a, int nw, hipStream_t stream) {
   if (a.M != 1) return hipErrorInvalidValue;
-  return launch_line_cfg<Act, NB, D, 1, 1>(a, nw, stream);
+  return launch_line_cfg<Act, NB, D, 1, 1, FMT>(a, nw, stream);
 }
 
-template <class Act>
+template <class Act, int FMT>
 hipError_t launch_line(const LinearArgs& a, int nb, int d, int nw, hipStream_t stream) {
-  if (nb == 2) return launch_line_m<Act, 2, 2>(a, nw, stream);
-  if (nb == 4) return d == 4 ? launch_line_m<Act, 4, 4>(a, nw, stream) : launch_line_m<Act, 4, 2>(a, nw, stream);
-  if (nb == 8) return d == 4 ? launch_line_m<Act, 8, 4>(a, nw, stream) : launch_line_m<Act, 8, 2>(a, nw, stream);
-  return d == 4 ? launch_line_m<Act, 16, 4>(a, nw, stream) : launch_line_m<Act, 16, 2>(a, nw, stream);
+  if (nb == 2) return launch_line_m<Act, 2, 2, FMT>(a, nw, stream);
+  if (nb == 4) return d == 4 ? launch_line_m<Act, 4, 4, FMT>(a, nw, stream) : launch_line_m<Act, 4, 2, FMT>(a, nw, stream);
+  return d == 4 ? launch_line_m<Act, 8, 4, FMT>(a, nw, stream) : launch_line_m<Act, 8, 2, FMT>(a, nw, stream);
 }
 
 // One token, 2/4-bit codes, group 128, rows of at least 8192 codes: the line-streaming kernel.
@@ -2523,13 +2539,15 @@ hipError_t launch_line(const LinearArgs& a, int nb, int d, int nw, hipStream_t s
 // on K = 4096 the two are within 2 %, and at 2-4 tokens the one-shot kernel leads.
 bool try_line(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.M != 1 || a.K < 8192) return false;
-  if (a.fmt != kNibble || a.M > 4 || a.group != 128 || a.K % 256 != 0 || a.G % 4 != 0) return false;
+  const bool bytes = a.fmt == kByte;
+  const int64_t block_k = bytes ? 128 : 256;  // codes per block of 128 bytes per row
+  if (a.group != 128 || a.K % block_k != 0 || a.G % 4 != 0) return false;
   if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
   if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
   if ((a.N + 15) / 16 > 0x7FFFFFFF) return false;
-  const int64_t blocks = a.K / 256;
+  const int64_t blocks = a.K / block_k;
   // Blocks per wave: the fewest that keep a tile within 16 waves (short runs spread the
   // per-wave arithmetic over more waves, which finish as their data lands).
   int nb = 0;
@@ -2543,20 +2561,27 @@ bool try_line(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   const int nw = int(blocks / nb);
   if (16 * a.G / 4 > int64_t(nw) * 64) return false;  // one scale piece per thread
   // Ring depth: every block of the wave up front when LDS allows, else two.
-  const int mmax = a.M == 1 ? 1 : 4;
-  auto lds_for = [&](int d) {
-    if (mmax == 1) {
-      if (nb == 2) return LineGeom<2, 2, 1>::lds_bytes(nw, a.G);
-      if (nb == 4) return d == 4 ? LineGeom<4, 4, 1>::lds_bytes(nw, a.G) : LineGeom<4, 2, 1>::lds_bytes(nw, a.G);
-      return d == 4 ? LineGeom<8, 4, 1>::lds_bytes(nw, a.G) : LineGeom<8, 2, 1>::lds_bytes(nw, a.G);
-    }
-    if (nb == 2) return LineGeom<2, 2, 4>::lds_bytes(nw, a.G);
-    return d == 4 ? LineGeom<4, 4, 4>::lds_bytes(nw, a.G) : LineGeom<4, 2, 4>::lds_bytes(nw, a.G);
+  auto lds_geo = [&](auto geo_nb, auto geo_d) -> size_t {
+    constexpr int kNb = decltype(geo_nb)::value, kD = decltype(geo_d)::value;
+    return bytes ? LineGeom<kNb, kD, 1, 1>::lds_bytes(nw, a.G) : LineGeom<kNb, kD, 1, 2>::lds_bytes(nw, a.G);
+  };
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
+  using I8 = std::integral_constant<int, 8>;
+  auto lds_for = [&](int d) -> size_t {
+    if (nb == 2) return lds_geo(I2{}, I2{});
+    if (nb == 4) return d == 4 ? lds_geo(I4{}, I4{}) : lds_geo(I4{}, I2{});
+    return d == 4 ? lds_geo(I8{}, I4{}) : lds_geo(I8{}, I2{});
   };
   int d = nb == 2 ? 2 : 4;
   if (lds_for(d) > 96 * 1024) d = 2;
   if (lds_for(d) > 160 * 1024) return false;
-  *err = a.act == kDtBf16 ? launch_line<ActBf16>(a, nb, d, nw, stream) : launch_line<ActF16>(a, nb, d, nw, stream);
+  if (bytes)
+    *err = a.act == kDtBf16 ? launch_line<ActBf16, kByte>(a, nb, d, nw, stream)
+                            : launch_line<ActF16, kByte>(a, nb, d, nw, stream);
+  else
+    *err = a.act == kDtBf16 ? launch_line<ActBf16, kNibble>(a, nb, d, nw, stream)
+                            : launch_line<ActF16, kNibble>(a, nb, d, nw, stream);
   return true;
 }
 
