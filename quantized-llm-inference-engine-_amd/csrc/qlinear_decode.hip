@@ -2130,9 +2130,13 @@ struct KsGeom {
   static constexpr size_t lds_bytes() { return ring_bytes() + red_bytes() + xt_bytes(); }
 };
 
-template <class Act, int NW, int R, int MB>
+// FMT = kByte: 8-bit codes; a block of 128 bytes per row is one 128-code step (a slice of NW
+// blocks covers 1024 codes), lane (col, kq) reads chunks 2kq and 2kq + 1 of its row, and the
+// byte operands, flipped signs and zero-point offset are the one-shot kernel's.
+template <class Act, int NW, int R, int MB, int FMT = kNibble>
 __global__ void __launch_bounds__(NW * 64)
     decode_ks_kernel(const LinearArgs a, int per_slice, uint32_t group_magic, float* partials) {
+  constexpr int SPB = FMT == kNibble ? 2 : 1;  // 128-code steps per block
   using Geo = KsGeom<NW, R, MB>;
   using Raw = typename Act::raw;
   constexpr int kLoadsPerTile = 4;
@@ -2149,13 +2153,13 @@ __global__ void __launch_bounds__(NW * 64)
   const int64_t tiles = (a.N + 15) / 16;
   if (first >= tiles) return;  // the host sizes the grid so that this does not happen
   const int ntiles = int((tiles - first + per_slice - 1) / per_slice);
-  const int blk = slice * NW + wave;  // this wave's block of 256 codes
+  const int blk = slice * NW + wave;  // this wave's block of 128 bytes per row
   uint8_t* const ring = base + size_t(wave) * R * Geo::kSlot;
   float* const red = reinterpret_cast<float*>(base + Geo::ring_bytes());
 
   // ---- the wave's activations, in whole lines: steps 2 b and 2 b + 1 of every token block ----
-  u32x4 xa[2][MB][4];
-  load_x_lines<2, MB>(xa, a, int64_t(blk) * 2);
+  u32x4 xa[SPB][MB][4];
+  load_x_lines<SPB, MB>(xa, a, int64_t(blk) * SPB);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- direct-to-LDS loads of tile j's block into slot j % R ----
@@ -2164,7 +2168,7 @@ __global__ void __launch_bounds__(NW * 64)
   const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_total);
   // Metadata: lane l loads row l % 16 of step (l / 16) % 2 of the block (lanes 32..63 repeat
   // lanes 0..31), landing at float l of the slot's scale (zero) area.
-  const uint32_t mgroup = div_small(uint32_t(2 * blk + ((lane >> 4) & 1)), group_magic);
+  const uint32_t mgroup = div_small(uint32_t(SPB * blk + (SPB == 2 ? (lane >> 4) & 1 : 0)), group_magic);
   const uint32_t meta_lane = (uint32_t(lane & 15) * uint32_t(a.G) + mgroup) * 4;
   const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
   const int r8 = lane >> 3;
@@ -2196,29 +2200,34 @@ __global__ void __launch_bounds__(NW * 64)
   // ---- activations into operand order (lane (col, kq), step i, token block mb, MFMA j takes
   //      x[16 mb + col][256 b + 128 i + 32 kq + 8 j .. + 8]), and their per-step sums (one MFMA
   //      chain against ones) ----
-  lines_to_fragments<2, MB>(xa, base + Geo::ring_bytes() + Geo::red_bytes() + size_t(wave) * kXTileBytes);
+  lines_to_fragments<SPB, MB>(xa, base + Geo::ring_bytes() + Geo::red_bytes() + size_t(wave) * kXTileBytes);
   const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  f32x4 xs[2][MB];
+  f32x4 xs[SPB][MB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < SPB; ++i)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xa[i][mb][j] = arrange<Act, kNibble>(xa[i][mb][j]);
+      for (int j = 0; j < 4; ++j) xa[i][mb][j] = arrange<Act, FMT>(xa[i][mb][j]);
       xs[i][mb] = Mfma16<Act>::run(xa[i][mb][0], ones, zero4);
 #pragma unroll
       for (int j = 1; j < 4; ++j) xs[i][mb] = Mfma16<Act>::run(xa[i][mb][j], ones, xs[i][mb]);
     }
 
   const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
-  const float z_shift = Act::kNibbleOffset;
+  const bool flipped = FMT == kByte && a.signed_codes;
+  const uint32_t flip = flipped ? 0x80808080u : 0u;
+  const float z_shift = Codes<Act, FMT>::kOffset + (flipped ? 128.0f : 0.0f);
   const float z_const = a.zero_const + z_shift;
-  // Byte offset, within a block, of chunk 4i + kq of row col.
+  // Byte offset, within a block, of chunk 4i + kq of row col (nibbles: step i of the block), or
+  // of chunk 2kq + i (bytes: half i of the lane's 32 codes of the block's one step).
   uint32_t rd_off[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-    rd_off[i] = uint32_t((col >> 3) * 1024 + ((col & 7) * 8 + ((4 * i + kq) ^ (col & 7))) * 16);
+  for (int i = 0; i < 2; ++i) {
+    const int chunk = FMT == kNibble ? 4 * i + kq : 2 * kq + i;
+    rd_off[i] = uint32_t((col >> 3) * 1024 + ((col & 7) * 8 + (chunk ^ (col & 7))) * 16);
+  }
   const Raw* bias = static_cast<const Raw*>(a.bias);
   Raw* y = static_cast<Raw*>(a.y);
   const int M = int(a.M);
@@ -2237,11 +2246,22 @@ __global__ void __launch_bounds__(NW * 64)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) tot[mb] = zero4;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < SPB; ++i) {
       const u32x4 w = *reinterpret_cast<const u32x4*>(slot + rd_off[i]);
       const float sc = sm[16 * i + col];
       const float zc = asym ? sm[64 + 16 * i + col] + z_shift : z_const;
-      const u32x4 b[4] = {nib.operand(w.x), nib.operand(w.y), nib.operand(w.z), nib.operand(w.w)};
+      u32x4 b[4];
+      if constexpr (FMT == kNibble) {
+        b[0] = nib.operand(w.x);
+        b[1] = nib.operand(w.y);
+        b[2] = nib.operand(w.z);
+        b[3] = nib.operand(w.w);
+      } else {
+        const u32x4 w2 = *reinterpret_cast<const u32x4*>(slot + rd_off[1]);
+        const uint32_t words[8] = {w.x, w.y, w.z, w.w, w2.x, w2.y, w2.z, w2.w};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) b[jj] = Codes<Act, kByte>::operand(words, jj, flip);
+      }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         f32x4 acc = Mfma16<Act>::run(xa[i][mb][0], b[0], zero4);
@@ -2844,12 +2864,18 @@ struct KsPlan {
 // tokens: 9.3 against 9.1 us).
 KsPlan plan_ks(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   KsPlan p;
-  if (bits != 2 && bits != 4) return p;
-  if (M > 64 || M < (K >= 8192 ? 5 : 17) || group % 128 != 0) return p;
+  if (bits != 2 && bits != 4 && bits != 8) return p;
+  // Byte codes: no resident-activation, N-split or multi-tile form takes them, so the kernel
+  // serves them from fewer tokens and on any grid (the streaming and skinny kernels are the
+  // alternative: down at 3-4 tokens 27 us there).
+  const bool bytes = bits == 8;
+  const int64_t min_m = K >= 8192 ? (bytes ? 3 : 5) : (bytes ? 9 : 17);
+  if (M > 64 || M < min_m || group % 128 != 0) return p;
   const int64_t tiles = (N + 15) / 16;
-  if (tiles >= 1024 || tiles < 1) return p;
-  if (K % (256 * kKsWaves) != 0) return p;
-  const int64_t slices = K / (256 * kKsWaves);
+  if ((tiles >= 1024 && !bytes) || tiles < 1) return p;
+  const int64_t block_k = bits == 8 ? 128 : 256;  // codes per block of 128 bytes per row
+  if (K % (block_k * kKsWaves) != 0) return p;
+  const int64_t slices = K / (block_k * kKsWaves);
   if (slices > kKsGrid) return p;
   p.slices = int(slices);
   p.per_slice = int(std::min<int64_t>(tiles, std::max<int64_t>(1, kKsGrid / slices)));
@@ -2861,11 +2887,11 @@ size_t ks_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bi
   return p.slices > 1 ? size_t(p.slices) * size_t(M) * size_t(N) * 4 : 0;
 }
 
-template <class Act, int MB>
+template <class Act, int MB, int FMT>
 hipError_t launch_ks_cfg(const LinearArgs& a, const KsPlan& p, uint32_t magic, hipStream_t stream) {
   using Geo = KsGeom<kKsWaves, kKsAhead, MB>;
   static_assert(Geo::lds_bytes() <= 160 * 1024, "LDS of one CU");
-  auto kern = decode_ks_kernel<Act, kKsWaves, kKsAhead, MB>;
+  auto kern = decode_ks_kernel<Act, kKsWaves, kKsAhead, MB, FMT>;
   const size_t lds = Geo::lds_bytes();
   if (lds > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -2880,8 +2906,14 @@ hipError_t launch_ks_cfg(const LinearArgs& a, const KsPlan& p, uint32_t magic, h
   return launch_splitk_reduce(a, partials, p.slices, stream);
 }
 
+template <class Act, int FMT>
+hipError_t launch_ks_mb(const LinearArgs& a, const KsPlan& p, uint32_t magic, hipStream_t stream) {
+  if (a.M <= 16) return launch_ks_cfg<Act, 1, FMT>(a, p, magic, stream);
+  if (a.M <= 32) return launch_ks_cfg<Act, 2, FMT>(a, p, magic, stream);
+  return launch_ks_cfg<Act, 4, FMT>(a, p, magic, stream);
+}
+
 bool try_ks(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
-  if (a.fmt != kNibble) return false;
   const KsPlan p = plan_ks(a.M, a.N, a.K, a.group, a.bits);
   if (p.slices == 0) return false;
   if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
@@ -2897,12 +2929,12 @@ bool try_ks(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   const uint32_t per_group = uint32_t(a.group / 128);
   const uint32_t magic = per_group == 1 ? 0u
       : uint32_t((uint64_t(1) << 32) / per_group + ((uint64_t(1) << 32) % per_group != 0));
-  if (a.M <= 16)
-    *err = a.act == kDtBf16 ? launch_ks_cfg<ActBf16, 1>(a, p, magic, stream) : launch_ks_cfg<ActF16, 1>(a, p, magic, stream);
-  else if (a.M <= 32)
-    *err = a.act == kDtBf16 ? launch_ks_cfg<ActBf16, 2>(a, p, magic, stream) : launch_ks_cfg<ActF16, 2>(a, p, magic, stream);
+  if (a.fmt == kByte)
+    *err = a.act == kDtBf16 ? launch_ks_mb<ActBf16, kByte>(a, p, magic, stream)
+                            : launch_ks_mb<ActF16, kByte>(a, p, magic, stream);
   else
-    *err = a.act == kDtBf16 ? launch_ks_cfg<ActBf16, 4>(a, p, magic, stream) : launch_ks_cfg<ActF16, 4>(a, p, magic, stream);
+    *err = a.act == kDtBf16 ? launch_ks_mb<ActBf16, kNibble>(a, p, magic, stream)
+                            : launch_ks_mb<ActF16, kNibble>(a, p, magic, stream);
   return true;
 }
 
@@ -3080,7 +3112,9 @@ bool nx_takes_wide(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
 
 size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   // The split of the kernel the decode path tries first: none for the resident-activation
-  // kernel, else the K-sliced kernel's, else the N-split kernel's over K slices.
+  // kernel, else the K-sliced kernel's (nibble or byte codes), else the N-split kernel's over K
+  // slices.
+  if (bits == 8) return ks_takes(M, N, K, group, bits) ? ks_workspace_bytes(M, N, K, group, bits) : 0;
   if (bits != 2 && bits != 4) return 0;
   if (kr_shape(M, N, K, group, bits)) return 0;
   if (ks_takes(M, N, K, group, bits)) return ks_workspace_bytes(M, N, K, group, bits);

@@ -520,13 +520,16 @@ def test_groups_of_64_one_hot_rows_return_weight_columns(m):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64])
 @pytest.mark.parametrize("n, k, symmetric, with_bias", [
-    (6144, 4096, False, False), (4100, 4096, True, True), (4096, 14336, False, False), (4096, 14336, True, False)])
+    (6144, 4096, False, False), (4100, 4096, True, True), (4096, 14336, False, False), (4096, 14336, True, False),
+    (16400, 4096, False, True)])
 def test_linear_byte_codes_decode(dtype, m, n, k, symmetric, with_bias):
-    # 8-bit codes (uint8 asymmetric, int8 symmetric, quantizers.py:231-234) at 1-8 tokens: the
-    # one-shot kernel's byte form (32 bytes per lane and step) where it fits, the streaming
-    # kernel for the rest; ragged N, bias, long rows.
+    # 8-bit codes (uint8 asymmetric, int8 symmetric, quantizers.py:231-234) at 1-64 tokens: the
+    # line kernel's byte form at one token on long rows, the one-shot kernel's (32 bytes per
+    # lane and step) at 1-8 tokens where it fits, the K-sliced kernel's (1024-code slices) from
+    # 3 tokens on long rows and from 9 on K = 4096, on any grid (N = 16400: 1025 tiles), the
+    # streaming kernel for the rest; ragged N, bias, long rows.
     qt = _host_qt(n, k, 8, 128, symmetric, seed=m + n + k)
     gen = torch.Generator().manual_seed(m)
     x = torch.randn(m, k, generator=gen).to(dtype)

@@ -92,10 +92,19 @@ def test_n_split_k_slices_where_the_k_sliced_kernel_does_not_fit(lib):
         assert _ws(lib, m, (4096, 9216)) == 9 * m * 4096 * 4, m
 
 
-def test_groups_below_128_and_8_bit_codes_never_take_the_decode_splits(lib):
+def test_groups_below_128_never_take_the_decode_splits(lib):
     for m in (5, 8, 16):
         assert _ws(lib, m, DOWN, group=64) == 0
-        assert _ws(lib, m, DOWN, bits=8) == 0
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 9, 16, 24, 32, 33, 48, 64])
+def test_byte_codes_take_k_slices_of_1024_codes(lib, m):
+    # 8-bit codes: a K slice of the K-sliced kernel is eight blocks of 128 bytes per row, 1024
+    # codes, so down (K 14336) splits into 14 slices from 3 tokens; K = 4096 into 4 from 9
+    # tokens, on any grid (gate_up too: no other fast kernel takes byte codes there).
+    assert _ws(lib, m, DOWN, bits=8) == (14 * m * 4096 * 4 if m >= 3 else 0)
+    assert _ws(lib, m, QKV, bits=8) == (4 * m * 6144 * 4 if m >= 9 else 0)
+    assert _ws(lib, m, GATE_UP, bits=8) == (4 * m * 28672 * 4 if m >= 9 else 0)
 
 
 def test_prefill_plans_above_64_tokens(lib):
