@@ -1900,8 +1900,9 @@ __device__ __forceinline__ void load_x_lines(u32x4 (&raw)[NS][MB][4], const Line
 }
 
 // The same pieces rearranged through the wave's LDS tile into MFMA fragments: frag[i][mb][j] =
-// x[16 mb + col][128 (step0 + i) + 32 kq + 8 j .. + 8] for lane (col, kq). In place.
-template <int NS, int MB>
+// x[16 mb + col][128 (step0 + i) + 32 kq + 8 j .. + 8] for lane (col, kq), or (TR, the order of
+// transposed code words) x[...][128 (step0 + i) + 32 j + 8 kq .. + 8]. In place.
+template <int NS, int MB, bool TR = false>
 __device__ __forceinline__ void lines_to_fragments(u32x4 (&v)[NS][MB][4], uint8_t* tile) {
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;
@@ -1917,7 +1918,7 @@ __device__ __forceinline__ void lines_to_fragments(u32x4 (&v)[NS][MB][4], uint8_
       wait_lgkmcnt0();
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        v[i][mb][j] = *reinterpret_cast<const u32x4*>(tile + col * kXTileRow + 64 * kq + 16 * j);
+        v[i][mb][j] = *reinterpret_cast<const u32x4*>(tile + col * kXTileRow + (TR ? 64 * j + 16 * kq : 64 * kq + 16 * j));
     }
   wait_lgkmcnt0();
 }
@@ -2133,9 +2134,15 @@ struct KsGeom {
 // FMT = kByte: 8-bit codes; a block of 128 bytes per row is one 128-code step (a slice of NW
 // blocks covers 1024 codes), lane (col, kq) reads chunks 2kq and 2kq + 1 of its row, and the
 // byte operands, flipped signs and zero-point offset are the one-shot kernel's.
-template <class Act, int NW, int R, int MB, int FMT = kNibble>
+// GS = 2: nibble codes in groups of 64, four groups per block. The lane's code words are
+// transposed across the wave's rows as in the one-shot kernel (MFMA e covers codes 32e .. 32e +
+// 31 of the step, inside group e / 2), the activation fragments are read in that order, and
+// each group keeps its own sums and scale; lane l loads the metadata of row l % 16 of group
+// l / 16 of the block.
+template <class Act, int NW, int R, int MB, int FMT = kNibble, int GS = 1>
 __global__ void __launch_bounds__(NW * 64)
     decode_ks_kernel(const LinearArgs a, int per_slice, uint32_t group_magic, float* partials) {
+  static_assert(GS == 1 || (GS == 2 && FMT == kNibble), "groups of 64: nibble codes");
   constexpr int SPB = FMT == kNibble ? 2 : 1;  // 128-code steps per block
   using Geo = KsGeom<NW, R, MB>;
   using Raw = typename Act::raw;
@@ -2168,7 +2175,8 @@ __global__ void __launch_bounds__(NW * 64)
   const auto mz = make_rsrc(asym ? a.zeros : a.scales, meta_total);
   // Metadata: lane l loads row l % 16 of step (l / 16) % 2 of the block (lanes 32..63 repeat
   // lanes 0..31), landing at float l of the slot's scale (zero) area.
-  const uint32_t mgroup = div_small(uint32_t(SPB * blk + (SPB == 2 ? (lane >> 4) & 1 : 0)), group_magic);
+  const uint32_t mgroup = GS == 2 ? uint32_t(4 * blk + (lane >> 4))
+                                  : div_small(uint32_t(SPB * blk + (SPB == 2 ? (lane >> 4) & 1 : 0)), group_magic);
   const uint32_t meta_lane = (uint32_t(lane & 15) * uint32_t(a.G) + mgroup) * 4;
   const auto wq = make_rsrc(a.qw, uint32_t(a.N * a.ldq));
   const int r8 = lane >> 3;
@@ -2200,19 +2208,25 @@ __global__ void __launch_bounds__(NW * 64)
   // ---- activations into operand order (lane (col, kq), step i, token block mb, MFMA j takes
   //      x[16 mb + col][256 b + 128 i + 32 kq + 8 j .. + 8]), and their per-step sums (one MFMA
   //      chain against ones) ----
-  lines_to_fragments<SPB, MB>(xa, base + Geo::ring_bytes() + Geo::red_bytes() + size_t(wave) * kXTileBytes);
+  lines_to_fragments<SPB, MB, GS == 2>(xa, base + Geo::ring_bytes() + Geo::red_bytes() + size_t(wave) * kXTileBytes);
   const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  f32x4 xs[SPB][MB];
+  // Per (step, group of the step, token block): the activation sums (with one group per step,
+  // entry [i][0] holds the whole step's).
+  f32x4 xs[SPB][GS][MB];
 #pragma unroll
   for (int i = 0; i < SPB; ++i)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) xa[i][mb][j] = arrange<Act, FMT>(xa[i][mb][j]);
-      xs[i][mb] = Mfma16<Act>::run(xa[i][mb][0], ones, zero4);
 #pragma unroll
-      for (int j = 1; j < 4; ++j) xs[i][mb] = Mfma16<Act>::run(xa[i][mb][j], ones, xs[i][mb]);
+      for (int h = 0; h < GS; ++h) {
+        constexpr int kPer = 4 / GS;
+        xs[i][h][mb] = Mfma16<Act>::run(xa[i][mb][kPer * h], ones, zero4);
+#pragma unroll
+        for (int j = 1; j < kPer; ++j) xs[i][h][mb] = Mfma16<Act>::run(xa[i][mb][kPer * h + j], ones, xs[i][h][mb]);
+      }
     }
 
   const NibbleConsts nib = NibbleConsts::make<Act>(uint32_t(a.ldq) & 0u);
@@ -2248,6 +2262,28 @@ __global__ void __launch_bounds__(NW * 64)
 #pragma unroll
     for (int i = 0; i < SPB; ++i) {
       const u32x4 w = *reinterpret_cast<const u32x4*>(slot + rd_off[i]);
+      if constexpr (GS == 2) {
+        // T[e] in row kq = word kq of row e: codes 32e + 8kq .. + 8 of the step.
+        const auto p02 = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
+        const auto p13 = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
+        const auto r01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+        const auto r23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+        const u32x4 b[4] = {nib.operand(r01[0]), nib.operand(r01[1]), nib.operand(r23[0]), nib.operand(r23[1])};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float sc = sm[16 * (2 * i + h) + col];
+          const float zc = asym ? sm[64 + 16 * (2 * i + h) + col] + z_shift : z_const;
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+            const f32x4 acc = Mfma16<Act>::run(xa[i][mb][2 * h + 1], b[2 * h + 1],
+                                               Mfma16<Act>::run(xa[i][mb][2 * h], b[2 * h], zero4));
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              tot[mb][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[i][h][mb][r], acc[r]), tot[mb][r]);
+          }
+        }
+        continue;
+      }
       const float sc = sm[16 * i + col];
       const float zc = asym ? sm[64 + 16 * i + col] + z_shift : z_const;
       u32x4 b[4];
@@ -2269,7 +2305,7 @@ __global__ void __launch_bounds__(NW * 64)
         for (int jj = 1; jj < 4; ++jj) acc = Mfma16<Act>::run(xa[i][mb][jj], b[jj], acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          tot[mb][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[i][mb][r], acc[r]), tot[mb][r]);
+          tot[mb][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[i][0][mb][r], acc[r]), tot[mb][r]);
       }
     }
     if (j + R < ntiles) {
@@ -2868,11 +2904,15 @@ KsPlan plan_ks(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   // Byte codes: no resident-activation, N-split or multi-tile form takes them, so the kernel
   // serves them from fewer tokens and on any grid (the streaming and skinny kernels are the
   // alternative: down at 3-4 tokens 27 us there).
+  // Groups of 64 (nibble codes): the multi-tile kernel takes 9-32 tokens, the skinny one 33-64;
+  // here from 9 tokens and on any grid as well.
   const bool bytes = bits == 8;
-  const int64_t min_m = K >= 8192 ? (bytes ? 3 : 5) : (bytes ? 9 : 17);
-  if (M > 64 || M < min_m || group % 128 != 0) return p;
+  const bool g64 = group == 64 && !bytes;
+  const bool wide = bytes || g64;  // no resident-activation or N-split form
+  const int64_t min_m = K >= 8192 ? (bytes ? 3 : 5) : (wide ? 9 : 17);
+  if (M > (g64 ? 32 : 64) || M < min_m || (group % 128 != 0 && !g64)) return p;
   const int64_t tiles = (N + 15) / 16;
-  if ((tiles >= 1024 && !bytes) || tiles < 1) return p;
+  if ((tiles >= 1024 && !wide) || tiles < 1) return p;
   const int64_t block_k = bits == 8 ? 128 : 256;  // codes per block of 128 bytes per row
   if (K % (block_k * kKsWaves) != 0) return p;
   const int64_t slices = K / (block_k * kKsWaves);
@@ -2887,11 +2927,11 @@ size_t ks_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bi
   return p.slices > 1 ? size_t(p.slices) * size_t(M) * size_t(N) * 4 : 0;
 }
 
-template <class Act, int MB, int FMT>
+template <class Act, int MB, int FMT, int GS>
 hipError_t launch_ks_cfg(const LinearArgs& a, const KsPlan& p, uint32_t magic, hipStream_t stream) {
   using Geo = KsGeom<kKsWaves, kKsAhead, MB>;
   static_assert(Geo::lds_bytes() <= 160 * 1024, "LDS of one CU");
-  auto kern = decode_ks_kernel<Act, kKsWaves, kKsAhead, MB, FMT>;
+  auto kern = decode_ks_kernel<Act, kKsWaves, kKsAhead, MB, FMT, GS>;
   const size_t lds = Geo::lds_bytes();
   if (lds > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -2906,11 +2946,13 @@ hipError_t launch_ks_cfg(const LinearArgs& a, const KsPlan& p, uint32_t magic, h
   return launch_splitk_reduce(a, partials, p.slices, stream);
 }
 
-template <class Act, int FMT>
+template <class Act, int FMT, int GS = 1>
 hipError_t launch_ks_mb(const LinearArgs& a, const KsPlan& p, uint32_t magic, hipStream_t stream) {
-  if (a.M <= 16) return launch_ks_cfg<Act, 1, FMT>(a, p, magic, stream);
-  if (a.M <= 32) return launch_ks_cfg<Act, 2, FMT>(a, p, magic, stream);
-  return launch_ks_cfg<Act, 4, FMT>(a, p, magic, stream);
+  if (a.M <= 16) return launch_ks_cfg<Act, 1, FMT, GS>(a, p, magic, stream);
+  if (a.M <= 32) return launch_ks_cfg<Act, 2, FMT, GS>(a, p, magic, stream);
+  // Four token blocks with two groups per step would spill (plan_ks stops groups of 64 at 32).
+  if constexpr (GS == 1) return launch_ks_cfg<Act, 4, FMT, GS>(a, p, magic, stream);
+  return hipErrorInvalidValue;
 }
 
 bool try_ks(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
@@ -2926,12 +2968,15 @@ bool try_ks(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
     if (!a.workspace || a.workspace_bytes < need || reinterpret_cast<uintptr_t>(a.workspace) % 16 != 0)
       return false;
   }
-  const uint32_t per_group = uint32_t(a.group / 128);
+  const uint32_t per_group = a.group == 64 ? 1u : uint32_t(a.group / 128);
   const uint32_t magic = per_group == 1 ? 0u
       : uint32_t((uint64_t(1) << 32) / per_group + ((uint64_t(1) << 32) % per_group != 0));
   if (a.fmt == kByte)
     *err = a.act == kDtBf16 ? launch_ks_mb<ActBf16, kByte>(a, p, magic, stream)
                             : launch_ks_mb<ActF16, kByte>(a, p, magic, stream);
+  else if (a.group == 64)
+    *err = a.act == kDtBf16 ? launch_ks_mb<ActBf16, kNibble, 2>(a, p, magic, stream)
+                            : launch_ks_mb<ActF16, kNibble, 2>(a, p, magic, stream);
   else
     *err = a.act == kDtBf16 ? launch_ks_mb<ActBf16, kNibble>(a, p, magic, stream)
                             : launch_ks_mb<ActF16, kNibble>(a, p, magic, stream);

@@ -92,9 +92,22 @@ def test_n_split_k_slices_where_the_k_sliced_kernel_does_not_fit(lib):
         assert _ws(lib, m, (4096, 9216)) == 9 * m * 4096 * 4, m
 
 
-def test_groups_below_128_never_take_the_decode_splits(lib):
+def test_groups_of_32_never_take_the_decode_splits(lib):
     for m in (5, 8, 16):
-        assert _ws(lib, m, DOWN, group=64) == 0
+        assert _ws(lib, m, DOWN, group=32) == 0
+
+
+@pytest.mark.parametrize("m", [1, 4, 5, 8, 9, 16, 32, 33, 64])
+def test_groups_of_64_take_k_slices_up_to_32_tokens(lib, m):
+    # Groups of 64 (nibble codes) run on the K-sliced kernel with four groups per block: down
+    # (7 slices) from 5 tokens, K = 4096 (2 slices) from 9, on any grid; above 32 tokens the
+    # split-K GEMM's own plan.
+    down, gate_up = _ws(lib, m, DOWN, group=64), _ws(lib, m, GATE_UP, group=64)
+    if m <= 32:
+        assert down == (7 * m * 4096 * 4 if m >= 5 else 0)
+        assert gate_up == (2 * m * 28672 * 4 if m >= 9 else 0)
+    else:
+        assert down % (m * 4096 * 4) == 0 and gate_up % (m * 28672 * 4) == 0
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 9, 16, 24, 32, 33, 48, 64])
