@@ -14,14 +14,20 @@
  *
  * Conventions:
  *   - Every pointer is a device pointer on the current HIP device, owned by the
- *     caller. The library keeps no tensors and allocates no device memory;
- *     scratch space for split-K comes in through `workspace`.
+ *     caller. The library keeps no tensors; scratch space (split-K partial sums,
+ *     the dense weight of the two-pass path) comes in through `workspace`. The
+ *     one allocation it makes is hipBLASLt's handle, created by the first
+ *     two-pass call on a device (so that call must not run under stream capture).
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream). Work is
- *     enqueued asynchronously; nothing synchronises the host.
+ *     enqueued asynchronously; nothing synchronises the host, except the first
+ *     two-pass call of a size class (M rounded up to 2^k or 3 * 2^(k-1)) on a
+ *     stream that is not being captured: it times hipBLASLt's candidate
+ *     algorithms on its own inputs and waits for them, once.
  *   - Return value: LLMOPT_OK (0) or a negative LLMOPT_ERR_* code. The message of
  *     the last failure on the calling thread is llmopt_q_last_error().
- *   - Reentrant: the only mutable global state is the per-thread error text and
- *     the static device scratch of llmopt_q_linear_noalloc (below); every other
+ *   - Reentrant: the mutable global state is the per-thread error text, the
+ *     static device scratch of llmopt_q_linear_noalloc (below), and the two-pass
+ *     path's hipBLASLt handles and plan cache, guarded by a mutex; every other
  *     entry point's calls from several host threads on different streams are
  *     independent.
  *   - group_size <= 0 means one group spanning the whole row.
@@ -57,6 +63,7 @@ extern "C" {
 #define LLMOPT_ALGO_GENERIC 1 /* any shape and dtype; scalar dequant + fp32 dot */
 #define LLMOPT_ALGO_DECODE 2  /* MFMA skinny GEMM, M <= 64 */
 #define LLMOPT_ALGO_PREFILL 3 /* MFMA GEMM with weight tiles dequantized into LDS */
+#define LLMOPT_ALGO_DENSE 4   /* the weight dequantized into the workspace, then hipBLASLt */
 
 /* ABI version of the loaded library (LLMOPT_QLINEAR_ABI_VERSION). */
 int llmopt_q_abi_version(void);
@@ -101,8 +108,9 @@ int llmopt_q_quantize_rtn(const void* weight, int w_dtype, int64_t ldw, int64_t 
  * Bytes of workspace llmopt_q_linear may use for these sizes (0 if none): fp32 partial sums of
  * a K split, splits * M * N * 4 bytes, for the prefill GEMM and for the decode kernels that
  * split K over fewer than 1024 tiles of 16 features (5-64 tokens on rows of K >= 8192, 33-64 on
- * shorter rows; none at 5-32 tokens over K = 4096 in groups of 128). With less, those shapes run
- * on the other kernels: correct, slower.
+ * shorter rows; none at 5-32 tokens over K = 4096 in groups of 128); from 1024 tokens, the
+ * two-pass path's llmopt_q_linear_dense_workspace bytes (or the split's, if larger). With less,
+ * those shapes run on the other kernels: correct, slower.
  */
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size);
 
@@ -110,12 +118,23 @@ size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int 
  * llmopt_q_linear_workspace for an activation dtype: the same for LLMOPT_DTYPE_BF16 / F16; for
  * LLMOPT_DTYPE_F32 the bytes of the fp32 path -- each activation split exactly into three bf16
  * pieces (3 * M * K * 2 bytes), the decode kernels' fp32 sums of a chunk of up to 21 tokens
- * (3 * chunk * N * 4) and their K-split partial sums. With less, fp32 runs on the generic kernel.
+ * (3 * chunk * N * 4) and their K-split partial sums; from 65 tokens, the two-pass path's fp32
+ * llmopt_q_linear_dense_workspace bytes (or the pieces', if larger). With less, fp32 runs on the
+ * generic kernel.
  * Sizes the workspace of QuantLinear.forward with compute_dtype float32
  * (src/llmopt/quantization/quant_linear.py:93-113), the reference engine's quantized model
  * (engine/llm_engine.py:258-264).
  */
 size_t llmopt_q_linear_workspace_ex(int64_t M, int64_t N, int64_t K, int bits, int group_size, int act_dtype);
+
+/*
+ * Bytes of workspace of the two-pass path (LLMOPT_ALGO_DENSE, and AUTO from 1024 tokens, 65 with
+ * fp32 activations): the dense [N, K] weight in the activation dtype, 256-byte aligned, then
+ * 32 MiB for hipBLASLt. The two passes are the reference's own computation,
+ * QuantLinear._dequantized_weight then F.linear (src/llmopt/quantization/quant_linear.py:93-113),
+ * with the dense weight rebuilt in the workspace by every call instead of cached in the module.
+ */
+size_t llmopt_q_linear_dense_workspace(int64_t N, int64_t K, int act_dtype);
 
 /*
  * y = x @ dequant(qweight)^T + bias, without materialising the dense weight.
@@ -134,9 +153,11 @@ int llmopt_q_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void
  * llmopt_q_linear without a workspace argument and without any allocation: the K-split
  * partial sums that llmopt_q_linear keeps in the caller's workspace live in a static device
  * array of the library instead, llmopt_q_linear_noalloc_max_scratch() bytes (32 MiB) per
- * device, held until the process ends. Results are those of llmopt_q_linear with a workspace
- * of llmopt_q_linear_workspace(...) bytes, bit for bit. A shape whose plan needs more scratch
- * than that returns LLMOPT_ERR_WORKSPACE and launches nothing. Calls that overlap on one
+ * device, held until the process ends. Below 1024 tokens, results are those of llmopt_q_linear
+ * with a workspace of llmopt_q_linear_workspace(...) bytes, bit for bit; from 1024 tokens it runs
+ * the fused GEMM (the two-pass path's dense weight does not fit the scratch): the results of
+ * llmopt_q_linear_ex with LLMOPT_ALGO_PREFILL. A shape whose plan needs more scratch than that
+ * returns LLMOPT_ERR_WORKSPACE and launches nothing. Calls that overlap on one
  * device (other streams, other threads) share that device's array and race on it; serialize
  * them. Run it with the stream's device current.
  * No counterpart in the reference: for callers that cannot allocate device memory (code

@@ -2,9 +2,11 @@
 //
 // Validates arguments the way the reference's torch code would reject them, fills the
 // kernel argument block and picks the kernel: the decode kernels for M <= 32, the MFMA
-// register-dequant GEMM (split over K on small grids) above, the LDS-dequant GEMM for the
-// shapes that one does not take, and the generic kernel for shapes, alignments or dtypes the
-// fast kernels do not take. Error text is kept per host thread.
+// register-dequant GEMM (split over K on small grids) above, from 1024 tokens (65 with fp32
+// activations) the weight dequantized into the workspace and hipBLASLt's dense GEMM, the
+// LDS-dequant GEMM for the shapes the register-dequant one does not take, and the generic kernel
+// for shapes, alignments or dtypes the fast kernels do not take. Error text is kept per host
+// thread.
 #include <stdarg.h>
 #include <algorithm>
 #include <stdio.h>
@@ -102,7 +104,29 @@ int describe_weight(llmopt::LinearArgs& a, const void* qweight, int64_t ldq, con
 }
 
 
-size_t swiglu_temp_bytes(int64_t M, int64_t N) { return (size_t(M) * size_t(N) * 4 + 255) / 256 * 256; }
+// The full [M, N] product that the combining kernel reads, in the activation dtype.
+size_t swiglu_temp_bytes(int64_t M, int64_t N, int act) {
+  return (size_t(M) * size_t(N) * (act == LLMOPT_DTYPE_F32 ? 4 : 2) + 255) / 256 * 256;
+}
+
+// Workspace of the fused kernels' plan (16-bit activations): the decode path's K split when it
+// has one for these sizes (a call given that much takes it), else the split-K GEMM's when the
+// GEMM takes the shape.
+size_t fused_workspace_bytes(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
+  if (M <= 0 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
+  const int64_t g = group_size <= 0 ? K : group_size;
+  const size_t dec = M <= 64 ? llmopt::decode_workspace_bytes(M, N, K, g, bits) : 0;
+  if (dec > 0 || !gemm_first(M, K, N, g, bits)) return dec;
+  return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
+}
+
+// Whether a call of this size with this workspace takes the two-pass path (dequantize, then
+// hipBLASLt) when hipBLASLt has an algorithm for it.
+bool dense_first(int64_t M, int64_t N, int64_t K, int act, const void* workspace, size_t workspace_bytes) {
+  return M >= llmopt::dense_min_tokens(act) && workspace != nullptr &&
+         reinterpret_cast<uintptr_t>(workspace) % 256 == 0 &&
+         workspace_bytes >= llmopt::dense_workspace_bytes(N, K, act);
+}
 
 // Dispatch shared by llmopt_q_linear_ex and llmopt_q_linear_swiglu. With the SwiGLU epilogue,
 // `y` is [M, N/2]; kernels that cannot apply it themselves write the full [M, N] product into
@@ -144,8 +168,12 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
   bool fits = false;
   hipError_t err = hipSuccess;
   if (epilogue != llmopt::kEpiNone) {
-    // Kernels with the fused epilogue first.
-    if (K > 0 && algo == LLMOPT_ALGO_AUTO) {
+    // Kernels with the fused epilogue first, unless the batch is long enough for the two-pass
+    // path and the workspace holds its product and dense weight.
+    const size_t temp = swiglu_temp_bytes(M, N, act_dtype);
+    const bool dense = algo == LLMOPT_ALGO_AUTO && workspace_bytes >= temp &&
+                       dense_first(M, N, K, act_dtype, workspace, workspace_bytes - temp);
+    if (K > 0 && algo == LLMOPT_ALGO_AUTO && !dense) {
       if (M <= kDecodeMaxTokens || !gemm_first(M, K, N, a.group, bits)) {
         err = llmopt::launch_linear_decode(a, s, &fits);
         if (!fits && M > kDecodeMaxTokens) err = llmopt::launch_linear_gemm(a, s, &fits);
@@ -156,7 +184,6 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
       if (fits) return hip_status(err, "linear launch");
     }
     // Then the plain product into the workspace, and the combining kernel.
-    const size_t temp = swiglu_temp_bytes(M, N);
     if (!workspace || workspace_bytes < temp || reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
       return fail(LLMOPT_ERR_WORKSPACE, "this shape needs a workspace of at least %zu bytes",
                   temp + llmopt_q_linear_workspace_ex(M, N, K, bits, group_size, act_dtype));
@@ -166,6 +193,21 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
                     workspace_bytes - temp, stream, algo, llmopt::kEpiNone);
     if (rc != LLMOPT_OK) return rc;
     return hip_status(llmopt::launch_swiglu_combine(t, N, y, ldy, M, N, act_dtype, s), "swiglu launch");
+  }
+
+  if (algo == LLMOPT_ALGO_DENSE || (algo == LLMOPT_ALGO_AUTO && dense_first(M, N, K, act_dtype, a.workspace,
+                                                                               a.workspace_bytes))) {
+    // Long batches: the weight dequantized into the workspace, then hipBLASLt's dense GEMM.
+    err = llmopt::launch_linear_dense(a, s, &fits);
+    if (fits) return hip_status(err, "dense linear");
+    if (algo == LLMOPT_ALGO_DENSE) {
+      const size_t need = llmopt::dense_workspace_bytes(N, K, act_dtype);
+      if (!a.workspace || a.workspace_bytes < need || reinterpret_cast<uintptr_t>(a.workspace) % 256 != 0)
+        return fail(LLMOPT_ERR_WORKSPACE, "the dense path needs a 256-byte aligned workspace of at least %zu bytes",
+                    need);
+      return fail(LLMOPT_ERR_UNSUPPORTED, "hipBLASLt offers no algorithm for M=%lld N=%lld K=%lld", (long long)M,
+                  (long long)N, (long long)K);
+    }
   }
 
   if (act_dtype == LLMOPT_DTYPE_F32 && algo == LLMOPT_ALGO_AUTO) {
@@ -330,19 +372,25 @@ int llmopt_q_quantize_rtn(const void* weight, int w_dtype, int64_t ldw, int64_t 
 size_t llmopt_q_linear_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
   // The GEMM's K split, and the decode path's kernels that split K over workgroups (5-64 tokens
   // on grids of fewer than 1024 tiles of 16 features); the other decode kernels reduce in LDS.
+  // From 1024 tokens the dense weight and hipBLASLt's workspace, and at least the fused plan's
+  // (what runs if hipBLASLt has no algorithm for the shape).
   if (M <= 0 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
-  const int64_t g = group_size <= 0 ? K : group_size;
-  // The decode path's K split when it has one for these sizes (a call given that much takes
-  // it), else the GEMM's when the GEMM takes the shape.
-  const size_t dec = M <= 64 ? llmopt::decode_workspace_bytes(M, N, K, g, bits) : 0;
-  if (dec > 0 || !gemm_first(M, K, N, g, bits)) return dec;
-  return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
+  const size_t fused = fused_workspace_bytes(M, N, K, bits, group_size);
+  if (M < llmopt::dense_min_tokens(LLMOPT_DTYPE_BF16)) return fused;
+  return std::max(fused, llmopt::dense_workspace_bytes(N, K, LLMOPT_DTYPE_BF16));
 }
 
 size_t llmopt_q_linear_workspace_ex(int64_t M, int64_t N, int64_t K, int bits, int group_size, int act_dtype) {
   if (act_dtype != LLMOPT_DTYPE_F32) return llmopt_q_linear_workspace(M, N, K, bits, group_size);
   if (M <= 0 || N <= 0 || K <= 0 || bits < 1 || bits > 8) return 0;
-  return llmopt::f32_workspace_bytes(M, N, K, group_size <= 0 ? K : group_size, bits);
+  const size_t pieces = llmopt::f32_workspace_bytes(M, N, K, group_size <= 0 ? K : group_size, bits);
+  if (M < llmopt::dense_min_tokens(LLMOPT_DTYPE_F32)) return pieces;
+  return std::max(pieces, llmopt::dense_workspace_bytes(N, K, LLMOPT_DTYPE_F32));
+}
+
+size_t llmopt_q_linear_dense_workspace(int64_t N, int64_t K, int act_dtype) {
+  if (!valid_dtype(act_dtype)) return 0;
+  return llmopt::dense_workspace_bytes(N, K, act_dtype);
 }
 
 int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
@@ -358,6 +406,9 @@ int llmopt_q_linear_ex(const void* x, int64_t M, int64_t K, int64_t ldx, const v
 size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const int64_t g = group_size <= 0 ? K : group_size;
+  // Long batches: the [M, N] product and the two-pass path's workspace, then the combining kernel.
+  if (M >= llmopt::dense_min_tokens(LLMOPT_DTYPE_BF16) && bits >= 1 && bits <= 8)
+    return swiglu_temp_bytes(M, N, LLMOPT_DTYPE_BF16) + llmopt_q_linear_workspace(M, N, K, bits, group_size);
   const bool nibble = bits == 2 || bits == 4;
   // Sizes whose kernels apply the activation themselves (assuming aligned, contiguous tensors):
   // the decode path's partial sums where its plan splits K, else nothing.
@@ -366,8 +417,8 @@ size_t llmopt_q_linear_swiglu_workspace(int64_t M, int64_t N, int64_t K, int bit
     return M <= 64 ? llmopt::decode_workspace_bytes(M, N, K, g, bits) : 0;
   if (M > kDecodeMaxTokens && bits >= 1 && bits <= 8 && g % 32 == 0 && K % 64 == 0)
     return llmopt::gemm_workspace_bytes(M, N, K, g, bits == 8 ? llmopt::kByte : llmopt::kNibble);
-  // Otherwise: the full [M, N] output in fp32-sized slots, then the combining kernel.
-  return swiglu_temp_bytes(M, N) + llmopt_q_linear_workspace(M, N, K, bits, group_size);
+  // Otherwise: the full [M, N] output, then the combining kernel.
+  return swiglu_temp_bytes(M, N, LLMOPT_DTYPE_BF16) + llmopt_q_linear_workspace(M, N, K, bits, group_size);
 }
 
 size_t llmopt_q_linear_swiglu_workspace_ex(int64_t M, int64_t N, int64_t K, int bits, int group_size,
@@ -376,7 +427,7 @@ size_t llmopt_q_linear_swiglu_workspace_ex(int64_t M, int64_t N, int64_t K, int 
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   // No fp32 kernel applies the activation itself: the product into the workspace, then the
   // combining kernel.
-  return swiglu_temp_bytes(M, N) + llmopt_q_linear_workspace_ex(M, N, K, bits, group_size, act_dtype);
+  return swiglu_temp_bytes(M, N, act_dtype) + llmopt_q_linear_workspace_ex(M, N, K, bits, group_size, act_dtype);
 }
 
 int llmopt_q_linear_swiglu(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
@@ -407,7 +458,8 @@ int llmopt_q_linear_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, co
                             int64_t ldq, const float* scales, const float* zeros, const void* bias,
                             void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
                             int symmetric, int signed_codes, void* stream) {
-  const size_t need = llmopt_q_linear_workspace(M, N, K, bits, group_size);
+  // The fused kernels' plan: the two-pass path's dense weight does not fit the scratch.
+  const size_t need = fused_workspace_bytes(M, N, K, bits, group_size);
   if (need > kNoAllocScratchBytes)
     return fail(LLMOPT_ERR_WORKSPACE,
                 "llmopt_q_linear_noalloc: M=%lld N=%lld K=%lld needs %zu bytes of scratch, beyond the %zu "

@@ -177,5 +177,12 @@ hipError_t launch_linear_f32_pieces(const LinearArgs& a, hipStream_t stream, boo
 // it (no workspace); *fits is false for the shapes it does not take.
 hipError_t launch_linear_oneshot_f32(const LinearArgs& a, hipStream_t stream, bool* fits);
 size_t f32_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group, int bits);
+// Long batches in two passes: the weight dequantized into the workspace, then hipBLASLt's dense
+// GEMM. *fits is false (nothing launched) when the workspace is smaller than
+// dense_workspace_bytes, for an epilogue, or when hipBLASLt offers no algorithm for the shape.
+hipError_t launch_linear_dense(const LinearArgs& a, hipStream_t stream, bool* fits);
+size_t dense_workspace_bytes(int64_t N, int64_t K, int act);
+// Batches from this many tokens take the two-pass path (given its workspace).
+int64_t dense_min_tokens(int act);
 
 }  // namespace llmopt

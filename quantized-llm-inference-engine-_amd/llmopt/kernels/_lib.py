@@ -19,6 +19,7 @@ __all__ = [
     "ALGO_DECODE",
     "ALGO_GENERIC",
     "ALGO_PREFILL",
+    "ALGO_DENSE",
     "DTYPE_CODES",
     "EXPORTED_SYMBOLS",
     "call",
@@ -32,6 +33,7 @@ ALGO_AUTO = 0
 ALGO_GENERIC = 1
 ALGO_DECODE = 2
 ALGO_PREFILL = 3
+ALGO_DENSE = 4
 
 ERR_INVALID_ARG = -1
 ERR_UNSUPPORTED = -2
@@ -85,6 +87,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmopt_q_linear_swiglu_workspace": (_size, [_i64, _i64, _i64, _int, _int]),
     "llmopt_q_linear_swiglu_workspace_ex": (_size, [_i64, _i64, _i64, _int, _int, _int]),
     "llmopt_q_linear_workspace_ex": (_size, [_i64, _i64, _i64, _int, _int, _int]),
+    "llmopt_q_linear_dense_workspace": (_size, [_i64, _i64, _int]),
     "llmopt_q_linear_swiglu": (
         _int,
         [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _int, _int, _int, _int, _int,

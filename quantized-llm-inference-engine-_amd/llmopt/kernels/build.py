@@ -88,6 +88,8 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
     torch_lib = _torch_lib_dir()
     if torch_lib:
         link.append(f"-Wl,-rpath,{torch_lib}")
+    # hipBLASLt for the two-pass prefill's dense GEMM.
+    link += ["-L/opt/rocm/lib", "-lhipblaslt"]
     if verbose:
         print(" ".join(link), flush=True)
     proc = subprocess.run(link, capture_output=True, text=True)

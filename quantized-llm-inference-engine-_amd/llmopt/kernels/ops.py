@@ -22,7 +22,7 @@ from __future__ import annotations
 
 import torch
 
-from llmopt.kernels._lib import ALGO_AUTO, DTYPE_CODES, call, load_library
+from llmopt.kernels._lib import ALGO_AUTO, ALGO_DENSE, DTYPE_CODES, call, load_library
 
 __all__ = [
     "dequantize",
@@ -238,11 +238,15 @@ def quant_linear(
         if bias is not None:
             bias = bias.contiguous()
         lib = load_library()
-        # Scratch for split-K partial sums (only some prefill shapes use it); it comes from
-        # torch's caching allocator, so repeated calls reuse the same block.
-        ws_bytes = int(
-            lib.llmopt_q_linear_workspace_ex(m, rows, cols, int(qt.bits), group, DTYPE_CODES[compute_dtype])
-        )
+        # Scratch for split-K partial sums, or from 1024 tokens (65 in fp32) the dense weight of
+        # the two-pass path; it comes from torch's caching allocator, so repeated calls reuse
+        # the same block.
+        if algo == ALGO_DENSE:
+            ws_bytes = int(lib.llmopt_q_linear_dense_workspace(rows, cols, DTYPE_CODES[compute_dtype]))
+        else:
+            ws_bytes = int(
+                lib.llmopt_q_linear_workspace_ex(m, rows, cols, int(qt.bits), group, DTYPE_CODES[compute_dtype])
+            )
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
         call(
             lib.llmopt_q_linear_ex(

@@ -15,7 +15,10 @@ Llama-3-8B projections without a GPU (no kernel is launched):
   (K >= 8192 not a multiple of 2048, 12-32 tokens);
 * nothing for gate_up up to 64 tokens (its N-split kernel keeps all of K per workgroup), nor at
   1-4 tokens anywhere;
-* the prefill GEMM's own plan above 64 tokens.
+* the prefill GEMM's own plan above 64 tokens;
+* from 1024 tokens the two-pass path: the dense weight in the compute dtype (256-byte aligned)
+  and 32 MiB for hipBLASLt, or the fused plan's bytes where those are more (what runs when
+  hipBLASLt has no algorithm); fp32 activations from 65 tokens.
 """
 
 from __future__ import annotations
@@ -124,11 +127,40 @@ def test_prefill_plans_above_64_tokens(lib):
     # The GEMM's K split is sized by its own plan: a multiple of one fp32 plane of M x N.
     for shape in (QKV, O, GATE_UP, DOWN):
         n = shape[0]
-        for m in (65, 256, 2048):
+        for m in (65, 256, 1023):
             ws = _ws(lib, m, shape)
             assert ws % (m * n * 4) == 0 and ws // (m * n * 4) in (0, 2, 3, 4, 5, 6, 7, 8), (shape, m, ws)
-    # A full grid of 256-token tiles does not split.
-    assert _ws(lib, 8192, GATE_UP) == 0
+
+
+BLAS_WS = 32 << 20
+
+
+def _dense(n, k, es):
+    return -(-n * k * es // 256) * 256 + BLAS_WS
+
+
+@pytest.mark.parametrize("m", [1024, 2048, 8192, 16384])
+def test_long_batches_take_the_two_pass_path(lib, m):
+    for n, k in (QKV, O, GATE_UP, DOWN):
+        assert lib.llmopt_q_linear_dense_workspace(n, k, _lib.DTYPE_CODES[torch.bfloat16]) == _dense(n, k, 2)
+        assert lib.llmopt_q_linear_dense_workspace(n, k, _lib.DTYPE_CODES[torch.float32]) == _dense(n, k, 4)
+        # The dense weight is larger than any split plan of these shapes.
+        assert _ws(lib, m, (n, k)) == _dense(n, k, 2), (n, k, m)
+        for bits, group in ((8, 128), (2, 64), (4, 32)):
+            assert _ws(lib, m, (n, k), bits, group) == _dense(n, k, 2)
+        # Fused gate/up + SwiGLU: the [M, N] product in the compute dtype, then the same.
+        sw = lib.llmopt_q_linear_swiglu_workspace(m, n, k, 4, 128)
+        assert sw == -(-m * n * 2 // 256) * 256 + _dense(n, k, 2)
+
+
+def test_fp32_takes_the_two_pass_path_from_65_tokens(lib):
+    f32 = _lib.DTYPE_CODES[torch.float32]
+    n, k = GATE_UP
+    assert lib.llmopt_q_linear_workspace_ex(64, n, k, 4, 64, f32) < _dense(n, k, 4)
+    for m in (65, 256, 2048):
+        assert lib.llmopt_q_linear_workspace_ex(m, n, k, 4, 64, f32) >= _dense(n, k, 4)
+    # A small weight with a long batch: the pieces' workspace (3 M K bf16 pieces ...) is larger.
+    assert lib.llmopt_q_linear_workspace_ex(4096, 256, 4096, 4, 64, f32) > _dense(256, 4096, 4)
 
 
 def test_wide_grids_at_33_to_64_tokens_keep_the_gemm_for_other_formats(lib):

@@ -75,3 +75,25 @@ def test_noalloc_refuses_plans_beyond_its_scratch():
     assert rc == -4 and b"static scratch" in lib.llmopt_q_last_error()
     torch.cuda.synchronize()
     assert bool(torch.isnan(y).all())  # nothing was launched
+
+
+def test_noalloc_long_batches_run_the_fused_gemm():
+    # From 1024 tokens llmopt_q_linear dequantizes into its workspace and calls hipBLASLt; the
+    # dense weight does not fit the static scratch, so the allocation-free entry point runs the
+    # fused GEMM instead: llmopt_q_linear_ex with LLMOPT_ALGO_PREFILL, bit for bit.
+    lib = _lib.load_library()
+    n, k, m = 4096, 4096, 1024
+    qw, sc, zr = _weight(n, k, 5)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    need = lib.llmopt_q_linear_workspace(m, n, k, 4, 128)
+    assert need > lib.llmopt_q_linear_noalloc_max_scratch()
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    want = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    rc = lib.llmopt_q_linear_ex(*_args(x, qw, sc, zr, want, n, k, m), ws.data_ptr(), need, stream, _lib.ALGO_PREFILL)
+    assert rc == 0, lib.llmopt_q_last_error()
+    got = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    rc = lib.llmopt_q_linear_noalloc(*_args(x, qw, sc, zr, got, n, k, m), stream)
+    assert rc == 0, lib.llmopt_q_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
