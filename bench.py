@@ -19,7 +19,9 @@ roofline       the dominant kernel (gate_up): its algorithmic bytes / its mean t
                inter-kernel gap;
                `traffic` = HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (each
                scaled by what it reads for a plain copy of known size), when recorded
-prefill        gate_up at M = 8192 through the MFMA prefill kernel, TFLOP/s vs dense bf16 peak
+prefill        gate_up at M = 8192 as QuantLinear runs it (from 1024 tokens: the weight
+               dequantized into the workspace, then hipBLASLt), TFLOP/s vs dense bf16 peak; and
+               the fused register-dequant MFMA GEMM on the same shape (`fused_gemm`)
 dense_comparator  (in roofline and prefill) torch's dense bf16 F.linear on the dequantized
                weight at the same shape: hipBLASLt's figure for the unquantized layer
 dequant, quantize, attention  the device dequantize and RTN quantizer on gate_up, and the
@@ -406,22 +408,35 @@ def _measured_traffic(m: int):
 
 
 def prefill(torch, ops, rotations):
-    """gate_up at M = 8192 (prefill kernel), per-launch time of back-to-back launches."""
+    """gate_up at M = 8192, per-call time of back-to-back calls: the automatic choice (the
+    two-pass path: device dequantize into the workspace, then hipBLASLt) and the fused
+    register-dequant GEMM (LLMOPT_ALGO_PREFILL) on the same shape."""
+    from llmopt.kernels._lib import ALGO_AUTO, ALGO_PREFILL
+
     name, n, k = PROJECTIONS[2]
     m = 8192
     qts = rotations[name]
     x = torch.randn(m, k, device="cuda:0").to(torch.bfloat16)
-    ops.quant_linear(x, qts[0], None, torch.bfloat16)
-    times = kernel_launch_times(
-        torch, lambda i: ops.quant_linear(x, qts[i % len(qts)], None, torch.bfloat16), len(qts)
-    )
-    us = statistics.median(times)
-    tflops = 2 * m * n * k / (us * 1e-6) / 1e12
-    print(f"# prefill gate_up M={m}: {us:.1f} us, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    out = {}
+    for label, algo in (("auto", ALGO_AUTO), ("fused_gemm", ALGO_PREFILL)):
+        ops.quant_linear(x, qts[0], None, torch.bfloat16, algo=algo)
+        times = kernel_launch_times(
+            torch, lambda i: ops.quant_linear(x, qts[i % len(qts)], None, torch.bfloat16, algo=algo), len(qts)
+        )
+        us = statistics.median(times)
+        out[label] = (us, 2 * m * n * k / (us * 1e-6) / 1e12)
+        print(f"# prefill gate_up M={m} ({label}): {us:.1f} us, {out[label][1]:.1f} TFLOP/s", file=sys.stderr,
+              flush=True)
+    us, tflops = out["auto"]
     dense = dense_comparator(torch, qts[0], m)
-    return {"kernel": f"quantized-linear prefill, gate_up M={m} (K 4096, N 28672)", "mean_launch_us": round(us, 2),
+    return {"kernel": f"quantized-linear prefill, gate_up M={m} (K 4096, N 28672): device dequantize into the "
+                      f"workspace, then hipBLASLt", "mean_launch_us": round(us, 2),
             "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "bound": "mfma", "dense_comparator": dense}
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "bound": "mfma",
+            "fused_gemm": {"mean_launch_us": round(out["fused_gemm"][0], 2),
+                           "achieved": round(out["fused_gemm"][1], 1),
+                           "frac": round(out["fused_gemm"][1] / BF16_PEAK_TFLOPS, 4)},
+            "dense_comparator": dense}
 
 
 def end_to_end(torch, seqs: int = 32, prompt_len: int = 512, steps: int = 128, ref_steps: int = 16):

@@ -20,9 +20,9 @@
  *     two-pass call on a device (so that call must not run under stream capture).
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream). Work is
  *     enqueued asynchronously; nothing synchronises the host, except the first
- *     two-pass call of a size class (M rounded up to 2^k or 3 * 2^(k-1)) on a
- *     stream that is not being captured: it times hipBLASLt's candidate
- *     algorithms on its own inputs and waits for them, once.
+ *     two-pass call of a size class (M rounded up to 2^k or 3 * 2^(k-1), up to
+ *     6144 tokens) on a stream that is not being captured: it times hipBLASLt's
+ *     candidate algorithms on its own inputs and waits for them, once.
  *   - Return value: LLMOPT_OK (0) or a negative LLMOPT_ERR_* code. The message of
  *     the last failure on the calling thread is llmopt_q_last_error().
  *   - Reentrant: the mutable global state is the per-thread error text, the

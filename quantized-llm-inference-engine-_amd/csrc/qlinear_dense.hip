@@ -14,13 +14,15 @@
 //
 // hipBLASLt state: one handle per device, created on the first dense call on that device, and a
 // bounded cache per shape of the matmul descriptors and the heuristic's first candidates
-// (kCandidates). Which candidate runs is measured, not guessed: the heuristic's first choice is
-// up to 18 % slower than the best of its first eight at 1024-2048 tokens on MI355X, and one of
-// its first choices there does not run at all. The first call of a size class (M rounded up to
+// (kCandidates). Up to 6144 tokens, which candidate runs is measured, not guessed: there the
+// heuristic's first choice is up to 18 % slower than the best of its first eight on MI355X, and
+// one of its first choices does not run at all. The first call of a size class (M rounded up to
 // a power of two or 1.5 times one) on a stream that is not being captured runs every candidate
 // on its own inputs, times them with HIP events and waits for them (the one place this library
 // blocks the host), then keeps the fastest; later calls of any M in that class run the same
-// algorithm when the heuristic offers it for their M. A candidate that fails to launch is
+// algorithm when the heuristic offers it for their M. From 8192 tokens the heuristic's first
+// choice measured fastest for every Llama-3-8B projection, and measuring there would cost tens
+// of milliseconds of GEMMs, so the heuristic's order stands. A candidate that fails to launch is
 // dropped and the next one runs; with none left the call reports that the path does not fit
 // and the fused kernels run. Both caches are guarded by one mutex, which is also held while a
 // call sets its bias pointer and enqueues the matmul. hipblasLtCreate allocates device memory:
@@ -44,6 +46,7 @@ constexpr int kMaxDevices = 64;
 constexpr size_t kMaxPlans = 256;
 constexpr int kCandidates = 8;
 constexpr int kTimedRuns = 2;
+constexpr int64_t kMeasureMaxTokens = 6144;  // largest size class whose candidates are timed
 
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
@@ -264,7 +267,7 @@ hipError_t launch_linear_dense(const LinearArgs& a, hipStream_t stream, bool* fi
   }
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &capture) != hipSuccess) capture = hipStreamCaptureStatusActive;
-  if (p->chosen < 0 && capture == hipStreamCaptureStatusNone) {
+  if (p->chosen < 0 && capture == hipStreamCaptureStatusNone && cls.M <= kMeasureMaxTokens) {
     hipEvent_t* ev = g_events[device];
     bool have = true;
     for (int i = 0; i < 2 * kCandidates && have; ++i)
