@@ -104,6 +104,12 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--e2e-only", action="store_true", help="only the end-to-end generation (for profiling)")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--pmc-workload", action="store_true", help="only the dominant kernel + a copy")
+    p.add_argument("--pmc-prefill", action="store_true",
+                   help="only gate_up at M = 8192, two-pass and fused GEMM, three calls each (for --pmc)")
+    p.add_argument("--pmc-decode", action="store_true",
+                   help="only qkv and o at M = 32 and 64, five calls each, and a copy (for --pmc)")
+    p.add_argument("--counters-from", type=str, default=None,
+                   help="rocprofv3 --pmc output dir: print each counter's mean per dispatch, per kernel and grid")
     p.add_argument("--roofline-only", action="store_true",
                    help="only the roofline block (graph replays of the dominant kernel), for rocprofv3 --stats")
     p.add_argument("--traffic-from", type=str, default=None, help="rocprofv3 --pmc output dir")
@@ -193,6 +199,8 @@ def main() -> int:
         return trace_runs(Path(args.trace_runs))
     if args.trace_kernels:
         return trace_kernels(Path(args.trace_kernels))
+    if args.counters_from:
+        return counters_summary(Path(args.counters_from))
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: the quantized-linear kernels run on one device and there "
@@ -212,6 +220,8 @@ def main() -> int:
     if args.e2e_only:
         print(json.dumps({"e2e": end_to_end(torch)}), flush=True)
         return 0
+    if args.pmc_prefill or args.pmc_decode:
+        return pmc_blocks(torch, ops, args.pmc_prefill)
 
     layer_bytes = sum(algorithmic_bytes(0, n, k) for _, n, k in PROJECTIONS)
     copies = max(2, -(-MIN_ROTATION_BYTES // layer_bytes))
@@ -943,6 +953,82 @@ def _counter_per_dispatch(csv_path: Path, counter: str):
     # them), not the smaller copies that set up the weight copies.
     flushes = [v for v in copy if v * 1024 >= COPY_BYTES / 4]
     return kern, flushes
+
+
+def pmc_blocks(torch, ops, prefill_block: bool) -> int:
+    """Workloads for counter runs: gate_up at M = 8192 through the two-pass path and through the
+    fused GEMM (one warm call, three counted calls each), or qkv and o at M = 32 and 64 (five
+    calls each from two weight copies, a 256 MiB copy between calls so no call finds the
+    previous one's weights in the caches; the copy also scales FETCH_SIZE / WRITE_SIZE)."""
+    from llmopt.kernels._lib import ALGO_AUTO, ALGO_PREFILL
+
+    base, layers, _ = build_layers(torch, 2, 1)
+    bf16 = torch.bfloat16
+    src = torch.empty(COPY_BYTES // 2, dtype=bf16, device="cuda:0")
+    dst = torch.empty_like(src)
+    if prefill_block:
+        name, n, k = PROJECTIONS[2]
+        x = torch.randn(8192, k, device="cuda:0").to(bf16)
+        for algo in (ALGO_AUTO, ALGO_PREFILL):
+            ops.quant_linear(x, base[name], None, bf16, algo=algo)
+            torch.cuda.synchronize()
+            for i in range(3):
+                dst.copy_(src)
+                ops.quant_linear(x, layers[i % 2][name], None, bf16, algo=algo)
+            torch.cuda.synchronize()
+        print(json.dumps({"pmc_prefill": "gate_up", "M": 8192, "calls": {"two-pass": 3, "fused_gemm": 3}}))
+        return 0
+    for name, n, k in PROJECTIONS[:2]:
+        for m in (32, 64):
+            x = torch.randn(m, k, device="cuda:0").to(bf16)
+            ops.quant_linear(x, base[name], None, bf16)
+            for i in range(5):
+                dst.copy_(src)
+                ops.quant_linear(x, layers[i % 2][name], None, bf16)
+            torch.cuda.synchronize()
+    print(json.dumps({"pmc_decode": ["qkv", "o"], "M": [32, 64], "calls": 5, "copy_bytes": COPY_BYTES}))
+    return 0
+
+
+def counters_summary(pmc_dir: Path) -> int:
+    """Each counter's mean value per dispatch, per kernel and grid size, over every
+    *counter_collection.csv under `pmc_dir` (one rocprofv3 --pmc pass each). Where the runs
+    hold the 256 MiB flush copies, FETCH_SIZE and WRITE_SIZE (KiB) are also given in bytes,
+    each scaled by what it reads for those copies, and TCP_TCC_READ_REQ_sum (L1 -> L2 read
+    requests) in bytes at the copy's bytes per request."""
+    table: dict[tuple[str, int], dict[str, list[float]]] = {}
+    flush: dict[str, list[float]] = {}
+    for path in sorted(pmc_dir.glob("**/*counter_collection.csv")):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                name, cname, value = row["Kernel_Name"], row["Counter_Name"], float(row["Counter_Value"])
+                key = (_kernel_short_name(name), int(row["Grid_Size"]))
+                table.setdefault(key, {}).setdefault(cname, []).append(value)
+                if "copy" in name.lower():
+                    flush.setdefault(cname, []).append(value)
+    # The flush copies are the largest copies of the runs (the others set up weight copies).
+    flush = {c: [v for v in vals if v >= 0.25 * max(vals)] for c, vals in flush.items() if max(vals) > 0}
+    scale = {}
+    if "FETCH_SIZE" in flush:
+        scale["FETCH_SIZE"] = COPY_BYTES / (statistics.median(flush["FETCH_SIZE"]) * 1024)
+    if "WRITE_SIZE" in flush:
+        scale["WRITE_SIZE"] = COPY_BYTES / (statistics.median(flush["WRITE_SIZE"]) * 1024)
+    per_req = COPY_BYTES / statistics.median(flush["TCP_TCC_READ_REQ_sum"]) if "TCP_TCC_READ_REQ_sum" in flush else 0
+    if scale or per_req:
+        print(f"# 256 MiB flush copies: FETCH_SIZE scale {scale.get('FETCH_SIZE', 0):.4f}, WRITE_SIZE scale "
+              f"{scale.get('WRITE_SIZE', 0):.4f}, {per_req:.1f} bytes per TCP_TCC_READ_REQ")
+    for (kname, grid), counters in sorted(table.items()):
+        calls = max(len(v) for v in counters.values())
+        print(f"{kname}  grid {grid}  dispatches {calls}")
+        for cname, vals in sorted(counters.items()):
+            mean = statistics.mean(vals)
+            extra = ""
+            if cname in scale:
+                extra = f"   = {mean * 1024 * scale[cname] / 1e6:10.2f} MB"
+            elif cname == "TCP_TCC_READ_REQ_sum" and per_req:
+                extra = f"   = {mean * per_req / 1e6:10.2f} MB read from L2"
+            print(f"    {cname:32s} {mean:16.1f}{extra}")
+    return 0
 
 
 def _kernel_short_name(name: str) -> str:

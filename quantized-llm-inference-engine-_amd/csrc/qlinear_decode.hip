@@ -882,9 +882,13 @@ struct LineGeom {
 // FMT = kByte: 8-bit codes. A block of 128 bytes per row is then one 128-code step, and lane
 // (col, kq) reads its 32 codes of the step as chunks 2kq and 2kq + 1 of row col; the byte
 // operands, flipped signs and zero-point offset are the one-shot kernel's.
-template <class Act, int NB, int D, int MMAX, int RM, int FMT = kNibble>
+// GS = 2: groups of 64 (nibble codes), as in the one-shot kernel: the step's code words
+// transposed across the wave's 16-lane rows, per-group accumulators, activation sums (MFMAs
+// against ones) and scales.
+template <class Act, int NB, int D, int MMAX, int RM, int FMT = kNibble, int GS = 1>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)))
     decode_line_kernel(const LinearArgs a) {
+  static_assert(GS == 1 || (GS == 2 && FMT == kNibble), "groups of 64: nibble codes");
   constexpr int SPB = FMT == kNibble ? 2 : 1;  // 128-code steps per block
   using Geo = LineGeom<NB, D, MMAX, SPB>;
   using Raw = typename Act::raw;
@@ -995,10 +999,12 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
   const uint32_t flip = flipped ? 0x80808080u : 0u;
   const float z_shift = Codes<Act, FMT>::kOffset + (flipped ? 128.0f : 0.0f);
   const float z_const = a.zero_const + z_shift;
-  const u32x4* const xrow = col < M ? xw + col * Geo::kRowPieces + kq * NM : zero4;
+  // Activation pieces 4 kq + j of a step (GS = 1), or 4 j + kq (GS = 2, the transposed words).
+  const u32x4* const xrow = col < M ? xw + col * Geo::kRowPieces + (GS == 1 ? kq * NM : kq) : zero4;
   const int xstep = col < M ? 4 * NM : 0;
-  const float* const srow = s_lds + col * mstride + step0;
-  const float* const zrow = z_lds + col * mstride + step0;
+  const int jstride = GS == 1 ? 1 : (col < M ? 4 : 0);
+  const float* const srow = s_lds + col * mstride + GS * step0;
+  const float* const zrow = z_lds + col * mstride + GS * step0;
   // Byte offset, within a block, of chunk 4h + kq of row col (nibbles: step h of the block), or
   // of chunk 2kq + h (bytes: half h of the lane's 32 codes of the block's one step).
   uint32_t rd_off[2];
@@ -1020,7 +1026,31 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
       const u32x4 w2 = FMT == kByte ? *reinterpret_cast<const u32x4*>(blk + rd_off[1]) : w;
       u32x4 xa[NM];
 #pragma unroll
-      for (int j = 0; j < NM; ++j) xa[j] = xrow[i * xstep + j];
+      for (int j = 0; j < NM; ++j) xa[j] = xrow[i * xstep + j * jstride];
+      if constexpr (GS == 2) {
+        const u32x4 ones = {Act::kOne2, Act::kOne2, Act::kOne2, Act::kOne2};
+        // Words of the step's codes, transposed: T[e] in row kq = word kq of row e.
+        const auto p02 = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
+        const auto p13 = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
+        const auto r01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+        const auto r23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+        const uint32_t tw[4] = {r01[0], r01[1], r23[0], r23[1]};
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          f32x4 v = {0.f, 0.f, 0.f, 0.f};
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 2 * g; j < 2 * g + 2; ++j) {
+            v = Mfma16<Act>::run(xa[j], ones, v);
+            acc = Mfma16<Act>::run(xa[j], nib.operand(tw[j]), acc);
+          }
+          const float sg = srow[2 * i + g];
+          const float zg = asym ? zrow[2 * i + g] + z_shift : z_const;
+#pragma unroll
+          for (int r = 0; r < RM; ++r) tot[r] = __builtin_fmaf(sg, __builtin_fmaf(-zg, v[r], acc[r]), tot[r]);
+        }
+        continue;
+      }
       float xs[RM];
       if constexpr (RM == 4) {
         const f32x4 v = *reinterpret_cast<const f32x4*>(xsum + i * 16 + 4 * kq);
@@ -2550,6 +2580,9 @@ bool try_oneshot_f32(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
   const int64_t tiles = (a.N + 15) / 16;
   if (tiles > 0x7FFFFFFF) return false;
+  // Two tokens (six piece rows) over 1024 tiles or more: the split into pieces and the decode
+  // kernels lead (gate_up at two tokens, groups of 64: 39.8 us here against 26 us).
+  if (a.M == 2 && tiles >= 1024) return false;
   const int64_t steps = a.K / 128;
   if (steps % 4 != 0 || steps / 4 > 16) return false;
   const int nw = int(steps / 4);
@@ -2563,10 +2596,10 @@ bool try_oneshot_f32(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   return true;
 }
 
-template <class Act, int NB, int D, int MMAX, int RM, int FMT>
+template <class Act, int NB, int D, int MMAX, int RM, int FMT, int GS>
 hipError_t launch_line_cfg(const LinearArgs& a, int nw, hipStream_t stream) {
   const size_t lds = LineGeom<NB, D, MMAX, FMT == kNibble ? 2 : 1>::lds_bytes(nw, a.G);
-  auto kernel = decode_line_kernel<Act, NB, D, MMAX, RM, FMT>;
+  auto kernel = decode_line_kernel<Act, NB, D, MMAX, RM, FMT, GS>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
@@ -2577,27 +2610,30 @@ hipError_t launch_line_cfg(const LinearArgs& a, int nw, hipStream_t stream) {
 }
 
 // One token only (try_line): the four-row forms would spill and are not instantiated.
-template <class Act, int NB, int D, int FMT>
+template <class Act, int NB, int D, int FMT, int GS>
 hipError_t launch_line_m(const LinearArgs& a, int nw, hipStream_t stream) {
   if (a.M != 1) return hipErrorInvalidValue;
-  return launch_line_cfg<Act, NB, D, 1, 1, FMT>(a, nw, stream);
+  return launch_line_cfg<Act, NB, D, 1, 1, FMT, GS>(a, nw, stream);
 }
 
-template <class Act, int FMT>
+template <class Act, int FMT, int GS = 1>
 hipError_t launch_line(const LinearArgs& a, int nb, int d, int nw, hipStream_t stream) {
-  if (nb == 2) return launch_line_m<Act, 2, 2, FMT>(a, nw, stream);
-  if (nb == 4) return d == 4 ? launch_line_m<Act, 4, 4, FMT>(a, nw, stream) : launch_line_m<Act, 4, 2, FMT>(a, nw, stream);
-  return d == 4 ? launch_line_m<Act, 8, 4, FMT>(a, nw, stream) : launch_line_m<Act, 8, 2, FMT>(a, nw, stream);
+  if (nb == 2) return launch_line_m<Act, 2, 2, FMT, GS>(a, nw, stream);
+  if (nb == 4)
+    return d == 4 ? launch_line_m<Act, 4, 4, FMT, GS>(a, nw, stream) : launch_line_m<Act, 4, 2, FMT, GS>(a, nw, stream);
+  return d == 4 ? launch_line_m<Act, 8, 4, FMT, GS>(a, nw, stream) : launch_line_m<Act, 8, 2, FMT, GS>(a, nw, stream);
 }
 
-// One token, 2/4-bit codes, group 128, rows of at least 8192 codes: the line-streaming kernel.
-// Measured on MI355X at one token: down (K 14336) 11.4 -> 9.2 us against the one-shot kernel;
-// on K = 4096 the two are within 2 %, and at 2-4 tokens the one-shot kernel leads.
+// One token, 2/4-bit codes in groups of 128 or 64 or 8-bit codes in groups of 128, rows of at
+// least 8192 codes: the line-streaming kernel. Measured on MI355X at one token: down (K 14336)
+// 11.4 -> 9.2 us against the one-shot kernel; on K = 4096 the two are within 2 %, and at 2-4
+// tokens the one-shot kernel leads.
 bool try_line(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.M != 1 || a.K < 8192) return false;
   const bool bytes = a.fmt == kByte;
+  const bool g64 = !bytes && a.group == 64;
   const int64_t block_k = bytes ? 128 : 256;  // codes per block of 128 bytes per row
-  if (a.group != 128 || a.K % block_k != 0 || a.G % 4 != 0) return false;
+  if ((a.group != 128 && !g64) || a.K % block_k != 0 || a.G % 4 != 0) return false;
   if (a.epilogue == kEpiSwiglu && a.N % 8 != 0) return false;
   if (a.ldq % 16 != 0 || reinterpret_cast<uintptr_t>(a.qw) % 16 != 0) return false;
   if (reinterpret_cast<uintptr_t>(a.x) % 16 != 0 || a.ldx % 8 != 0) return false;
@@ -2635,6 +2671,9 @@ bool try_line(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (bytes)
     *err = a.act == kDtBf16 ? launch_line<ActBf16, kByte>(a, nb, d, nw, stream)
                             : launch_line<ActF16, kByte>(a, nb, d, nw, stream);
+  else if (g64)
+    *err = a.act == kDtBf16 ? launch_line<ActBf16, kNibble, 2>(a, nb, d, nw, stream)
+                            : launch_line<ActF16, kNibble, 2>(a, nb, d, nw, stream);
   else
     *err = a.act == kDtBf16 ? launch_line<ActBf16, kNibble>(a, nb, d, nw, stream)
                             : launch_line<ActF16, kNibble>(a, nb, d, nw, stream);
@@ -2905,11 +2944,12 @@ KsPlan plan_ks(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   // serves them from fewer tokens and on any grid (the streaming and skinny kernels are the
   // alternative: down at 3-4 tokens 27 us there).
   // Groups of 64 (nibble codes): the multi-tile kernel takes 9-32 tokens, the skinny one 33-64;
-  // here from 9 tokens and on any grid as well.
+  // here from 9 tokens (3 on rows of K >= 8192: down at 3-4 tokens 15.0-16.0 -> 14.7-14.8 us,
+  // and the fp32 path's three piece rows of one token) and on any grid as well.
   const bool bytes = bits == 8;
   const bool g64 = group == 64 && !bytes;
   const bool wide = bytes || g64;  // no resident-activation or N-split form
-  const int64_t min_m = K >= 8192 ? (bytes ? 3 : 5) : (wide ? 9 : 17);
+  const int64_t min_m = K >= 8192 ? (bytes || g64 ? 3 : 5) : (wide ? 9 : 17);
   if (M > (g64 ? 32 : 64) || M < min_m || (group % 128 != 0 && !g64)) return p;
   const int64_t tiles = (N + 15) / 16;
   if ((tiles >= 1024 && !wide) || tiles < 1) return p;

@@ -100,14 +100,14 @@ def test_groups_of_32_never_take_the_decode_splits(lib):
         assert _ws(lib, m, DOWN, group=32) == 0
 
 
-@pytest.mark.parametrize("m", [1, 4, 5, 8, 9, 16, 32, 33, 64])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16, 32, 33, 64])
 def test_groups_of_64_take_k_slices_up_to_32_tokens(lib, m):
     # Groups of 64 (nibble codes) run on the K-sliced kernel with four groups per block: down
-    # (7 slices) from 5 tokens, K = 4096 (2 slices) from 9, on any grid; above 32 tokens the
+    # (7 slices) from 3 tokens, K = 4096 (2 slices) from 9, on any grid; above 32 tokens the
     # split-K GEMM's own plan.
     down, gate_up = _ws(lib, m, DOWN, group=64), _ws(lib, m, GATE_UP, group=64)
     if m <= 32:
-        assert down == (7 * m * 4096 * 4 if m >= 5 else 0)
+        assert down == (7 * m * 4096 * 4 if m >= 3 else 0)
         assert gate_up == (2 * m * 28672 * 4 if m >= 9 else 0)
     else:
         assert down % (m * 4096 * 4) == 0 and gate_up % (m * 28672 * 4) == 0
