@@ -29,6 +29,18 @@ int llmopt_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr
                    void* stream);
 
 /*
+ * llmopt_rmsnorm with a residual, whose x is a linear's K-split partial sums left by
+ * llmopt_q_linear_deferred: planes [splits][rows][hidden] fp32 (16-byte aligned), x = their sum
+ * in slice order plus bias ([hidden] of dtype, may be NULL), rounded to dtype; then h = residual
+ * + x and y = RMSNorm(h) as llmopt_rmsnorm computes them. Bit for bit llmopt_q_linear's
+ * split-K reduction followed by llmopt_rmsnorm (the residual add + RMSNorm of
+ * src/llmopt/model/layers.py:185-195 after the down projection), in one launch instead of two.
+ */
+int llmopt_rmsnorm_planes(const float* planes, int64_t splits, const void* bias, const void* residual, int64_t ldr,
+                          void* h_out, int64_t ldh, const void* weight, void* y, int64_t ldy, int64_t rows,
+                          int64_t hidden, float eps, int dtype, void* stream);
+
+/*
  * Rotary embedding of q and k at positions[t] (int64): out = x * cos + rotate_half(x) * sin,
  * rotate_half([a, b]) = [-b, a] over the two halves of each head; cos_table / sin_table are the
  * fp32 [table_rows, head_dim] tables, cast to dtype as the reference casts them. Replaces

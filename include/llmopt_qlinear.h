@@ -150,6 +150,24 @@ int llmopt_q_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void
                     void* stream);
 
 /*
+ * llmopt_q_linear whose K-split partial sums may be left for the consumer to add up. When the
+ * plan for these sizes is the K-sliced decode kernel with S > 1 slices (llmopt_q_linear_workspace
+ * reports S * M * N * 4 bytes), no reduction runs, y is left untouched, and *planes = S: the
+ * fp32 partial sums [S][M][N] (bias not added) sit at the start of the workspace, and
+ * llmopt_rmsnorm_planes (llmopt_model.h) adds them up inside the residual add + RMSNorm that
+ * follows. Otherwise *planes = 0 and y holds the result, as from llmopt_q_linear. 16-bit
+ * activations only defer (fp32 finishes as usual). The pair replaces the down projection's
+ * QuantLinear.forward and the next layer's residual add + RMSNorm
+ * (src/llmopt/quantization/quant_linear.py:110-113; src/llmopt/model/layers.py:185-195) with
+ * one launch fewer and the same bits.
+ */
+int llmopt_q_linear_deferred(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                             int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                             void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                             int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
+                             void* stream, int* planes);
+
+/*
  * llmopt_q_linear without a workspace argument and without any allocation: the K-split
  * partial sums that llmopt_q_linear keeps in the caller's workspace live in a static device
  * array of the library instead, llmopt_q_linear_noalloc_max_scratch() bytes (32 MiB) per

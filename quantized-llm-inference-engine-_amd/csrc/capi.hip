@@ -134,7 +134,9 @@ bool dense_first(int64_t M, int64_t N, int64_t K, int act, const void* workspace
 int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight, int64_t ldq,
                const float* scales, const float* zeros, const void* bias, void* y, int64_t N,
                int64_t ldy, int act_dtype, int bits, int group_size, int symmetric, int signed_codes,
-               void* workspace, size_t workspace_bytes, void* stream, int algo, int epilogue) {
+               void* workspace, size_t workspace_bytes, void* stream, int algo, int epilogue,
+               int* deferred = nullptr) {
+  if (deferred) *deferred = 0;
   if (!valid_dtype(act_dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", act_dtype);
   if (M < 0) return fail(LLMOPT_ERR_INVALID_ARG, "negative M=%lld", (long long)M);
   llmopt::LinearArgs a{};
@@ -157,6 +159,8 @@ int run_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qwe
   a.workspace = workspace;
   a.workspace_bytes = workspace ? workspace_bytes : 0;
   a.epilogue = epilogue;
+  a.defer_reduce = deferred != nullptr && epilogue == llmopt::kEpiNone && act_dtype != LLMOPT_DTYPE_F32;
+  a.deferred_planes = a.defer_reduce ? deferred : nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (K == 0 && epilogue == llmopt::kEpiNone) {
@@ -442,6 +446,17 @@ int llmopt_q_linear_swiglu(const void* x, int64_t M, int64_t K, int64_t ldx, con
                     LLMOPT_ALGO_AUTO, llmopt::kEpiSwiglu);
 }
 
+int llmopt_q_linear_deferred(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
+                             int64_t ldq, const float* scales, const float* zeros, const void* bias,
+                             void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
+                             int symmetric, int signed_codes, void* workspace, size_t workspace_bytes,
+                             void* stream, int* planes) {
+  if (!planes) return fail(LLMOPT_ERR_INVALID_ARG, "null planes pointer");
+  return run_linear(x, M, K, ldx, qweight, ldq, scales, zeros, bias, y, N, ldy, act_dtype, bits,
+                    group_size, symmetric, signed_codes, workspace, workspace_bytes, stream,
+                    LLMOPT_ALGO_AUTO, llmopt::kEpiNone, planes);
+}
+
 int llmopt_q_linear(const void* x, int64_t M, int64_t K, int64_t ldx, const void* qweight,
                     int64_t ldq, const float* scales, const float* zeros, const void* bias,
                     void* y, int64_t N, int64_t ldy, int act_dtype, int bits, int group_size,
@@ -679,6 +694,40 @@ int llmopt_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr
   a.rows = rows;
   a.hidden = hidden;
   a.ldx = ldx;
+  a.ldr = ldr;
+  a.ldh = ldh;
+  a.ldy = ldy;
+  a.eps = eps;
+  a.dtype = dtype;
+  return hip_status(llmopt::launch_rmsnorm(a, static_cast<hipStream_t>(stream)), "rmsnorm launch");
+}
+
+int llmopt_rmsnorm_planes(const float* planes, int64_t splits, const void* bias, const void* residual, int64_t ldr,
+                          void* h_out, int64_t ldh, const void* weight, void* y, int64_t ldy, int64_t rows,
+                          int64_t hidden, float eps, int dtype, void* stream) {
+  if (dtype != LLMOPT_DTYPE_BF16 && dtype != LLMOPT_DTYPE_F16)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "rmsnorm kernel: dtype %d (bf16 and fp16 only)", dtype);
+  if (rows < 0 || hidden < 1 || rows > 0x7FFFFFFF || splits < 1 || splits > 4096)
+    return fail(LLMOPT_ERR_INVALID_ARG, "bad rmsnorm shape");
+  if (rows == 0) return LLMOPT_OK;
+  if (!planes || !residual || !h_out || !weight || !y) return fail(LLMOPT_ERR_INVALID_ARG, "null rmsnorm pointer");
+  if (ldy < hidden || ldr < hidden || ldh < hidden)
+    return fail(LLMOPT_ERR_INVALID_ARG, "rmsnorm row stride below hidden=%lld", (long long)hidden);
+  auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (hidden % 8 || ldy % 8 || ldr % 8 || ldh % 8 || !aligned(planes) || !aligned(y) || !aligned(weight) ||
+      !aligned(residual) || !aligned(h_out))
+    return fail(LLMOPT_ERR_UNSUPPORTED, "rmsnorm kernel: needs hidden and row strides % 8 == 0, 16-byte aligned rows");
+  llmopt::RmsNormArgs a{};
+  a.planes = planes;
+  a.splits = splits;
+  a.plane_bias = bias;
+  a.residual = residual;
+  a.h_out = h_out;
+  a.weight = weight;
+  a.y = y;
+  a.rows = rows;
+  a.hidden = hidden;
+  a.ldx = hidden;
   a.ldr = ldr;
   a.ldh = ldh;
   a.ldy = ldy;

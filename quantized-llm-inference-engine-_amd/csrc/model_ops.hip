@@ -42,7 +42,7 @@ template <class Act>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const RmsNormArgs a) {
   using Raw = typename Act::raw;
   const int64_t row = blockIdx.x;
-  const Raw* x = static_cast<const Raw*>(a.x) + row * a.ldx;
+  const Raw* x = a.x ? static_cast<const Raw*>(a.x) + row * a.ldx : nullptr;
   const Raw* r = a.residual ? static_cast<const Raw*>(a.residual) + row * a.ldr : nullptr;
   Raw* h_out = a.h_out ? static_cast<Raw*>(a.h_out) + row * a.ldh : nullptr;
   Raw* y = static_cast<Raw*>(a.y) + row * a.ldy;
@@ -52,7 +52,30 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const RmsNormArgs a) {
   float ss = 0.0f;
   for (int64_t e = int64_t(tid) * 8; e < a.hidden; e += 256 * 8) {
     float h[8];
-    unpack8<Act>(*reinterpret_cast<const u32x4*>(x + e), h);
+    if (a.planes) {
+      // x = the partial sums added in slice order, plus the bias, rounded: the split-K
+      // reduction's arithmetic.
+      const size_t plane = size_t(a.rows) * size_t(a.hidden);
+      const float* p = a.planes + size_t(row) * size_t(a.hidden) + e;
+      f32x4 lo = *reinterpret_cast<const f32x4*>(p), hi = *reinterpret_cast<const f32x4*>(p + 4);
+      for (int64_t s = 1; s < a.splits; ++s) {
+        const f32x4 l2 = *reinterpret_cast<const f32x4*>(p + s * plane);
+        const f32x4 h2 = *reinterpret_cast<const f32x4*>(p + s * plane + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo[i] += l2[i];
+          hi[i] += h2[i];
+        }
+      }
+      const Raw* pb = static_cast<const Raw*>(a.plane_bias);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h[i] = Act::load(Act::store(pb ? lo[i] + Act::load(pb[e + i]) : lo[i]));
+        h[4 + i] = Act::load(Act::store(pb ? hi[i] + Act::load(pb[e + 4 + i]) : hi[i]));
+      }
+    } else {
+      unpack8<Act>(*reinterpret_cast<const u32x4*>(x + e), h);
+    }
     if (r) {
       float rv[8];
       unpack8<Act>(*reinterpret_cast<const u32x4*>(r + e), rv);
@@ -80,6 +103,68 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const RmsNormArgs a) {
     for (int i = 0; i < 8; ++i) o[i] = __fmul_rn(__fmul_rn(h[i], inv), wv[i]);
     *reinterpret_cast<u32x4*>(y + e) = pack8<Act>(o);
   }
+}
+
+// The same for rows of 512 to 8192 elements (hidden % 512 == 0): one thread per 8 elements,
+// hidden / 8 threads per row, h kept in registers between the two passes, every load of a row
+// issued before the first wait. Rows of a linear's partial sums (a.planes) read S planes per
+// element: one launch with all of them in flight instead of a reduction kernel and a norm.
+template <class Act>
+__global__ void __launch_bounds__(1024) rmsnorm_rows_kernel(const RmsNormArgs a) {
+  using Raw = typename Act::raw;
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t e = int64_t(tid) * 8;
+  const Raw* w = static_cast<const Raw*>(a.weight);
+  float h[8];
+  if (a.planes) {
+    const size_t plane = size_t(a.rows) * size_t(a.hidden);
+    const float* p = a.planes + size_t(row) * size_t(a.hidden) + e;
+    f32x4 lo = *reinterpret_cast<const f32x4*>(p), hi = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll 4
+    for (int64_t s = 1; s < a.splits; ++s) {
+      const f32x4 l2 = *reinterpret_cast<const f32x4*>(p + s * plane);
+      const f32x4 h2 = *reinterpret_cast<const f32x4*>(p + s * plane + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lo[i] += l2[i];
+        hi[i] += h2[i];
+      }
+    }
+    const Raw* pb = static_cast<const Raw*>(a.plane_bias);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = Act::load(Act::store(pb ? lo[i] + Act::load(pb[e + i]) : lo[i]));
+      h[4 + i] = Act::load(Act::store(pb ? hi[i] + Act::load(pb[e + 4 + i]) : hi[i]));
+    }
+  } else {
+    unpack8<Act>(*reinterpret_cast<const u32x4*>(static_cast<const Raw*>(a.x) + row * a.ldx + e), h);
+  }
+  if (a.residual) {
+    float rv[8];
+    unpack8<Act>(*reinterpret_cast<const u32x4*>(static_cast<const Raw*>(a.residual) + row * a.ldr + e), rv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = Act::load(Act::store(rv[i] + h[i]));
+    *reinterpret_cast<u32x4*>(static_cast<Raw*>(a.h_out) + row * a.ldh + e) = pack8<Act>(h);
+  }
+  float wv[8];
+  unpack8<Act>(*reinterpret_cast<const u32x4*>(w + e), wv);
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(h[i], h[i], ss);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  __shared__ float part[16];
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  const int nw = int(blockDim.x) >> 6;
+  float total = part[0];
+  for (int i = 1; i < nw; ++i) total += part[i];
+  const float inv = __frsqrt_rn(total / float(a.hidden) + a.eps);
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = __fmul_rn(__fmul_rn(h[i], inv), wv[i]);
+  *reinterpret_cast<u32x4*>(static_cast<Raw*>(a.y) + row * a.ldy + e) = pack8<Act>(o);
 }
 
 // Grid (token, chunk of 256 pairs); a thread per (head, i < D/2) pair rotates dims i and
@@ -135,6 +220,14 @@ __global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
 
 hipError_t launch_rmsnorm(const RmsNormArgs& a, hipStream_t stream) {
   if (a.rows == 0) return hipSuccess;
+  if (a.hidden % 512 == 0 && a.hidden <= 8192) {
+    const dim3 block(unsigned(a.hidden / 8));
+    if (a.dtype == kDtBf16)
+      hipLaunchKernelGGL(rmsnorm_rows_kernel<ActBf16>, dim3(unsigned(a.rows)), block, 0, stream, a);
+    else
+      hipLaunchKernelGGL(rmsnorm_rows_kernel<ActF16>, dim3(unsigned(a.rows)), block, 0, stream, a);
+    return hipGetLastError();
+  }
   if (a.dtype == kDtBf16)
     hipLaunchKernelGGL(rmsnorm_kernel<ActBf16>, dim3(unsigned(a.rows)), dim3(256), 0, stream, a);
   else

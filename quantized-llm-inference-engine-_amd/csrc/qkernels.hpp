@@ -34,6 +34,12 @@ struct LinearArgs {
   // bf16 pieces); only the decode kernels and the K-split reduction take it, with no bias
   // and no epilogue.
   int out_f32;
+  // Host side only. defer_reduce = 1: a K-sliced decode plan leaves its fp32 partial sums
+  // [slices][M][N] at the start of the workspace, launches no reduction, leaves y untouched and
+  // stores the slice count in *deferred_planes (which the caller zeroes first); other plans
+  // finish as usual. Only without an epilogue and with out_f32 = 0.
+  int defer_reduce;
+  int* deferred_planes;
 };
 enum : int { kEpiNone = 0, kEpiSwiglu = 1 };
 
@@ -121,6 +127,13 @@ struct RmsNormArgs {
   int64_t rows, hidden, ldx, ldr, ldh, ldy;
   float eps;
   int dtype;             // kDtBf16 or kDtF16
+  // Optional, in place of x (needs the residual): the K-sliced decode kernel's partial sums
+  // [splits][rows][hidden] fp32, x = their sum in slice order plus plane_bias ([hidden] of the
+  // activation dtype, may be null), rounded to the activation dtype -- the split-K reduction's
+  // result, bit for bit.
+  const float* planes;
+  int64_t splits;
+  const void* plane_bias;
 };
 hipError_t launch_rmsnorm(const RmsNormArgs& a, hipStream_t stream);
 

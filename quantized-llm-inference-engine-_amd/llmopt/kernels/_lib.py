@@ -70,6 +70,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int,
         [_p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, ctypes.c_float, _int, _p],
     ),
+    "llmopt_rmsnorm_planes": (
+        _int,
+        [_p, _i64, _p, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, ctypes.c_float, _int, _p],
+    ),
     "llmopt_rope": (
         _int,
         [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _p],
@@ -97,6 +101,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int,
         [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _int, _int, _int, _int, _int,
          _p, _size, _p],
+    ),
+    "llmopt_q_linear_deferred": (
+        _int,
+        [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64, _int, _int, _int, _int, _int,
+         _p, _size, _p, ctypes.POINTER(ctypes.c_int)],
     ),
     "llmopt_q_linear_noalloc": (
         _int,

@@ -20,6 +20,8 @@ library is missing or reports an error. Nothing here computes on the host.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from llmopt.kernels._lib import ALGO_AUTO, ALGO_DENSE, DTYPE_CODES, call, load_library
@@ -198,16 +200,43 @@ def dequantize(qt, dtype: torch.dtype = torch.float32) -> torch.Tensor:  # noqa:
     return out if native == dtype else out.to(dtype)
 
 
+class PartialSums:
+    """A linear's output left as the K-split partial sums of its decode kernel: ``planes``
+    ``[S, M, N]`` fp32 (the bias not added), ``bias`` (``[N]`` or None), the output ``dtype`` and
+    ``shape``. :func:`rmsnorm` with a residual adds them up inside its kernel;
+    :meth:`materialize` gives the output tensor, as the split-K reduction computes it."""
+
+    def __init__(self, planes: torch.Tensor, bias: torch.Tensor | None, dtype: torch.dtype,
+                 shape: tuple[int, ...]) -> None:
+        self.planes = planes
+        self.bias = bias
+        self.dtype = dtype
+        self.shape = torch.Size(shape)
+        self.device = planes.device
+
+    def materialize(self) -> torch.Tensor:
+        """The slices added in order, then the bias, rounded once: the reduction's arithmetic."""
+        v = self.planes[0]
+        for s in range(1, int(self.planes.shape[0])):
+            v = v + self.planes[s]
+        if self.bias is not None:
+            v = v + self.bias.float()
+        return v.to(self.dtype).view(self.shape)
+
+
 def quant_linear(
     x: torch.Tensor,
     qt,  # noqa: ANN001 - QuantizedTensor
     bias: torch.Tensor | None,
     compute_dtype: torch.dtype,
     algo: int = ALGO_AUTO,
-) -> torch.Tensor:
+    defer: bool = False,
+) -> torch.Tensor | PartialSums:
     """``F.linear(x, dequantize(qt, compute_dtype), bias)`` without a dense weight.
 
-    Raises the errors ``F.linear`` would raise for mismatched dtypes, devices or shapes.
+    Raises the errors ``F.linear`` would raise for mismatched dtypes, devices or shapes. With
+    ``defer`` (16-bit activations), a batch whose plan is the K-sliced decode kernel returns
+    its :class:`PartialSums` instead of the output (``llmopt_q_linear_deferred``).
     """
     if x.dtype != compute_dtype:
         raise RuntimeError(
@@ -248,6 +277,23 @@ def quant_linear(
                 lib.llmopt_q_linear_workspace_ex(m, rows, cols, int(qt.bits), group, DTYPE_CODES[compute_dtype])
             )
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+        if defer and algo == ALGO_AUTO and compute_dtype != torch.float32:
+            planes = ctypes.c_int(0)
+            call(
+                lib.llmopt_q_linear_deferred(
+                    x2.data_ptr(), m, cols, max(ldx, cols), qweight.data_ptr(), ldq, scales.data_ptr(),
+                    zeros.data_ptr() if zeros is not None else None, bias.data_ptr() if bias is not None else None,
+                    y.data_ptr(), rows, rows, DTYPE_CODES[compute_dtype], int(qt.bits), group,
+                    int(bool(qt.symmetric)), int(signed), ws.data_ptr() if ws is not None else None, ws_bytes,
+                    _stream_handle(x.device), ctypes.byref(planes),
+                ),
+                "llmopt_q_linear_deferred",
+            )
+            if planes.value:
+                s = int(planes.value)
+                pl = ws[: s * m * rows * 4].view(torch.float32).view(s, m, rows)
+                return PartialSums(pl, bias, compute_dtype, (*lead_shape, rows))
+            return y.reshape(*lead_shape, rows)
         call(
             lib.llmopt_q_linear_ex(
                 x2.data_ptr(),
@@ -476,8 +522,16 @@ def paged_decode_attention(
 # ---- decoder elementwise steps -------------------------------------------------------------------
 
 
-def rmsnorm_supported(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor | None = None) -> bool:
-    """Whether :func:`rmsnorm` takes these tensors (bf16/fp16 on a HIP device, 16-byte rows)."""
+def rmsnorm_supported(x: torch.Tensor | PartialSums, weight: torch.Tensor,
+                      residual: torch.Tensor | None = None) -> bool:
+    """Whether :func:`rmsnorm` takes these tensors (bf16/fp16 on a HIP device, 16-byte rows;
+    :class:`PartialSums` with a residual)."""
+    if isinstance(x, PartialSums):
+        return (residual is not None and residual.shape == x.shape and residual.dtype == x.dtype
+                and x.dtype in (torch.bfloat16, torch.float16) and weight.dtype == x.dtype
+                and int(x.shape[-1]) % 8 == 0 and weight.numel() == int(x.shape[-1]) and weight.is_contiguous()
+                and residual.is_contiguous() and residual.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0
+                and x.planes.data_ptr() % 16 == 0 and residual.device == x.device)
     if x.device.type != "cuda" or x.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != x.dtype:
         return False
     hidden = int(x.shape[-1]) if x.dim() else 0
@@ -489,10 +543,31 @@ def rmsnorm_supported(x: torch.Tensor, weight: torch.Tensor, residual: torch.Ten
     return all(t.data_ptr() % 16 == 0 and (t.dim() < 2 or t.stride(-1) == 1) for t in tensors)
 
 
-def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+def rmsnorm(x: torch.Tensor | PartialSums, weight: torch.Tensor, eps: float,
             residual: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
     """``(y, h)``: ``h = residual + x`` (rounded to the dtype; None without a residual) and
-    ``y = RMSNorm(h or x) * weight``, in one kernel (``layers.py:14-31,185-195``)."""
+    ``y = RMSNorm(h or x) * weight``, in one kernel (``layers.py:14-31,185-195``). ``x`` may be
+    a linear's :class:`PartialSums` (with a residual): the kernel adds them up first, bit for bit
+    as the split-K reduction would have."""
+    if isinstance(x, PartialSums):
+        if residual is None:
+            raise ValueError("partial sums need the residual add")
+        shape = x.shape
+        hidden = int(shape[-1])
+        r2 = residual.reshape(-1, hidden).contiguous()
+        rows = int(r2.shape[0])
+        y = torch.empty(rows, hidden, dtype=x.dtype, device=x.device)
+        h = torch.empty_like(y)
+        bias = x.bias.contiguous() if x.bias is not None else None
+        call(
+            load_library().llmopt_rmsnorm_planes(
+                x.planes.data_ptr(), int(x.planes.shape[0]), None if bias is None else bias.data_ptr(),
+                r2.data_ptr(), hidden, h.data_ptr(), hidden, weight.data_ptr(), y.data_ptr(), hidden, rows, hidden,
+                float(eps), DTYPE_CODES[x.dtype], _stream_handle(x.device),
+            ),
+            "llmopt_rmsnorm_planes",
+        )
+        return y.view(shape), h.view(shape)
     shape = x.shape
     hidden = int(shape[-1])
     x2 = x.reshape(-1, hidden)

@@ -52,15 +52,18 @@ class RMSNorm(nn.Module):
                 return ops.rmsnorm(x, self.weight, self.eps)[0]
         return self._reference(x)
 
-    def add_forward(self, x: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    def add_forward(self, x, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:  # noqa: ANN001
         """``(norm(h), h)`` with ``h = residual + x``: the residual add and the norm after it
-        (``layers.py:185-195``), one kernel on HIP devices."""
+        (``layers.py:185-195``), one kernel on HIP devices. ``x`` may be a linear's
+        ``PartialSums`` (:meth:`SwiGLUMLP.forward` with ``defer``), which the kernel adds up."""
         if self.fused_ops and _hip(x):
             from llmopt.kernels import ops
 
             if ops.rmsnorm_supported(x, self.weight, residual):
                 y, h = ops.rmsnorm(x, self.weight, self.eps, residual)
                 return y, h
+        if not isinstance(x, torch.Tensor):
+            x = x.materialize()
         h = residual + x
         return self._reference(h), h
 
@@ -86,10 +89,16 @@ class SwiGLUMLP(nn.Module):
         del self.gate_proj, self.up_proj
         return True
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, defer: bool = False):  # noqa: ANN201 - Tensor or ops.PartialSums
+        """With ``defer``, a quantized ``down_proj`` may return its K-split partial sums, for the
+        residual add + RMSNorm that follows to add up (:meth:`RMSNorm.add_forward`)."""
         if self.gate_up is not None:
-            return self.down_proj(self.gate_up(x))
-        return self.down_proj(torch.nn.functional.silu(self.gate_proj(x)) * self.up_proj(x))
+            h = self.gate_up(x)
+        else:
+            h = torch.nn.functional.silu(self.gate_proj(x)) * self.up_proj(x)
+        if defer and isinstance(self.down_proj, QuantLinear):
+            return self.down_proj.forward_deferred(h)
+        return self.down_proj(h)
 
 
 class PagedAttentionLayer(nn.Module):
@@ -235,18 +244,20 @@ class DecoderLayer(nn.Module):
                                                token_offsets, q_len)
         return hidden + mlp_out
 
-    def forward_chained(self, hidden: torch.Tensor, pending: torch.Tensor | None, positions: torch.Tensor,
+    def forward_chained(self, hidden: torch.Tensor, pending, positions: torch.Tensor,  # noqa: ANN001
                         cache: object | None = None, block_ids: torch.Tensor | None = None,
                         context_lens: torch.Tensor | None = None, token_offsets: torch.Tensor | None = None,
-                        q_len: int = 1) -> tuple[torch.Tensor, torch.Tensor]:
+                        q_len: int = 1, defer_mlp: bool = False) -> tuple[torch.Tensor, object]:
         """The layer with its final residual add left to the caller: takes ``hidden`` plus the
         previous layer's not-yet-added MLP output ``pending`` (or None) and returns ``(hidden,
         mlp_out)``. The input stream is ``hidden + pending``, formed inside the first norm's
-        kernel, so a stack of layers runs one fused add + norm per residual add."""
+        kernel, so a stack of layers runs one fused add + norm per residual add. With
+        ``defer_mlp`` the MLP output may be its down projection's partial sums, which the next
+        layer's first norm adds up (one launch fewer, the same bits)."""
         if pending is None:
             normed = self.input_layernorm(hidden)
         else:
             normed, hidden = self.input_layernorm.add_forward(pending, hidden)
         attn = self.self_attn(normed, positions, cache, block_ids, context_lens, token_offsets, q_len)
         normed, hidden = self.post_attention_layernorm.add_forward(attn, hidden)
-        return hidden, self.mlp(normed)
+        return hidden, self.mlp(normed, defer=defer_mlp)

@@ -47,6 +47,9 @@ class DecoderOnlyModel(nn.Module):
         self.layers = nn.ModuleList(DecoderLayer(config, i, backend) for i in range(config.num_hidden_layers))
         self.norm = RMSNorm(config.hidden_size, config.rms_norm_eps)
         self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        # False: every down projection finishes its own K-split reduction (the results are the
+        # same bits either way).
+        self.defer_reductions = True
         if config.tie_word_embeddings:
             self.lm_head.weight = self.embed_tokens.weight
         self.to(dtype or torch.float32)
@@ -63,10 +66,13 @@ class DecoderOnlyModel(nn.Module):
         positions = positions.reshape(-1)
         hidden = self.embed_tokens(input_ids)
         pending = None  # each layer's MLP output, added inside the next norm's kernel
-        for layer in self.layers:
+        last = len(self.layers) - 1
+        for i, layer in enumerate(self.layers):
+            # Every layer but the last may hand its down projection's partial sums to the next
+            # layer's first norm (the final norm takes the last layer's output rows).
             hidden, pending = layer.forward_chained(hidden, pending, positions, cache=cache, block_ids=block_ids,
                                                     context_lens=context_lens, token_offsets=token_offsets,
-                                                    q_len=q_len)
+                                                    q_len=q_len, defer_mlp=self.defer_reductions and i < last)
         seqs = int(hidden.shape[0]) // max(1, q_len)
         if last_only:
             # The residual add, RMSNorm and lm_head act row by row, so keeping only the last rows

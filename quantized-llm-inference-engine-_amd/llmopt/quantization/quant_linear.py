@@ -143,6 +143,16 @@ class QuantLinear(nn.Module):
             return ops.quant_linear(x, self.quantized_tensor(), self.bias, self.config.compute_dtype)
         return torch.nn.functional.linear(x, self._dequantized_weight(), self.bias)
 
+    def forward_deferred(self, x: torch.Tensor):  # noqa: ANN201 - Tensor or ops.PartialSums
+        """:meth:`forward`, except that on a HIP device a batch whose plan splits K over the
+        decode kernel's slices returns its ``PartialSums`` for a following residual add + RMSNorm
+        to add up (``ops.rmsnorm``); the result is the same, bit for bit."""
+        if x.device.type == "cuda" and not (self._forward_hooks or self._forward_pre_hooks):
+            from llmopt.kernels import ops
+
+            return ops.quant_linear(x, self.quantized_tensor(), self.bias, self.config.compute_dtype, defer=True)
+        return self(x)
+
     def extra_repr(self) -> str:
         return (
             f"in_features={self.in_features}, out_features={self.out_features}, "

@@ -126,6 +126,71 @@ def test_llama3_8b_width_decoder_end_to_end_prompt_batch(llama_two_layers):
     assert torch.equal(got.argmax(-1)[sure], exact.argmax(-1)[sure])
 
 
+@pytest.mark.timeout(900)
+def test_deferred_down_reductions_are_bit_identical(llama_two_layers):
+    # Layer 0's down projection at 32 decode tokens runs on the K-sliced kernel (seven slices);
+    # with deferred reductions its partial sums go to layer 1's first norm, which adds them up
+    # (llmopt_rmsnorm_planes) instead of a reduction kernel: every logit is the same bits.
+    from llmopt.kernels import ops
+    from llmopt.model import layers as model_layers
+
+    gpu, _ = llama_two_layers
+    g = torch.Generator().manual_seed(9)
+    prompts = torch.randint(0, 128256, (32, 8), generator=g)
+    forced = torch.randint(0, 128256, (32, 3), generator=g)
+    kinds = []
+    real_forward = model_layers.SwiGLUMLP.forward
+
+    def recording_forward(self, x, defer=False):
+        out = real_forward(self, x, defer=defer)
+        kinds.append(type(out).__name__)
+        return out
+
+    model_layers.SwiGLUMLP.forward = recording_forward
+    try:
+        gpu.defer_reductions = True
+        deferred = forced_logits(gpu, prompts, forced)
+        gpu.defer_reductions = False
+        plain = forced_logits(gpu, prompts, forced)
+    finally:
+        model_layers.SwiGLUMLP.forward = real_forward
+        gpu.defer_reductions = True
+    # Deferred: the decode steps' layer-0 MLP outputs are partial sums (three steps), the
+    # prefill's (256 rows) and layer 1's are tensors.
+    assert kinds[:8].count(ops.PartialSums.__name__) == 3, kinds
+    assert ops.PartialSums.__name__ not in kinds[8:], kinds
+    assert torch.equal(deferred, plain)
+
+
+@pytest.mark.parametrize("rows,with_bias", [(8, False), (32, True), (3, True)])
+def test_rmsnorm_planes_equal_reduction_then_rmsnorm(rows, with_bias):
+    # The C ABI pair: llmopt_q_linear_deferred leaves S planes, llmopt_rmsnorm_planes adds them
+    # up; against llmopt_q_linear (its own reduction) followed by llmopt_rmsnorm, bit for bit.
+    from llmopt.kernels import ops
+    from llmopt.quantization import RoundToNearestQuantizer
+
+    hidden, k = 4096, 14336
+    w = torch.randn(hidden, k, generator=torch.Generator().manual_seed(rows)) * 0.02
+    qt = RoundToNearestQuantizer(4, 128, False).quantize(w)
+    qt = type(qt)(qt.qweight.to(DEV), qt.scales.to(DEV), qt.zeros.to(DEV), 4, 128, False, qt.shape)
+    g = torch.Generator().manual_seed(rows + 1)
+    x = torch.randn(rows, k, generator=g).to(torch.bfloat16).to(DEV)
+    bias = (torch.randn(hidden, generator=g) * 0.1).to(torch.bfloat16).to(DEV) if with_bias else None
+    residual = torch.randn(rows, hidden, generator=g).to(torch.bfloat16).to(DEV)
+    weight = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(DEV)
+    part = ops.quant_linear(x, qt, bias, torch.bfloat16, defer=True)
+    y_plain = ops.quant_linear(x, qt, bias, torch.bfloat16)
+    if rows < 5:  # below the K-sliced kernel's 5 tokens on these rows: no slices to defer
+        assert isinstance(part, torch.Tensor) and torch.equal(part.view(torch.int16), y_plain.view(torch.int16))
+        return
+    assert isinstance(part, ops.PartialSums) and int(part.planes.shape[0]) == 7
+    assert torch.equal(part.materialize().view(torch.int16), y_plain.view(torch.int16))
+    got_y, got_h = ops.rmsnorm(part, weight, 1e-5, residual)
+    want_y, want_h = ops.rmsnorm(y_plain, weight, 1e-5, residual)
+    assert torch.equal(got_h.view(torch.int16), want_h.view(torch.int16))
+    assert torch.equal(got_y.view(torch.int16), want_y.view(torch.int16))
+
+
 @pytest.fixture(scope="module")
 def deep_narrow():
     cfg = dataclasses.replace(ModelConfig.tiny(), num_hidden_layers=32)

@@ -269,3 +269,19 @@ def test_harness_batches_follow_the_seeded_per_sample_draws():
     assert [r.tolist() for r in rows] == [[[97, 98, 99, 0, 0]], [[97, 98, 99, 100, 101]]]
     with pytest.raises(TypeError):
         CalibrationHarness().from_tokenizer(object(), ["x"])
+
+
+def test_partial_sums_materialize_in_slice_order_then_bias():
+    # PartialSums.materialize is the split-K reduction's arithmetic: slices added in order, then
+    # the bias, one rounding to the output dtype.
+    from llmopt.kernels.ops import PartialSums
+
+    g = torch.Generator().manual_seed(0)
+    planes = torch.randn(5, 3, 16, generator=g) * torch.tensor([1e8, 1.0, -1e8, 1e-3, 7.0]).view(5, 1, 1)
+    bias = torch.randn(16, generator=g).to(torch.bfloat16)
+    got = PartialSums(planes, bias, torch.bfloat16, (3, 16)).materialize()
+    v = planes[0]
+    for s in range(1, 5):
+        v = v + planes[s]
+    assert torch.equal(got.view(torch.int16), (v + bias.float()).to(torch.bfloat16).view(torch.int16))
+    assert got.shape == (3, 16) and got.dtype == torch.bfloat16
