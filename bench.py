@@ -1014,9 +1014,11 @@ def counters_summary(pmc_dir: Path) -> int:
     if "WRITE_SIZE" in flush:
         scale["WRITE_SIZE"] = COPY_BYTES / (statistics.median(flush["WRITE_SIZE"]) * 1024)
     per_req = COPY_BYTES / statistics.median(flush["TCP_TCC_READ_REQ_sum"]) if "TCP_TCC_READ_REQ_sum" in flush else 0
-    if scale or per_req:
-        print(f"# 256 MiB flush copies: FETCH_SIZE scale {scale.get('FETCH_SIZE', 0):.4f}, WRITE_SIZE scale "
-              f"{scale.get('WRITE_SIZE', 0):.4f}, {per_req:.1f} bytes per TCP_TCC_READ_REQ")
+    notes = [f"{c} scale {v:.4f}" for c, v in sorted(scale.items())]
+    if per_req:
+        notes.append(f"{per_req:.1f} bytes per TCP_TCC_READ_REQ")
+    if notes:
+        print("# 256 MiB flush copies: " + ", ".join(notes))
     for (kname, grid), counters in sorted(table.items()):
         calls = max(len(v) for v in counters.values())
         print(f"{kname}  grid {grid}  dispatches {calls}")
@@ -1060,24 +1062,33 @@ def trace_kernels(trace_csv: Path) -> int:
 
 def trace_runs(trace_csv: Path, min_launches: int = 8) -> int:
     """Summarise a rocprofv3 kernel trace of this script by runs: consecutive dispatches of
-    this library's kernels with the same main kernel (name, grid, workgroup) form one run -- one
-    timed block, e.g. one (projection, M) of the per-shape sweep -- and the split-K reductions
-    that follow a kernel are counted with it. Prints one line per run of at least
-    `min_launches` main-kernel dispatches: kernel, grid x workgroup, count, median and mean
-    kernel-only duration in microseconds."""
+    this library's kernels (and of hipBLASLt's, which its two-pass path and torch's dense
+    comparator launch) with the same main kernel (name, grid, workgroup) form one run -- one
+    timed block, e.g. one (projection, M) of the per-shape sweep. The split-K reductions that
+    follow a kernel and the dequantization that precedes a hipBLASLt GEMM are counted with it.
+    Prints one line per run of at least `min_launches` main-kernel dispatches: kernel, grid x
+    workgroup, count, median and mean kernel-only duration in microseconds."""
     short = _kernel_short_name
     with open(trace_csv, newline="") as f:
-        rows = sorted((r for r in csv.DictReader(f) if "llmopt" in r["Kernel_Name"]),
+        rows = sorted((r for r in csv.DictReader(f) if "llmopt" in r["Kernel_Name"] or "Cijk" in r["Kernel_Name"]),
                       key=lambda r: int(r["Start_Timestamp"]))
     runs: list[tuple[tuple, dict]] = []
-    for r in rows:
+    ahead: list[tuple[tuple, float]] = []  # a dequantization waiting for the GEMM after it
+    for i, r in enumerate(rows):
         block = int(r["Workgroup_Size_X"])
-        key = (short(r["Kernel_Name"]), int(r["Grid_Size_X"]) // block, block)
+        key = (short(r["Kernel_Name"])[:90], int(r["Grid_Size_X"]) // block, block)
         dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        nxt = rows[i + 1]["Kernel_Name"] if i + 1 < len(rows) else ""
+        if key[0].startswith("dequant_") and "Cijk" in nxt:
+            ahead.append((key, dur))
+            continue
         if not key[0].startswith("splitk_reduce") and (not runs or runs[-1][0] != key):
             runs.append((key, {}))
         if runs:
             runs[-1][1].setdefault(key, []).append(dur)
+            for k, d in ahead:
+                runs[-1][1].setdefault(k, []).append(d)
+            ahead.clear()
     for i, (main_key, kernels) in enumerate(runs):
         if len(kernels[main_key]) < min_launches:
             continue
