@@ -169,3 +169,26 @@ def test_swiglu_in_fp32(m):
     ref = torch.nn.functional.silu(g) * u
     assert y.dtype == torch.float32 and y.shape == (m, inter)
     assert _rel(y, ref) <= 1e-4
+
+
+@pytest.mark.parametrize("n,k", [(4096, 14336), (2048, 4096)])
+@pytest.mark.parametrize("group,symmetric", [(64, True), (128, False)])
+@pytest.mark.parametrize("m", [1, 2, 3, 6, 10])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_k_sliced_pieces(n, k, group, symmetric, m, with_bias):
+    # One to ten fp32 tokens whose piece rows the K-sliced kernel splits over K (long rows from
+    # one token, K = 4096 from 3 tokens in groups of 64 or 6 in groups of 128): the pieces, the
+    # K-sliced kernel with its reduction into fp32 sums, then the combining kernel.
+    qt = _host_qt(n, k, 4, group, symmetric, seed=m + n + group)
+    dqt = _to_device(qt)
+    gen = torch.Generator().manual_seed(m + 100)
+    x = torch.randn(m, k, generator=gen)
+    bias = torch.randn(n, generator=gen) if with_bias else None
+    xd = x.to(DEV)
+    y = ops.quant_linear(xd, dqt, None if bias is None else bias.to(DEV), torch.float32)
+    assert y.dtype == torch.float32 and y.shape == (m, n)
+    assert _rel(y, _f64_reference(xd, dqt, None if bias is None else bias.to(DEV))) <= F64_TOL
+    cols = np.sort(np.random.default_rng(m).choice(n, size=64, replace=False))
+    w = torch.from_numpy(np.ascontiguousarray(_oracle_dense(qt)[cols]))
+    ref = qo.reference_linear(x, w, None if bias is None else bias[torch.from_numpy(cols)])
+    assert _rel(y[:, torch.from_numpy(cols).to(DEV)].cpu(), ref) <= F32_TOL
