@@ -59,14 +59,12 @@ def _rel(y, ref):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("bits,symmetric,group", [(4, False, 128), (4, True, 64), (8, False, 128), (8, True, 32),
-                                                  (2, False, 16)])
-@pytest.mark.parametrize("n,k", [(48, 256), (200, 512), (64, 176), (96, 1024)])
+@pytest.mark.parametrize("bits,symmetric", [(4, False), (4, True), (8, False), (8, True), (2, False)])
+@pytest.mark.parametrize("n,k,group", [(48, 256, 128), (200, 512, 64), (64, 176, 16), (96, 1024, 32),
+                                       (80, 1024, 256)])
 @pytest.mark.parametrize("m", [1, 7, 200])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_dense_small_shapes(dtype, bits, symmetric, group, n, k, m, with_bias):
-    if k % group:
-        pytest.skip("group does not divide K")
+def test_dense_small_shapes(dtype, bits, symmetric, n, k, group, m, with_bias):
     qt = _host_qt(n, k, bits, group, symmetric, seed=n + k + bits + group)
     gen = torch.Generator().manual_seed(m + n)
     x = torch.randn(m, k, generator=gen).to(dtype)
