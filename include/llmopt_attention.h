@@ -70,6 +70,32 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
                                   const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
                                   float softcap, void* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * The attention layer's decode step in one launch: llmopt_rope_kv_write_decode (include/
+ * llmopt_model.h) followed by llmopt_paged_attention_decode. Replaces, for one token per
+ * sequence, the rotary step (apply_rotary_pos_emb), PagedKVCache.write_decode and
+ * PagedAttention.forward of the attention layer (src/llmopt/model/layers.py:118-140;
+ * src/llmopt/cache/paged_cache.py:246-277; src/llmopt/attention/paged_attention.py:145-182).
+ * q, k, v: the step's raw rows, [num_seqs, num_heads | kv_heads, head_dim] with token strides ldq,
+ * ldk, ldv elements, of dtype = the cache dtype (BF16 or F16). positions (int64), cos_table /
+ * sin_table ([table_rows, head_dim] fp32) and token_offsets (int32) as in
+ * llmopt_rope_kv_write_decode: the rotated k and v are stored at the slot of token_offsets[s].
+ * The cache, block table, context lengths, scale, softcap, out and workspace as in
+ * llmopt_paged_attention_decode (the same workspace query). The new token's key and value enter
+ * the softmax from registers, so the results are those of the two calls bit for bit whenever the
+ * slot a sequence writes is not also a key of another sequence of the call -- which holds for
+ * the reference's block pool, where only full (immutable) blocks are shared
+ * (src/llmopt/cache/block_pool.py:65-70).
+ */
+int llmopt_paged_attention_decode_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                                       int64_t ldv, const int64_t* positions, const float* cos_table,
+                                       const float* sin_table, int64_t table_rows, int dtype, void* key_cache,
+                                       void* value_cache, int64_t num_blocks, int64_t block_size, int64_t kv_heads,
+                                       int64_t head_dim, const int32_t* block_ids, int64_t ldb,
+                                       const int32_t* token_offsets, const int32_t* context_lens, int64_t num_seqs,
+                                       int64_t num_heads, float scale, float softcap, void* out, void* workspace,
+                                       size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -603,11 +603,18 @@ size_t llmopt_paged_attention_workspace(int64_t num_seqs, int64_t num_heads, int
   return size_t(plan.splits) * size_t(num_seqs) * size_t(num_heads) * size_t(head_dim + 1) * sizeof(float);
 }
 
-int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_stride, const void* key_cache,
-                                  const void* value_cache, int cache_dtype, int64_t num_blocks, int64_t block_size,
-                                  int64_t kv_heads, int64_t head_dim, const int32_t* block_ids, int64_t ldb,
-                                  const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
-                                  float softcap, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Checks and work split shared by the decode attention entry points; fills `a` (its launch fields
+// included) and returns LLMOPT_OK, or the error to return. num_seqs == 0 returns LLMOPT_OK with
+// a.num_seqs == 0 (nothing to launch).
+int prepare_paged_decode(llmopt::PagedDecodeArgs& a, const void* query, int q_dtype, int64_t q_seq_stride,
+                         const void* key_cache, const void* value_cache, int cache_dtype, int64_t num_blocks,
+                         int64_t block_size, int64_t kv_heads, int64_t head_dim, const int32_t* block_ids,
+                         int64_t ldb, const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
+                         float softcap, void* out, void* workspace, size_t workspace_bytes) {
   if (!valid_dtype(q_dtype) || !valid_dtype(cache_dtype))
     return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d / %d", q_dtype, cache_dtype);
   if (num_seqs < 0 || num_heads < 1 || kv_heads < 1 || num_heads % kv_heads != 0)
@@ -627,12 +634,12 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
     return fail(LLMOPT_ERR_UNSUPPORTED, "block table row of %lld blocks too long", (long long)ldb);
   if (q_seq_stride < num_heads * head_dim)
     return fail(LLMOPT_ERR_INVALID_ARG, "query row stride %lld < heads x head_dim", (long long)q_seq_stride);
+  a = llmopt::PagedDecodeArgs{};
   if (num_seqs == 0) return LLMOPT_OK;
   if (!query || !key_cache || !value_cache || !block_ids || !context_lens || !out)
     return fail(LLMOPT_ERR_INVALID_ARG, "null pointer argument");
   if (reinterpret_cast<uintptr_t>(key_cache) % 16 != 0 || reinterpret_cast<uintptr_t>(value_cache) % 16 != 0)
     return fail(LLMOPT_ERR_UNSUPPORTED, "caches must be 16-byte aligned");
-  llmopt::PagedDecodeArgs a{};
   a.query = query;
   a.q_dtype = q_dtype;
   a.q_seq_stride = q_seq_stride;
@@ -652,6 +659,8 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
   a.softcap = softcap;
   a.out = out;
   a.out_dtype = q_dtype;
+  const int64_t q_esize = q_dtype == LLMOPT_DTYPE_F32 ? 4 : 2;
+  a.q_vec = reinterpret_cast<uintptr_t>(query) % 16 == 0 && (q_seq_stride * q_esize) % 16 == 0;
   const DecodePlan plan = plan_decode(num_seqs, kv_heads, group, ldb, block_size);
   int splits = plan.splits;
   int64_t per = plan.tiles_per_split;
@@ -668,6 +677,62 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
     a.part_out = static_cast<float*>(workspace);
     a.part_lse = a.part_out + size_t(splits) * size_t(num_seqs) * size_t(num_heads) * size_t(head_dim);
   }
+  return LLMOPT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_stride, const void* key_cache,
+                                  const void* value_cache, int cache_dtype, int64_t num_blocks, int64_t block_size,
+                                  int64_t kv_heads, int64_t head_dim, const int32_t* block_ids, int64_t ldb,
+                                  const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, float scale,
+                                  float softcap, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  llmopt::PagedDecodeArgs a{};
+  const int rc = prepare_paged_decode(a, query, q_dtype, q_seq_stride, key_cache, value_cache, cache_dtype, num_blocks,
+                                      block_size, kv_heads, head_dim, block_ids, ldb, context_lens, num_seqs,
+                                      num_heads, scale, softcap, out, workspace, workspace_bytes);
+  if (rc != LLMOPT_OK || a.num_seqs == 0) return rc;
+  return hip_status(llmopt::launch_paged_decode(a, static_cast<hipStream_t>(stream)), "paged attention launch");
+}
+
+int llmopt_paged_attention_decode_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                                       int64_t ldv, const int64_t* positions, const float* cos_table,
+                                       const float* sin_table, int64_t table_rows, int dtype, void* key_cache,
+                                       void* value_cache, int64_t num_blocks, int64_t block_size, int64_t kv_heads,
+                                       int64_t head_dim, const int32_t* block_ids, int64_t ldb,
+                                       const int32_t* token_offsets, const int32_t* context_lens, int64_t num_seqs,
+                                       int64_t num_heads, float scale, float softcap, void* out, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  if (dtype != LLMOPT_DTYPE_BF16 && dtype != LLMOPT_DTYPE_F16)
+    return fail(LLMOPT_ERR_UNSUPPORTED, "fused rotary + decode attention: dtype %d (bf16 and fp16 only)", dtype);
+  if (table_rows < 1 || kv_heads < 1 || ldk < kv_heads * head_dim || ldv < kv_heads * head_dim)
+    return fail(LLMOPT_ERR_INVALID_ARG, "bad rotary table or k / v token stride");
+  llmopt::PagedDecodeArgs a{};
+  const int rc = prepare_paged_decode(a, q, dtype, ldq, key_cache, value_cache, dtype, num_blocks, block_size,
+                                      kv_heads, head_dim, block_ids, ldb, context_lens, num_seqs, num_heads, scale,
+                                      softcap, out, workspace, workspace_bytes);
+  if (rc != LLMOPT_OK || a.num_seqs == 0) return rc;
+  if (!k || !v || !positions || !cos_table || !sin_table || !token_offsets)
+    return fail(LLMOPT_ERR_INVALID_ARG, "null rotary / cache-write pointer");
+  auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (!a.q_vec || !aligned(k) || !aligned(v) || ldk % 8 != 0 || ldv % 8 != 0 || !aligned(cos_table) ||
+      !aligned(sin_table))
+    return fail(LLMOPT_ERR_UNSUPPORTED, "fused rotary + decode attention: q, k, v rows and the rotary tables must "
+                "be 16-byte aligned");
+  a.rope = 1;
+  a.new_k = k;
+  a.new_v = v;
+  a.ldk = ldk;
+  a.ldv = ldv;
+  a.positions = positions;
+  a.cos_table = cos_table;
+  a.sin_table = sin_table;
+  a.table_rows = table_rows;
+  a.offsets = token_offsets;
+  a.k_store = key_cache;
+  a.v_store = value_cache;
   return hip_status(llmopt::launch_paged_decode(a, static_cast<hipStream_t>(stream)), "paged attention launch");
 }
 

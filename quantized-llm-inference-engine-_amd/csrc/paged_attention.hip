@@ -33,6 +33,7 @@
 #include "qcommon.hpp"
 #include "qkernels.hpp"
 
+
 namespace llmopt {
 namespace {
 
@@ -150,7 +151,15 @@ struct Mfma16x16<ActF16> {
 //   (HD/16) col + i for MFMA i, i.e. one contiguous HD/16-dim piece of four V rows per lane.
 //   Lane l accumulates O[head col][dims (HD/16)(4kb + r) + i]: HD/4 contiguous dims of one head,
 //   so the per-head rescale of the online softmax needs no data from other lanes.
-template <class C, int HD, int GQ, int W>
+//
+// ROPE: the step's rotary embedding and cache write in the same launch (the reference's
+// apply_rotary_pos_emb, then PagedKVCache.write_decode, then the attention). Every lane rotates
+// its q dims and the new token's k dims (dims i and i + HD/2 are m and m + kNm/2 of one lane) with
+// the roundings of the rotary kernel; the first split's wave 0 stores k and v into the slot of
+// offsets[s]; and the tile that holds that token takes its key and value from these registers
+// instead of the cache, so no workgroup waits for the store. The slot a sequence writes must not be
+// a key of another sequence in the same call (a block being filled is never shared).
+template <class C, int HD, int GQ, int W, bool ROPE = false>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) paged_decode_kernel(const PagedDecodeArgs a) {
   constexpr int kNm = HD / 32;  // score MFMAs per tile (32 dims each)
   constexpr int kNv = HD / 16;  // P V MFMAs per tile; also V dims per lane per token
@@ -176,35 +185,127 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
 
   // Query heads kvh * GQ + col (col < GQ) as the B operand of the scores, cast to the cache dtype
   // (q.to(k.dtype)); columns >= GQ are zero. One branch on the dtype, then independent loads.
+  // ROPE: the group's rotated q heads and the rotated new key, [GQ + 1][HD] of the cache dtype.
+  __shared__ __align__(16) typename C::raw rot_lds[ROPE ? (GQ + 1) * HD : 8];
   u32x4 qf[kNm];
-  {
-    const bool hv = col < GQ;
-    const int64_t q0 = s * a.q_seq_stride + (kvh * GQ + (hv ? col : 0)) * HD + 8 * kb;
-    float x[kNm][8];
-    if (a.q_dtype == kDtF32) {
-      const float* q = static_cast<const float*>(a.query) + q0;
+  u32x4 knew[ROPE ? kNm : 1];     // the new key, dims 32m + 8kb .. + 8 (the K operand's order)
+  uint32_t vnew[ROPE ? kVw : 1];  // the new value, dims kNv col .. + kNv (the V operand's order)
+  int64_t off_new = -1;           // its position in the sequence
+  // The query (and with ROPE the new key and value): converted, rotated, in the operand order.
+  auto load_query = [&]() {
+    if constexpr (ROPE) {
+      // Each (head, pair i < HD/2) of the group's q heads and of the new k is rotated once per
+      // workgroup, one pair per thread, into LDS; the lanes then read their operand pieces.
+      using Raw = typename C::raw;
+      constexpr int kHalf = HD / 2;
+      int64_t p = a.positions[s];
+      p = p < 0 ? 0 : (p >= a.table_rows ? a.table_rows - 1 : p);  // the host checks the range
+      const Raw* qrow = static_cast<const Raw*>(a.query) + s * a.q_seq_stride + kvh * GQ * HD;
+      const Raw* krow = static_cast<const Raw*>(a.new_k) + s * a.ldk + kvh * HD;
+      const float* ct = a.cos_table + p * HD;
+      const float* st = a.sin_table + p * HD;
+      for (int j = int(threadIdx.x); j < (GQ + 1) * kHalf; j += 64 * W) {
+        const int h = j / kHalf;
+        const int i = j - h * kHalf;
+        const Raw* src = h < GQ ? qrow + h * HD : krow;
+        const float x1 = C::load(src[i]), x2 = C::load(src[i + kHalf]);
+        // The tables are cast to the activation dtype first (cos.to(q.dtype)); rotate_half(x) =
+        // [-x2, x1]; every product and the sum rounded as torch rounds them.
+        const float c1 = C::load(C::store(ct[i])), s1 = C::load(C::store(st[i]));
+        const float c2 = C::load(C::store(ct[i + kHalf])), s2 = C::load(C::store(st[i + kHalf]));
+        rot_lds[h * HD + i] = C::store(C::load(C::store(x1 * c1)) + C::load(C::store(-x2 * s1)));
+        rot_lds[h * HD + i + kHalf] = C::store(C::load(C::store(x2 * c2)) + C::load(C::store(x1 * s2)));
+      }
+      __syncthreads();
 #pragma unroll
-      for (int m = 0; m < kNm; ++m)
+      for (int m = 0; m < kNm; ++m) {
+        qf[m] = col < GQ ? *reinterpret_cast<const u32x4*>(rot_lds + col * HD + 32 * m + 8 * kb) : u32x4{0u, 0u, 0u, 0u};
+        knew[m] = *reinterpret_cast<const u32x4*>(rot_lds + GQ * HD + 32 * m + 8 * kb);
+      }
+      const Raw* vr = static_cast<const Raw*>(a.new_v) + s * a.ldv + kvh * HD + kNv * col;
+      if constexpr (kVw == 4) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(vr);
+        vnew[0] = w.x, vnew[1] = w.y, vnew[2] = w.z, vnew[3] = w.w;
+      } else {
+        const u32x2 w = *reinterpret_cast<const u32x2*>(vr);
+        vnew[0] = w.x, vnew[1] = w.y;
+      }
+      off_new = a.offsets[s];
+      // The cache write (paged_cache.py:246-277): block block_ids[s, off / B], replaced by block 0
+      // outside [0, num_blocks); an offset outside the table row writes nothing.
+      if (split == 0 && wave == 0) {
+        const int64_t index = off_new >= 0 ? off_new / a.block_size : -1;
+        if (index >= 0 && index < a.ldb) {
+          int64_t block = a.block_ids[s * a.ldb + index];
+          if (block < 0 || block >= a.num_blocks) block = 0;
+          const int64_t row = ((block * a.block_size + off_new % a.block_size) * a.kv_heads + kvh) * HD;
+          Raw* kd = static_cast<Raw*>(a.k_store) + row;
+          Raw* vd = static_cast<Raw*>(a.v_store) + row + kNv * col;
+          if (col == 0) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[m][e] = q[32 * m + e];
+            for (int m = 0; m < kNm; ++m) *reinterpret_cast<u32x4*>(kd + 32 * m + 8 * kb) = knew[m];
+          }
+          if (kb == 0) {
+            if constexpr (kVw == 4)
+              *reinterpret_cast<u32x4*>(vd) = u32x4{vnew[0], vnew[1], vnew[2], vnew[3]};
+            else
+              *reinterpret_cast<u32x2*>(vd) = u32x2{vnew[0], vnew[1]};
+          }
+        }
+      }
     } else {
-      const uint16_t* q = static_cast<const uint16_t*>(a.query) + q0;
-      const bool half = a.q_dtype == kDtF16;
+      const bool hv = col < GQ;
+      const int64_t q0 = s * a.q_seq_stride + (kvh * GQ + (hv ? col : 0)) * HD + 8 * kb;
+      float x[kNm][8];
+      // Eight consecutive dims per lane and m: one or two 16-byte loads when the rows are
+      // 16-byte aligned (a.q_vec, checked on the host), else element loads.
+      if (a.q_dtype == kDtF32) {
+        const float* q = static_cast<const float*>(a.query) + q0;
+        if (a.q_vec) {
 #pragma unroll
-      for (int m = 0; m < kNm; ++m)
+          for (int m = 0; m < kNm; ++m) {
+            const f32x4 v0 = *reinterpret_cast<const f32x4*>(q + 32 * m);
+            const f32x4 v1 = *reinterpret_cast<const f32x4*>(q + 32 * m + 4);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[m][e] = half ? f16_to_f32(q[32 * m + e]) : bf16_to_f32(q[32 * m + e]);
+            for (int e = 0; e < 4; ++e) x[m][e] = v0[e], x[m][e + 4] = v1[e];
+          }
+        } else {
+#pragma unroll
+          for (int m = 0; m < kNm; ++m)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[m][e] = q[32 * m + e];
+        }
+      } else {
+        const uint16_t* q = static_cast<const uint16_t*>(a.query) + q0;
+        const bool half = a.q_dtype == kDtF16;
+        auto cvt = [&](uint16_t h) { return half ? f16_to_f32(h) : bf16_to_f32(h); };
+        if (a.q_vec) {
+#pragma unroll
+          for (int m = 0; m < kNm; ++m) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(q + 32 * m);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              x[m][2 * e] = cvt(uint16_t(ws[e])), x[m][2 * e + 1] = cvt(uint16_t(ws[e] >> 16));
+          }
+        } else {
+#pragma unroll
+          for (int m = 0; m < kNm; ++m)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[m][e] = cvt(q[32 * m + e]);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < kNm; ++m) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = hv ? uint32_t(C::store(x[m][2 * e])) | (uint32_t(C::store(x[m][2 * e + 1])) << 16) : 0u;
+        qf[m] = u32x4{w[0], w[1], w[2], w[3]};
+      }
     }
-#pragma unroll
-    for (int m = 0; m < kNm; ++m) {
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = hv ? uint32_t(C::store(x[m][2 * e])) | (uint32_t(C::store(x[m][2 * e + 1])) << 16) : 0u;
-      qf[m] = u32x4{w[0], w[1], w[2], w[3]};
-    }
-  }
-
+  };
+  load_query();
   // Slot row (block * block_size + slot) of token t0 + col, or -1 when that token is not a key.
   // 32-bit arithmetic: contexts, table widths and slot rows stay below 2^31 (checked on the host).
   const uint32_t bsz = uint32_t(a.block_size);
@@ -257,8 +358,32 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
   for (int i = 0; i < kNv; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // One tile: scores, online softmax, P V, all on 64 lanes without LDS.
-  auto compute = [&](const u32x4* kf, const uint32_t (*vf)[kVw], uint32_t bits) {
+  // One tile (tokens t0 .. t0 + 15): scores, online softmax, P V, all on 64 lanes without LDS.
+  auto compute = [&](const u32x4* kf_in, const uint32_t (*vf_in)[kVw], uint32_t bits, int64_t t0) {
+    u32x4 kf[kNm];
+    uint32_t vf[4][kVw];
+#pragma unroll
+    for (int m = 0; m < kNm; ++m) kf[m] = kf_in[m];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int w = 0; w < kVw; ++w) vf[k][w] = vf_in[k][w];
+    if constexpr (ROPE) {
+      // The new token, when it is a key of this tile: its key and value from registers.
+      const int64_t rel = off_new - t0;
+      if (rel >= 0 && rel < 16 && ((bits >> rel) & 1u)) {
+        if (col == int(rel)) {
+#pragma unroll
+          for (int m = 0; m < kNm; ++m) kf[m] = knew[m];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (4 * kb + k == int(rel)) {
+#pragma unroll
+            for (int w = 0; w < kVw; ++w) vf[k][w] = vnew[w];
+          }
+      }
+    }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < kNm; ++m) acc = Mfma16x32<C>::run(kf[m], qf[m], acc);
@@ -327,7 +452,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   for (; g + kDepth <= n_tiles; g += kDepth) {
 #pragma unroll
     for (int u = 0; u < kDepth; ++u) {
-      compute(kf[u], vf[u], bits[u]);
+      compute(kf[u], vf[u], bits[u], tile_t0(g + u));
       const int32_t next = row_of(tile_t0(g + u + kDepth), rows[u]);
       rows[u] = fetch_block(tile_t0(g + u + 2 * kDepth));
       fetch_kv(next, kf[u], vf[u], bits[u]);
@@ -335,7 +460,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   }
 #pragma unroll
   for (int u = 0; u < kDepth; ++u)
-    if (g + u < n_tiles) compute(kf[u], vf[u], bits[u]);
+    if (g + u < n_tiles) compute(kf[u], vf[u], bits[u], tile_t0(g + u));
 
   // Lane l holds head col, dims (HD/4) kb + (HD/16) r + i, unnormalized, with the wave's running
   // max m_run and (after this sum) its running sum l_run of that head.
@@ -473,16 +598,25 @@ __global__ void __launch_bounds__(64) paged_merge_kernel(const PagedDecodeArgs a
     store_any(a.out, (s * a.num_heads + h) * HD + kDpl * lane + d, a.out_dtype, wsum > 0.0f ? acc[d] / wsum : 0.0f);
 }
 
-template <class C, int HD, int GQ>
+template <class C, int HD, int GQ, bool ROPE>
 void launch_decode_group(const PagedDecodeArgs& a, dim3 grid, hipStream_t stream) {
   switch (a.waves) {
-    case 1: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 1>), grid, dim3(64), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 2>), grid, dim3(128), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 4>), grid, dim3(256), 0, stream, a); break;
+    case 1: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 1, ROPE>), grid, dim3(64), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 2, ROPE>), grid, dim3(128), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 4, ROPE>), grid, dim3(256), 0, stream, a); break;
     default:
-      if constexpr (GQ < 16) hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 8>), grid, dim3(512), 0, stream, a);
+      if constexpr (GQ < 16)
+        hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 8, ROPE>), grid, dim3(512), 0, stream, a);
       break;
   }
+}
+
+template <class C, int HD, int GQ>
+void launch_decode_group(const PagedDecodeArgs& a, dim3 grid, hipStream_t stream) {
+  if (a.rope)
+    launch_decode_group<C, HD, GQ, true>(a, grid, stream);
+  else
+    launch_decode_group<C, HD, GQ, false>(a, grid, stream);
 }
 
 template <class C, int HD>

@@ -115,6 +115,23 @@ struct PagedDecodeArgs {
   int splits;
   int64_t tiles_per_split;  // 16-token tiles per split (per workgroup)
   int waves;                // waves per workgroup: 1, 2, 4 or 8 (8 only below 16 heads per KV head)
+  int q_vec;                // query rows 16-byte aligned: vector loads
+  // Rotary step in the same launch (rope != 0; query, caches and new rows all of cache_dtype):
+  // `query` holds the step's raw q rows; new_k / new_v the raw k and v rows [num_seqs, kv_heads,
+  // head_dim] (token strides ldk / ldv). q and k are rotated at positions[s] from the fp32
+  // tables, k and v are stored into the cache slot of offsets[s] (k_store / v_store: the same
+  // caches), and the new token's key and value enter the softmax from registers.
+  int rope;
+  const void* new_k;
+  const void* new_v;
+  int64_t ldk, ldv;
+  const int64_t* positions;
+  const float* cos_table;
+  const float* sin_table;
+  int64_t table_rows;
+  const int32_t* offsets;
+  void* k_store;
+  void* v_store;
 };
 hipError_t launch_paged_decode(const PagedDecodeArgs& a, hipStream_t stream);
 

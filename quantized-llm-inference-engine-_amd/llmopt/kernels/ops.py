@@ -38,6 +38,7 @@ __all__ = [
     "rmsnorm_supported",
     "rope",
     "rope_kv_write_decode",
+    "paged_decode_attention_rope",
     "unpack_nibbles",
 ]
 
@@ -517,6 +518,69 @@ def paged_decode_attention(
     )
     return out
 
+
+
+def paged_decode_attention_rope(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    positions: torch.Tensor,
+    cos_table: torch.Tensor,
+    sin_table: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_ids: torch.Tensor,
+    context_lens: torch.Tensor,
+    token_offsets: torch.Tensor,
+    scale: float,
+    softcap: float = 0.0,
+) -> torch.Tensor:
+    """The attention layer's decode step in one launch: :func:`rope_kv_write_decode` (rotate q
+    and k, store k and v at ``token_offsets``) then :func:`paged_decode_attention`, with the same
+    results. ``q [seqs, heads, d]`` and ``k``/``v [seqs, kv_heads, d]`` are the raw projection
+    rows (unit inner strides), in the cache dtype (bf16 or fp16); returns ``[seqs, heads, d]``.
+    Raises ``NotImplementedError`` where either kernel would (see :func:`paged_decode_attention`).
+    The slot a sequence writes must not be a key of another sequence in the same call."""
+    seqs, heads, d = (int(s) for s in q.shape)
+    kv_heads = int(k.shape[1])
+    nb, bs, kvh, hd, cdt = _layer_cache(key_cache, value_cache)
+    if q.dtype != key_cache.dtype or k.dtype != q.dtype or v.dtype != q.dtype or (kvh, hd) != (kv_heads, d) \
+            or tuple(v.shape) != tuple(k.shape):
+        raise ValueError("paged_decode_attention_rope: cache dtype/shape does not match q/k/v")
+    if int(k.shape[0]) != seqs or block_ids.dim() != 2:
+        raise ValueError("paged_decode_attention_rope: k/v need one row per query row, block_ids [seqs, blocks]")
+    _check_rows("paged_decode_attention_rope", seqs, positions=positions.reshape(-1),
+                token_offsets=token_offsets.reshape(-1), block_ids=block_ids, context_lens=context_lens.reshape(-1))
+
+    def inner_ok(t: torch.Tensor) -> bool:
+        return t.stride(2) == 1 and t.stride(1) == d
+
+    q, k, v = (t if inner_ok(t) else t.contiguous() for t in (q, k, v))
+    dev = key_cache.device
+    out = torch.empty(seqs, heads, d, dtype=q.dtype, device=dev)
+    if seqs == 0:
+        return out
+    pos = positions.to(device=dev, dtype=torch.int64).contiguous()
+    cos_t = cos_table.to(device=dev, dtype=torch.float32).contiguous()
+    sin_t = sin_table.to(device=dev, dtype=torch.float32).contiguous()
+    table = _int32(block_ids, dev)
+    offsets = _int32(token_offsets, dev)
+    lens = _int32(context_lens, dev)
+    ldb = int(table.shape[1])
+    lib = load_library()
+    ws_bytes = lib.llmopt_paged_attention_workspace(seqs, heads, kvh, hd, ldb, bs)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    call(
+        lib.llmopt_paged_attention_decode_rope(
+            q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), pos.data_ptr(),
+            cos_t.data_ptr(), sin_t.data_ptr(), int(cos_t.shape[0]), cdt, key_cache.data_ptr(),
+            value_cache.data_ptr(), nb, bs, kvh, hd, table.data_ptr(), ldb, offsets.data_ptr(), lens.data_ptr(),
+            seqs, heads, float(scale), float(softcap), out.data_ptr(), None if ws is None else ws.data_ptr(),
+            ws_bytes, _stream_handle(dev),
+        ),
+        "llmopt_paged_attention_decode_rope",
+    )
+    return out
 
 
 # ---- decoder elementwise steps -------------------------------------------------------------------

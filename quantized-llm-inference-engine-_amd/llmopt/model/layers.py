@@ -170,8 +170,20 @@ class PagedAttentionLayer(nn.Module):
         if self.fused_ops and _hip(q) and paged and q_len == 1 and self._fused_cache_write(cache, q):
             from llmopt.kernels import ops
 
-            # Decode: the rotary kernel stores k and v straight into the cache slots.
             self.rotary.check(positions)
+            if self.attn.backend == "hip":
+                # Decode: rotary step, cache write and attention in one launch.
+                try:
+                    out = ops.paged_decode_attention_rope(
+                        q.view(total, self.num_heads, self.head_dim),
+                        k.view(total, self.num_kv_heads, self.head_dim),
+                        v.view(total, self.num_kv_heads, self.head_dim), positions, self.rotary.cos_cached,
+                        self.rotary.sin_cached, cache.key_cache[self.layer_idx], cache.value_cache[self.layer_idx],
+                        block_ids, context_lens, offsets, self.attn.scale, self.attn.config.softcap)
+                    return self.o_proj(out.view(total, self.num_heads * self.head_dim))
+                except NotImplementedError:
+                    pass  # a shape outside the attention kernel: the rotary kernel, then the module
+            # Decode: the rotary kernel stores k and v straight into the cache slots.
             q = ops.rope_kv_write_decode(
                 q.view(total, self.num_heads, self.head_dim), k.view(total, self.num_kv_heads, self.head_dim),
                 v.view(total, self.num_kv_heads, self.head_dim), positions, self.rotary.cos_cached,

@@ -173,6 +173,13 @@ def test_cache_write_wrappers_reject_short_per_sequence_tensors():
     for name, (p, o, t, kk) in bad.items():
         with pytest.raises(ValueError):
             ops.rope_kv_write_decode(q, kk, kk.clone(), p, cos, cos, kc, vc, t, o)
+        with pytest.raises(ValueError):
+            ops.paged_decode_attention_rope(q, kk, kk.clone(), p, cos, cos, kc, vc, t, offs + 1, o, 0.125)
+    lens = offs + 1
+    with pytest.raises(ValueError):  # context lengths short
+        ops.paged_decode_attention_rope(q, k, k.clone(), pos, cos, cos, kc, vc, table, lens[:2], offs, 0.125)
+    with pytest.raises(ValueError):  # q in another dtype than the cache
+        ops.paged_decode_attention_rope(q.half(), k, k.clone(), pos, cos, cos, kc, vc, table, lens, offs, 0.125)
     with pytest.raises(ValueError):
         ops.kv_write_decode(kc, vc, table[:1], offs, k, k)
     with pytest.raises(ValueError):

@@ -104,6 +104,33 @@ def test_unsplit_launch_agrees_with_split():
     assert _rel(whole.float().cpu().numpy(), split.float().cpu().numpy().astype(np.float64)) <= 1e-2
 
 
+@pytest.mark.parametrize("q_dtype,code", [(torch.bfloat16, 2), (torch.float32, 0)])
+def test_unaligned_query_rows_take_element_loads(q_dtype, code):
+    """Query rows that are not 16-byte aligned (an odd element offset and row stride) are read
+    element by element; the output equals the aligned call's bit for bit."""
+    ctx, heads, kv_heads, head_dim, bs = [300, 41, 129], 16, 4, 128, 16
+    blocks = 64
+    cache = _filled_cache(blocks, bs, kv_heads, head_dim, torch.bfloat16, seed=12)
+    table = torch.from_numpy(_table(ctx, bs, 20, blocks, seed=12)).to(DEV)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=DEV)
+    stride = heads * head_dim + 3
+    buf = torch.randn(3 * stride + 8, device=DEV).to(q_dtype)
+    q_odd = buf[1 : 1 + 3 * stride].view(3, stride)[:, : heads * head_dim]
+    assert q_odd.data_ptr() % 16 != 0
+    aligned = ops.paged_decode_attention(q_odd.reshape(3, heads, head_dim).contiguous(), cache.key_cache[0],
+                                         cache.value_cache[0], table, lens, 0.1)
+    lib = _lib.load_library()
+    ws_bytes = lib.llmopt_paged_attention_workspace(3, heads, kv_heads, head_dim, 20, bs)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    odd = torch.empty(3, heads, head_dim, dtype=q_dtype, device=DEV)
+    rc = lib.llmopt_paged_attention_decode(
+        q_odd.data_ptr(), code, stride, cache.key_cache.data_ptr(), cache.value_cache.data_ptr(), 2, blocks, bs,
+        kv_heads, head_dim, table.data_ptr(), 20, lens.data_ptr(), 3, heads, ctypes.c_float(0.1), ctypes.c_float(0.0),
+        odd.data_ptr(), ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    assert torch.equal(odd, aligned)
+
+
 def test_softcap():
     ctx = [40, 90]
     cache = _filled_cache(16, 16, 2, 64, torch.float16, seed=9)
@@ -184,6 +211,112 @@ def test_decode_step_write_then_attend_at_llama_shape():
     last = [(table[s, (c - 1) // 16], (c - 1) % 16) for s, c in enumerate(ctx)]
     got = torch.stack([cache.key_cache[0, b, slot] for b, slot in last]).cpu()
     assert torch.equal(got, new_k)
+
+
+def _private_table(ctx, block_size, width, num_blocks, seed):
+    """Block tables drawn from blocks 1 .. num_blocks - 1 (block 0 is never a key), one block per
+    started block of each context plus one, -1 past that."""
+    rng = np.random.default_rng(seed)
+    free = list(rng.permutation(np.arange(1, num_blocks)))
+    table = np.full((len(ctx), width), -1, dtype=np.int32)
+    for s, length in enumerate(ctx):
+        n = min(-(-length // block_size) + 1, width)
+        table[s, :n] = [free.pop() for _ in range(n)]
+    return table
+
+
+def _rope_step(ctx, heads, kvh, d, bs, dtype, seed, offsets=None, table=None, softcap=0.0):
+    """Both ways of one decode step on the same inputs: rope_kv_write_decode then
+    paged_decode_attention, and paged_decode_attention_rope; returns both outputs and caches."""
+    from llmopt.model import RotaryEmbedding
+
+    seqs = len(ctx)
+    width = -(-max(max(ctx), 1) // bs) + 2
+    nb = seqs * width + 2
+    if table is None:
+        table = _private_table(ctx, bs, width, nb, seed)
+    gen = torch.Generator().manual_seed(seed)
+    fused = torch.randn(seqs, (heads + 2 * kvh) * d, generator=gen).to(dtype).to(DEV)
+    q = fused[:, : heads * d].view(seqs, heads, d)
+    k = fused[:, heads * d : (heads + kvh) * d].view(seqs, kvh, d)
+    v = fused[:, (heads + kvh) * d :].view(seqs, kvh, d)
+    offs = np.array(ctx) - 1 if offsets is None else np.array(offsets)
+    pos = torch.from_numpy(np.clip(offs, 0, None)).to(DEV)
+    rot = RotaryEmbedding(d, 4096, base=500000.0).to(DEV)
+    init_k = torch.randn(nb, bs, kvh, d, generator=gen).to(dtype).to(DEV)
+    init_v = torch.randn(nb, bs, kvh, d, generator=gen).to(dtype).to(DEV)
+    kc1, vc1 = init_k.clone(), init_v.clone()
+    kc2, vc2 = init_k.clone(), init_v.clone()
+    t = torch.from_numpy(table).to(DEV)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=DEV)
+    o = torch.from_numpy(offs.astype(np.int32)).to(DEV)
+    q1 = ops.rope_kv_write_decode(q, k, v, pos, rot.cos_cached, rot.sin_cached, kc1, vc1, t, o)
+    out1 = ops.paged_decode_attention(q1, kc1, vc1, t, lens, d**-0.5, softcap)
+    out2 = ops.paged_decode_attention_rope(q, k, v, pos, rot.cos_cached, rot.sin_cached, kc2, vc2, t, lens, o,
+                                           d**-0.5, softcap)
+    torch.cuda.synchronize()
+    return out1, out2, (kc1, vc1), (kc2, vc2), init_k
+
+
+ROPE_CASES = [  # (ctx, heads, kv_heads, head_dim, block_size, softcap)
+    (list(np.random.default_rng(11).integers(512, 641, size=32)), 32, 8, 128, 16, 0.0),
+    ([12, 20, 9], 4, 2, 64, 8, 0.0),
+    ([200, 75, 130, 1], 16, 1, 128, 16, 0.0),
+    ([64, 64, 3], 8, 8, 64, 32, 30.0),
+    ([2000], 16, 16, 128, 16, 0.0),  # the context in five splits, the new token in the last
+    ([513, 1, 240], 32, 4, 64, 8, 0.0),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", range(len(ROPE_CASES)))
+def test_fused_rope_attention_equals_rope_write_then_attend(case, dtype):
+    """The one-launch decode step returns the two calls' output bit for bit and leaves the same
+    caches (the new token's k and v at its slot)."""
+    ctx, heads, kvh, d, bs, softcap = ROPE_CASES[case]
+    out1, out2, c1, c2, init_k = _rope_step([int(c) for c in ctx], heads, kvh, d, bs, dtype, seed=case,
+                                            softcap=softcap)
+    assert out2.shape == (len(ctx), heads, d) and out2.dtype == dtype
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(c1[0], c2[0]) and torch.equal(c1[1], c2[1])
+    assert not torch.equal(c2[0], init_k)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_rope_attention_offsets_off_the_last_position(dtype):
+    """Offsets that are not context - 1: past the context (written, not a key), inside it (the key
+    at that position is replaced), past the table row or negative (nothing written), and a slot
+    whose block id is past the pool (written into block 0, which no sequence reads here)."""
+    ctx = [30, 17, 40, 5, 64, 33, 20]
+    offsets = [29, 20, 12, 4, 80, 32, -3]
+    bs, width, nb = 16, 5, 40
+    table = _private_table(ctx, bs, width, nb, seed=3)
+    table[5, 2] = nb + 7
+    out1, out2, c1, c2, _ = _rope_step(ctx, 8, 2, 128, bs, dtype, seed=4, offsets=offsets, table=table)
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(c1[0], c2[0]) and torch.equal(c1[1], c2[1])
+
+
+def test_fused_rope_attention_refuses_unaligned_rows():
+    """Rows off 16-byte alignment are refused before anything runs (NotImplementedError: the
+    attention layer then takes the rotary kernel and the attention kernel), caches untouched."""
+    from llmopt.model import RotaryEmbedding
+
+    seqs, heads, kvh, d, bs = 2, 8, 2, 128, 16
+    buf = torch.randn(seqs, (heads + 2 * kvh) * d + 1, device=DEV).to(torch.bfloat16)
+    q = buf[:, 1 : 1 + heads * d].view(seqs, heads, d)
+    k = buf[:, 1 + heads * d : 1 + (heads + kvh) * d].view(seqs, kvh, d)
+    v = buf[:, 1 + (heads + kvh) * d :].view(seqs, kvh, d)
+    kc = torch.zeros(8, bs, kvh, d, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    rot = RotaryEmbedding(d, 64, base=10000.0).to(DEV)
+    table = torch.tensor([[1, 2], [3, 4]], dtype=torch.int32, device=DEV)
+    lens = torch.tensor([5, 20], dtype=torch.int32, device=DEV)
+    with pytest.raises(NotImplementedError):
+        ops.paged_decode_attention_rope(q, k, v, (lens - 1).long(), rot.cos_cached, rot.sin_cached, kc, vc, table,
+                                        lens, lens - 1, d**-0.5)
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(kc)) == 0 and int(torch.count_nonzero(vc)) == 0
 
 
 def test_unsupported_shapes_fall_back_to_the_torch_sequence():

@@ -51,10 +51,10 @@ def test_decode_steps_run_the_attention_and_cache_kernels(models, monkeypatch):
     from llmopt.kernels import ops
 
     gpu, _ = models
-    calls = {"attn": 0, "write": 0, "rope_write": 0}
+    calls = {"attn": 0, "write": 0, "rope_write": 0, "rope_attn": 0}
     originals = {name: getattr(ops, fn) for name, fn in
                  (("attn", "paged_decode_attention"), ("write", "kv_write_decode"),
-                  ("rope_write", "rope_kv_write_decode"))}
+                  ("rope_write", "rope_kv_write_decode"), ("rope_attn", "paged_decode_attention_rope"))}
 
     def counting(name):
         def wrapped(*a, **k):
@@ -65,8 +65,9 @@ def test_decode_steps_run_the_attention_and_cache_kernels(models, monkeypatch):
     monkeypatch.setattr(ops, "paged_decode_attention", counting("attn"))
     monkeypatch.setattr(ops, "kv_write_decode", counting("write"))
     monkeypatch.setattr(ops, "rope_kv_write_decode", counting("rope_write"))
+    monkeypatch.setattr(ops, "paged_decode_attention_rope", counting("rope_attn"))
     prompts = torch.randint(0, 512, (2, 5), generator=torch.Generator().manual_seed(3))
     GreedyGenerator(gpu, use_graph=False).generate(prompts, 3)
     layers = len(gpu.layers)
-    # Each decode step's k and v go into the cache from the rotary kernel itself.
-    assert calls == {"attn": 2 * layers, "write": 0, "rope_write": 2 * layers}
+    # Each decode step's rotary step, cache write and attention run as one launch per layer.
+    assert calls == {"attn": 0, "write": 0, "rope_write": 0, "rope_attn": 2 * layers}
