@@ -78,6 +78,15 @@ int llmopt_rope_kv_write_decode(const void* q, int64_t ldq, const void* k, int64
                                 int64_t num_blocks, int64_t block_size, const int32_t* block_ids, int64_t ldb,
                                 const int32_t* token_offsets, void* stream);
 
+/*
+ * Greedy sampling's argmax of each row: out[r] = the index of the first maximum of row r of
+ * x ([rows, cols] of dtype F32 / F16 / BF16, row stride ldx elements), a NaN counting as larger
+ * than every number (the first NaN wins) -- torch.argmax(logits, dim=-1) of the reference's
+ * greedy sampler (src/llmopt/engine/sampler.py:94-95). out: int64 [rows] on the device.
+ */
+int llmopt_argmax_rows(const void* x, int dtype, int64_t rows, int64_t cols, int64_t ldx, int64_t* out,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -801,6 +801,26 @@ int llmopt_rmsnorm_planes(const float* planes, int64_t splits, const void* bias,
   return hip_status(llmopt::launch_rmsnorm(a, static_cast<hipStream_t>(stream)), "rmsnorm launch");
 }
 
+int llmopt_argmax_rows(const void* x, int dtype, int64_t rows, int64_t cols, int64_t ldx, int64_t* out,
+                       void* stream) {
+  if (!valid_dtype(dtype)) return fail(LLMOPT_ERR_INVALID_ARG, "bad dtype code %d", dtype);
+  if (rows < 0 || rows > 0x7FFFFFFF || cols < 1 || ldx < cols)
+    return fail(LLMOPT_ERR_INVALID_ARG, "bad argmax shape: rows %lld, cols %lld, ldx %lld", (long long)rows,
+                (long long)cols, (long long)ldx);
+  if (rows == 0) return LLMOPT_OK;
+  if (!x || !out) return fail(LLMOPT_ERR_INVALID_ARG, "null argmax pointer");
+  const int64_t esize = dtype == LLMOPT_DTYPE_F32 ? 4 : 2;
+  llmopt::ArgmaxArgs a{};
+  a.x = x;
+  a.dtype = dtype;
+  a.rows = rows;
+  a.cols = cols;
+  a.ldx = ldx;
+  a.vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (ldx * esize) % 16 == 0;
+  a.out = out;
+  return hip_status(llmopt::launch_argmax_rows(a, static_cast<hipStream_t>(stream)), "argmax launch");
+}
+
 int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, void* q_out,
                 void* k_out, void* v_out, const int64_t* positions, const float* cos_table, const float* sin_table,
                 int64_t table_rows, int64_t tokens, int64_t heads, int64_t kv_heads, int64_t head_dim, int dtype,

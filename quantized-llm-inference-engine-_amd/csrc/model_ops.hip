@@ -216,6 +216,84 @@ __global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
   }
 }
 
+// Greedy sampling's argmax over each row (the reference's greedy sampler, torch.argmax(logits,
+// dim=-1), src/llmopt/engine/sampler.py:94-95): the index of the first maximum, a NaN counting
+// as larger than every number (the first NaN wins), as torch returns it. One workgroup of 1024
+// threads per row; thread t takes the 8-element pieces t, t + 1024, ... of the row, sixteen loads
+// in flight at a time, then the workgroup combines the threads' winners.
+__device__ __forceinline__ bool argmax_gt(float a, float b) { return (a != a && b == b) || a > b; }
+
+__device__ __forceinline__ void argmax_take(float& v, int64_t& i, float v2, int64_t i2) {
+  if (argmax_gt(v2, v) || (!argmax_gt(v, v2) && i2 < i)) v = v2, i = i2;
+}
+
+template <class T>
+__device__ __forceinline__ float argmax_load(const void* x, int64_t idx, int dtype) {
+  if constexpr (sizeof(T) == 4) return static_cast<const float*>(x)[idx];
+  const uint16_t h = static_cast<const uint16_t*>(x)[idx];
+  return dtype == kDtF16 ? f16_to_f32(h) : bf16_to_f32(h);
+}
+
+template <class T>
+__global__ void __launch_bounds__(1024) argmax_rows_kernel(const ArgmaxArgs a) {
+  constexpr int kPer = 16 / sizeof(T);  // elements per 16-byte piece
+  constexpr int kAhead = 16;
+  const int64_t row = blockIdx.x;
+  const int tid = int(threadIdx.x);
+  const T* x = static_cast<const T*>(a.x) + row * a.ldx;
+  float best = -__int_as_float(0x7F800000);
+  int64_t at = INT64_MAX;
+  const int64_t pieces = a.vec ? a.cols / kPer : 0;
+  for (int64_t base = 0; base < pieces; base += 1024 * kAhead) {
+    u32x4 v[kAhead];
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const int64_t c = base + tid + 1024 * u;
+      v[u] = *reinterpret_cast<const u32x4*>(x + kPer * (c < pieces ? c : 0));
+    }
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const int64_t c = base + tid + 1024 * u;
+      const bool in = c < pieces;  // a predicate, not a branch: the loads above stay in flight together
+      const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        float f;
+        if constexpr (sizeof(T) == 4)
+          f = __uint_as_float(w[e]);
+        else {
+          const uint16_t h = uint16_t(w[e / 2] >> (16 * (e % 2)));
+          f = a.dtype == kDtF16 ? f16_to_f32(h) : bf16_to_f32(h);
+        }
+        // Pieces and their elements come in increasing index order: a strict comparison keeps
+        // the first of equal values.
+        const bool take = in && argmax_gt(f, best);
+        best = take ? f : best;
+        at = take ? kPer * c + e : at;
+      }
+    }
+  }
+  for (int64_t j = pieces * kPer + tid; j < a.cols; j += 1024) {  // the tail, or every element
+    const float f = argmax_load<T>(x, j, a.dtype);
+    if (argmax_gt(f, best)) best = f, at = j;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float v2 = __shfl_xor(best, off, 64);
+    const int64_t i2 = __shfl_xor(at, off, 64);
+    argmax_take(best, at, v2, i2);
+  }
+  __shared__ float wv[16];
+  __shared__ int64_t wi[16];
+  const int lane = tid & 63, wave = tid >> 6;
+  if (lane == 0) wv[wave] = best, wi[wave] = at;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < int(blockDim.x >> 6); ++w) argmax_take(best, at, wv[w], wi[w]);
+    a.out[row] = at == INT64_MAX ? 0 : at;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm(const RmsNormArgs& a, hipStream_t stream) {
@@ -242,6 +320,15 @@ hipError_t launch_rope(const RopeArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(rope_kernel<ActBf16>, grid, dim3(256), 0, stream, a);
   else
     hipLaunchKernelGGL(rope_kernel<ActF16>, grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows(const ArgmaxArgs& a, hipStream_t stream) {
+  if (a.rows == 0) return hipSuccess;
+  if (a.dtype == kDtF32)
+    hipLaunchKernelGGL(argmax_rows_kernel<float>, dim3(unsigned(a.rows)), dim3(1024), 0, stream, a);
+  else
+    hipLaunchKernelGGL(argmax_rows_kernel<uint16_t>, dim3(unsigned(a.rows)), dim3(1024), 0, stream, a);
   return hipGetLastError();
 }
 

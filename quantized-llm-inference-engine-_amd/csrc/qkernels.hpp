@@ -177,6 +177,15 @@ struct RopeArgs {
   int64_t ldb, num_blocks, block_size;
 };
 hipError_t launch_rope(const RopeArgs& a, hipStream_t stream);
+
+struct ArgmaxArgs {
+  const void* x;  // [rows, cols] of dtype, row stride ldx elements
+  int dtype;
+  int64_t rows, cols, ldx;
+  int vec;        // rows 16-byte aligned: 16-byte loads
+  int64_t* out;   // [rows]
+};
+hipError_t launch_argmax_rows(const ArgmaxArgs& a, hipStream_t stream);
 hipError_t launch_linear_generic(const LinearArgs& a, hipStream_t stream);
 // Decode and prefill report `fits = false` (and launch nothing) when the shape, alignment or
 // dtype is outside what the kernel handles.

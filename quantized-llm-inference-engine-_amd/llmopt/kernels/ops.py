@@ -39,6 +39,7 @@ __all__ = [
     "rope",
     "rope_kv_write_decode",
     "paged_decode_attention_rope",
+    "argmax_rows",
     "unpack_nibbles",
 ]
 
@@ -579,6 +580,28 @@ def paged_decode_attention_rope(
             ws_bytes, _stream_handle(dev),
         ),
         "llmopt_paged_attention_decode_rope",
+    )
+    return out
+
+
+def argmax_rows(x: torch.Tensor) -> torch.Tensor:
+    """``torch.argmax(x, dim=-1)`` of a 2-D device tensor (fp32 / fp16 / bf16, unit inner
+    stride) as one kernel: the first maximum of each row, NaN above every number; int64
+    ``[rows]``. The greedy sampler's step (``sampler.py:94-95``)."""
+    if x.dim() != 2 or x.dtype not in DTYPE_CODES:
+        raise ValueError(f"argmax_rows takes a 2-D fp32/fp16/bf16 tensor, got {tuple(x.shape)} {x.dtype}")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    rows, cols = (int(d) for d in x.shape)
+    out = torch.empty(rows, dtype=torch.long, device=x.device)
+    if rows == 0:
+        return out
+    if cols == 0:
+        raise ValueError("argmax_rows of an empty row")
+    call(
+        load_library().llmopt_argmax_rows(x.data_ptr(), DTYPE_CODES[x.dtype], rows, cols, max(x.stride(0), cols),
+                                          out.data_ptr(), _stream_handle(x.device)),
+        "llmopt_argmax_rows",
     )
     return out
 

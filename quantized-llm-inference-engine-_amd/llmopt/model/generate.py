@@ -35,6 +35,15 @@ class GenerationResult:
         return seqs * (steps - 2) / self.decode_seconds if steps > 2 and self.decode_seconds > 0 else 0.0
 
 
+def _argmax(logits: torch.Tensor) -> torch.Tensor:
+    """The greedy choice of each row: the argmax kernel on HIP devices, torch elsewhere."""
+    if logits.is_cuda and logits.dim() == 2 and logits.dtype in (torch.float32, torch.float16, torch.bfloat16):
+        from llmopt.kernels import ops
+
+        return ops.argmax_rows(logits)
+    return logits.argmax(-1)
+
+
 class GreedyGenerator:
     """Greedy decoding of a batch of equal-length prompts with ``model``.
 
@@ -81,7 +90,7 @@ class GreedyGenerator:
         logits = self.model(ids, pos, cache=cache, block_ids=table, context_lens=lens,
                             token_offsets=torch.zeros(seqs, dtype=torch.int32, device=dev), q_len=plen,
                             last_only=True).last_logits()
-        out[:, 0] = logits.argmax(-1)
+        out[:, 0] = _argmax(logits)
         self._sync()
         prefill_s = time.perf_counter() - t0
         prefill_logits = logits.float()
@@ -95,7 +104,7 @@ class GreedyGenerator:
         def step() -> None:
             lg = self.model(tok, pos, cache=cache, block_ids=table, context_lens=lens, q_len=1,
                             last_only=True).last_logits()
-            nxt.copy_(lg.argmax(-1))
+            nxt.copy_(_argmax(lg))
             pos.add_(1)
             lens.add_(1)
 

@@ -65,6 +65,9 @@ class DecoderOnlyModel(nn.Module):
         input_ids = input_ids.reshape(-1)
         positions = positions.reshape(-1)
         hidden = self.embed_tokens(input_ids)
+        if token_offsets is None and context_lens is not None and block_ids is not None:
+            # Where this step's tokens go in the cache: computed once here, not in every layer.
+            token_offsets = context_lens - q_len
         pending = None  # each layer's MLP output, added inside the next norm's kernel
         last = len(self.layers) - 1
         for i, layer in enumerate(self.layers):

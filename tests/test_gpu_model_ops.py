@@ -99,3 +99,29 @@ def test_rope_kv_write_decode_matches_rope_then_write(dtype):
     assert torch.equal(q1, q2)
     assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
     assert not torch.equal(kc2, init)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,cols", [(32, 128256), (3, 1001), (1, 8), (5, 7)])
+def test_argmax_rows_matches_torch(dtype, rows, cols):
+    """The greedy sampler's argmax (torch.argmax(logits, dim=-1), sampler.py:94-95): the first
+    maximum of each row, including ties, NaN (above every number, the first one wins), -inf
+    rows, a tail past the 16-byte pieces, and rows read element by element (odd stride)."""
+    g = torch.Generator().manual_seed(rows * cols)
+    x = torch.randn(rows, cols, generator=g).to(dtype)
+    if rows >= 3:
+        x[0] = 0.0  # all equal: index 0
+        x[1, cols // 3] = 50.0
+        x[1, cols // 2] = 50.0  # a tie: the first
+        x[2] = -float("inf")
+        if cols > 4:
+            x[2, cols - 2] = float("nan")
+            x[2, cols - 1] = float("nan")
+    want = torch.argmax(x, dim=-1)
+    got = ops.argmax_rows(x.to(DEV))
+    assert got.dtype == torch.long and torch.equal(got.cpu(), want)
+    assert torch.equal(got, torch.argmax(x.to(DEV), dim=-1))
+    wide = torch.zeros(rows, cols + 3, dtype=dtype)
+    wide[:, 1 : cols + 1] = x
+    odd = wide.to(DEV)[:, 1 : cols + 1]  # rows off 16-byte alignment
+    assert torch.equal(ops.argmax_rows(odd).cpu(), want)
