@@ -71,6 +71,25 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
                                   float softcap, void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Prefill attention (q_len query tokens per sequence) read in place from the paged cache, after
+ * this step's K/V were written. Replaces PagedAttention.forward with q_len > 1
+ * (src/llmopt/attention/paged_attention.py:145-182, 210-290: the gather, the padding + causal
+ * mask of _build_mask, and the dense or split softmax). Query token j of sequence s sits at
+ * position context_lens[s] - q_len + j and sees the keys t <= that position (t < context_lens[s],
+ * block id >= 0); a query with no keys gets zeros. query element (s, j, h, d) at
+ * s * q_seq_stride + j * q_tok_stride + h * q_head_stride + d (q_dtype); out likewise with the
+ * out_* strides, in q_dtype. Cache, table, scale, softcap and the supported shapes as in
+ * llmopt_paged_attention_decode.
+ */
+int llmopt_paged_attention_prefill(const void* query, int q_dtype, int64_t q_seq_stride, int64_t q_tok_stride,
+                                   int64_t q_head_stride, const void* key_cache, const void* value_cache,
+                                   int cache_dtype, int64_t num_blocks, int64_t block_size, int64_t kv_heads,
+                                   int64_t head_dim, const int32_t* block_ids, int64_t ldb,
+                                   const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, int64_t q_len,
+                                   float scale, float softcap, void* out, int64_t out_seq_stride,
+                                   int64_t out_tok_stride, int64_t out_head_stride, void* stream);
+
+/*
  * The attention layer's decode step in one launch: llmopt_rope_kv_write_decode (include/
  * llmopt_model.h) followed by llmopt_paged_attention_decode. Replaces, for one token per
  * sequence, the rotary step (apply_rotary_pos_emb), PagedKVCache.write_decode and

@@ -20,13 +20,21 @@ It restates, in numpy, what the reference computes:
   times V; query head ``h`` reads KV head ``h // (heads / kv_heads)`` (``:184-205``). A
   sequence with no valid key gives zeros (``:233-235``). Computed in float64: the reference's
   own fp16/bf16 intermediate roundings are what the GPU tests' tolerance covers.
+* ``paged_prefill_attention`` -- ``PagedAttention.forward`` for ``q_len`` query tokens per
+  sequence (``:145-182,210-250``): query token ``j`` sits at ``ctx - q_len + j`` and sees the
+  valid keys up to and including its own position (``_build_mask``, ``:210-229``); a query with
+  no key gives zeros (``nan_to_num``, ``:248-249``).
 * ``merge_states`` -- ``merge_states`` (``:30-56``), the log-sum-exp merge of the split path.
 
 Pinned by tests/test_attention_oracle.py: context length 1 returns that token's value exactly;
 identical keys give the mean of the values; a dominant key returns its value; agreement with
 torch's ``scaled_dot_product_attention`` in float64 (a library routine) with explicit GQA
 expansion and padding masks; the split path (``merge_states`` over chunks) equals the dense
-one; write -> gather round trips, including the block-0 substitution and the stop at -1.
+one; write -> gather round trips, including the block-0 substitution and the stop at -1. The
+prefill form: one query token at the last position equals the decode form; the first token of a
+prompt with no prefix returns the first value exactly; identical keys give the mean of the
+values up to each position; agreement with torch's ``scaled_dot_product_attention`` in float64
+with the causal + padding mask built independently from positions.
 """
 
 from __future__ import annotations
@@ -37,7 +45,8 @@ import numpy as np
 
 from oracle.quant_oracle import round_to_dtype
 
-__all__ = ["kv_gather", "kv_write", "kv_write_decode", "merge_states", "paged_decode_attention"]
+__all__ = ["kv_gather", "kv_write", "kv_write_decode", "merge_states", "paged_decode_attention",
+           "paged_prefill_attention"]
 
 
 def _cast(values: np.ndarray, dtype: str) -> np.ndarray:
@@ -123,6 +132,39 @@ def paged_decode_attention(query, key_cache, value_cache, layer, block_ids, cont
                 scores = np.tanh(scores / softcap) * softcap
             p = np.exp(scores - scores.max())
             out[s, h] = (p / p.sum()) @ v
+    return out
+
+
+def paged_prefill_attention(query, key_cache, value_cache, layer, block_ids, context_lens,
+                            scale=None, softcap=0.0, cache_dtype="float16"):
+    """paged_attention.py:145-182, 210-250 for ``q_len`` tokens per sequence, in float64.
+
+    query ``[seq, heads, q_len, head_dim]``; token ``j`` of sequence ``s`` sits at
+    ``context_lens[s] - q_len + j`` and attends to the valid keys at positions up to its own.
+    Returns ``[seq, heads, q_len, head_dim]`` float64.
+    """
+    seqs, heads, q_len, head_dim = query.shape
+    kv_heads = key_cache.shape[3]
+    group = heads // kv_heads
+    scale = head_dim ** -0.5 if scale is None else scale
+    q = _cast(query, cache_dtype).astype(np.float64)
+    keys, values, valid = kv_gather(key_cache, value_cache, layer, block_ids, context_lens)
+    out = np.zeros((seqs, heads, q_len, head_dim), dtype=np.float64)
+    for s in range(seqs):
+        for j in range(q_len):
+            pos = int(context_lens[s]) - q_len + j
+            mask = valid[s] & (np.arange(valid.shape[1]) <= pos)
+            if not mask.any():
+                continue
+            for h in range(heads):
+                g = h // group
+                k = keys[s, mask, g].astype(np.float64)
+                v = values[s, mask, g].astype(np.float64)
+                scores = (k @ q[s, h, j]) * scale
+                if softcap > 0:
+                    scores = np.tanh(scores / softcap) * softcap
+                p = np.exp(scores - scores.max())
+                out[s, h, j] = (p / p.sum()) @ v
     return out
 
 

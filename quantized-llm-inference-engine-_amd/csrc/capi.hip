@@ -697,6 +697,37 @@ int llmopt_paged_attention_decode(const void* query, int q_dtype, int64_t q_seq_
   return hip_status(llmopt::launch_paged_decode(a, static_cast<hipStream_t>(stream)), "paged attention launch");
 }
 
+int llmopt_paged_attention_prefill(const void* query, int q_dtype, int64_t q_seq_stride, int64_t q_tok_stride,
+                                   int64_t q_head_stride, const void* key_cache, const void* value_cache,
+                                   int cache_dtype, int64_t num_blocks, int64_t block_size, int64_t kv_heads,
+                                   int64_t head_dim, const int32_t* block_ids, int64_t ldb,
+                                   const int32_t* context_lens, int64_t num_seqs, int64_t num_heads, int64_t q_len,
+                                   float scale, float softcap, void* out, int64_t out_seq_stride,
+                                   int64_t out_tok_stride, int64_t out_head_stride, void* stream) {
+  if (q_len < 1 || q_len > 0x7FFFFFFF)
+    return fail(LLMOPT_ERR_INVALID_ARG, "prefill attention: q_len %lld", (long long)q_len);
+  if (q_tok_stride < 1 || q_head_stride < 1 || out_seq_stride < 1 || out_tok_stride < 1 || out_head_stride < 1)
+    return fail(LLMOPT_ERR_INVALID_ARG, "prefill attention: strides must be positive");
+  llmopt::PagedDecodeArgs a{};
+  const int rc = prepare_paged_decode(a, query, q_dtype, q_seq_stride, key_cache, value_cache, cache_dtype, num_blocks,
+                                      block_size, kv_heads, head_dim, block_ids, ldb, context_lens, num_seqs,
+                                      num_heads, scale, softcap, out, nullptr, 0);
+  if (rc != LLMOPT_OK || a.num_seqs == 0) return rc;
+  const int64_t esize = q_dtype == LLMOPT_DTYPE_F32 ? 4 : 2;
+  a.q_vec = a.q_vec && (q_tok_stride * esize) % 16 == 0 && (q_head_stride * esize) % 16 == 0;
+  a.q_len = q_len;
+  a.q_tok_stride = q_tok_stride;
+  a.q_head_stride = q_head_stride;
+  a.out_seq_stride = out_seq_stride;
+  a.out_tok_stride = out_tok_stride;
+  a.out_head_stride = out_head_stride;
+  // Waves per workgroup: the key tiles of the longest context (the table's width) in turns.
+  const int64_t tiles = (ldb * block_size + 15) / 16;
+  a.splits = 1;
+  a.waves = tiles >= 16 ? 4 : tiles >= 4 ? 2 : 1;
+  return hip_status(llmopt::launch_paged_prefill(a, static_cast<hipStream_t>(stream)), "prefill attention launch");
+}
+
 int llmopt_paged_attention_decode_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
                                        int64_t ldv, const int64_t* positions, const float* cos_table,
                                        const float* sin_table, int64_t table_rows, int dtype, void* key_cache,

@@ -159,8 +159,17 @@ struct Mfma16x16<ActF16> {
 // offsets[s]; and the tile that holds that token takes its key and value from these registers
 // instead of the cache, so no workgroup waits for the store. The slot a sequence writes must not be
 // a key of another sequence in the same call (a block being filled is never shared).
-template <class C, int HD, int GQ, int W, bool ROPE = false>
+//
+// PRE: prefill, q_len query tokens per sequence. The 16 columns of the B operand are kTpt = 16 / GQ
+// consecutive query tokens x the GQ heads of the KV head (column c: token j0 + c / GQ, head
+// c % GQ); workgroup x takes tokens j0 = x kTpt ..; key t enters column c's softmax iff it is a key
+// and t <= ctx - q_len + token (the reference's causal mask), and the workgroup reads the keys up
+// to its last token's position.
+template <class C, int HD, int GQ, int W, bool ROPE = false, bool PRE = false>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) paged_decode_kernel(const PagedDecodeArgs a) {
+  static_assert(!(ROPE && PRE), "the rotary step is a decode-step fusion");
+  constexpr int kNc = PRE ? 16 : GQ;  // columns of the B operand that carry queries
+  constexpr int kTpt = 16 / GQ;       // PRE: query tokens per workgroup
   constexpr int kNm = HD / 32;  // score MFMAs per tile (32 dims each)
   constexpr int kNv = HD / 16;  // P V MFMAs per tile; also V dims per lane per token
   constexpr int kVw = kNv / 2;  // 32-bit words of V per lane per token
@@ -170,8 +179,21 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   const int kb = lane >> 4;
   const int64_t split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
   const int64_t ctx = a.context_lens[s];
-  const int64_t t_begin = split * a.tiles_per_split * 16;
-  const int64_t t_end = ctx < t_begin + a.tiles_per_split * 16 ? ctx : t_begin + a.tiles_per_split * 16;
+  // PRE: this column's query token and head, and the last key position it sees (-1: none).
+  const int64_t j0 = PRE ? split * kTpt : 0;
+  const int64_t q_tok = PRE ? j0 + col / GQ : 0;
+  const bool q_ok = !PRE || q_tok < a.q_len;
+  const int64_t q_pos = PRE && q_ok ? ctx - a.q_len + q_tok : -1;
+  int64_t t_begin, t_end;
+  if constexpr (PRE) {
+    const int64_t last = j0 + kTpt < a.q_len ? j0 + kTpt : a.q_len;  // tokens j0 .. last - 1
+    const int64_t lim = ctx - a.q_len + last;                         // keys t < lim
+    t_begin = 0;
+    t_end = ctx < lim ? ctx : lim;
+  } else {
+    t_begin = split * a.tiles_per_split * 16;
+    t_end = ctx < t_begin + a.tiles_per_split * 16 ? ctx : t_begin + a.tiles_per_split * 16;
+  }
   // The workgroup's tiles are dealt to its waves in turn: wave w takes tiles w, w + W, ...
   auto tile_t0 = [&](int64_t j) -> int64_t { return t_begin + 16 * (wave + int64_t(W) * j); };
   const int64_t row_stride = a.kv_heads * HD;  // elements between two slots
@@ -254,8 +276,10 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
         }
       }
     } else {
-      const bool hv = col < GQ;
-      const int64_t q0 = s * a.q_seq_stride + (kvh * GQ + (hv ? col : 0)) * HD + 8 * kb;
+      const bool hv = PRE ? q_ok : col < GQ;
+      const int64_t q0 = PRE ? s * a.q_seq_stride + (q_ok ? q_tok : 0) * a.q_tok_stride +
+                                   (kvh * GQ + col % GQ) * a.q_head_stride + 8 * kb
+                             : s * a.q_seq_stride + (kvh * GQ + (hv ? col : 0)) * HD + 8 * kb;
       float x[kNm][8];
       // Eight consecutive dims per lane and m: one or two 16-byte loads when the rows are
       // 16-byte aligned (a.q_vec, checked on the host), else element loads.
@@ -397,7 +421,8 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     float tmax = neg_inf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      sc[r] = ((bits >> (4 * kb + r)) & 1u) ? sc[r] : neg_inf;
+      const bool key = ((bits >> (4 * kb + r)) & 1u) && (!PRE || t0 + 4 * kb + r <= q_pos);
+      sc[r] = key ? sc[r] : neg_inf;
       tmax = fmaxf(tmax, sc[r]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -469,15 +494,16 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   const int64_t h0 = kvh * GQ;
   const int64_t d0 = (HD / 4) * kb;
   if constexpr (W == 1) {
-    if (col >= GQ) return;
-    const int64_t h = h0 + col;
+    if (PRE ? !q_ok : col >= GQ) return;
+    const int64_t h = h0 + (PRE ? col % GQ : col);
     float v[4][kNv];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
       for (int i = 0; i < kNv; ++i) v[r][i] = l_run > 0.0f ? o[i][r] / l_run : 0.0f;
-    if (a.splits == 1) {
-      const int64_t base = (s * a.num_heads + h) * HD + d0;
+    if (PRE || a.splits == 1) {
+      const int64_t base = PRE ? s * a.out_seq_stride + q_tok * a.out_tok_stride + h * a.out_head_stride + d0
+                               : (s * a.num_heads + h) * HD + d0;
       if (a.out_dtype == kDtF32) {
         float* out = static_cast<float*>(a.out) + base;
 #pragma unroll
@@ -504,10 +530,10 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   } else {
     // Merge the W waves in LDS (the reference's merge_states over W parts): weights
     // exp(m_w - max m), then one (head, dim) element per thread.
-    __shared__ float m_lds[W][GQ];
-    __shared__ float l_lds[W][GQ];
-    __shared__ float o_lds[W][GQ][HD];
-    if (col < GQ) {
+    __shared__ float m_lds[W][kNc];
+    __shared__ float l_lds[W][kNc];
+    __shared__ float o_lds[W][kNc][HD];
+    if (col < kNc) {
       if (kb == 0) m_lds[wave][col] = m_run, l_lds[wave][col] = l_run;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
@@ -515,8 +541,9 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
         for (int i = 0; i < kNv; ++i) o_lds[wave][col][d0 + kNv * r + i] = o[i][r];
     }
     __syncthreads();
-    for (int e = int(threadIdx.x); e < GQ * HD; e += 64 * W) {
-      const int hh = e / HD, d = e % HD;
+    for (int e = int(threadIdx.x); e < kNc * HD; e += 64 * W) {
+      const int hh = e / HD, d = e % HD;  // hh: the column (PRE: token j0 + hh / GQ, head hh % GQ)
+      if (PRE && j0 + hh / GQ >= a.q_len) continue;
       float top = neg_inf;
 #pragma unroll
       for (int w = 0; w < W; ++w) top = fmaxf(top, m_lds[w][hh]);
@@ -531,9 +558,10 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
         }
       }
       const float val = lsum > 0.0f ? acc / lsum : 0.0f;
-      const int64_t h = h0 + hh;
-      if (a.splits == 1) {
-        const int64_t i = (s * a.num_heads + h) * HD + d;
+      const int64_t h = h0 + (PRE ? hh % GQ : hh);
+      if (PRE || a.splits == 1) {
+        const int64_t i = PRE ? s * a.out_seq_stride + (j0 + hh / GQ) * a.out_tok_stride + h * a.out_head_stride + d
+                              : (s * a.num_heads + h) * HD + d;
         if (a.out_dtype == kDtF32)
           static_cast<float*>(a.out)[i] = val;
         else if (a.out_dtype == kDtF16)
@@ -638,7 +666,38 @@ hipError_t launch_decode_hd(const PagedDecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <class C, int HD, int GQ>
+void launch_prefill_group(const PagedDecodeArgs& a, hipStream_t stream) {
+  constexpr int kTpt = 16 / GQ;
+  const dim3 grid(unsigned((a.q_len + kTpt - 1) / kTpt), unsigned(a.kv_heads), unsigned(a.num_seqs));
+  switch (a.waves) {
+    case 1: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 1, false, true>), grid, dim3(64), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 2, false, true>), grid, dim3(128), 0, stream, a); break;
+    default: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 4, false, true>), grid, dim3(256), 0, stream, a); break;
+  }
+}
+
+template <class C, int HD>
+hipError_t launch_prefill_hd(const PagedDecodeArgs& a, hipStream_t stream) {
+  switch (a.num_heads / a.kv_heads) {
+    case 1: launch_prefill_group<C, HD, 1>(a, stream); break;
+    case 2: launch_prefill_group<C, HD, 2>(a, stream); break;
+    case 4: launch_prefill_group<C, HD, 4>(a, stream); break;
+    case 8: launch_prefill_group<C, HD, 8>(a, stream); break;
+    case 16: launch_prefill_group<C, HD, 16>(a, stream); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_paged_prefill(const PagedDecodeArgs& a, hipStream_t stream) {
+  if (a.num_seqs == 0 || a.q_len == 0) return hipSuccess;
+  if (a.cache_dtype == kDtBf16)
+    return a.head_dim == 128 ? launch_prefill_hd<ActBf16, 128>(a, stream) : launch_prefill_hd<ActBf16, 64>(a, stream);
+  return a.head_dim == 128 ? launch_prefill_hd<ActF16, 128>(a, stream) : launch_prefill_hd<ActF16, 64>(a, stream);
+}
 
 hipError_t launch_kv_write(const KvWriteArgs& a, int64_t q_len, bool decode, hipStream_t stream) {
   if (a.num_seqs == 0 || q_len == 0) return hipSuccess;

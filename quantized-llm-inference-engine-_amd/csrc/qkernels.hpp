@@ -132,8 +132,16 @@ struct PagedDecodeArgs {
   const int32_t* offsets;
   void* k_store;
   void* v_store;
+  // Prefill (launch_paged_prefill): q_len query tokens per sequence at positions
+  // context_lens[s] - q_len + j, each seeing the keys up to its own position. query element
+  // (s, j, h, d) at s * q_seq_stride + j * q_tok_stride + h * q_head_stride + d; out likewise
+  // with the out_* strides.
+  int64_t q_len;
+  int64_t q_tok_stride, q_head_stride;
+  int64_t out_seq_stride, out_tok_stride, out_head_stride;
 };
 hipError_t launch_paged_decode(const PagedDecodeArgs& a, hipStream_t stream);
+hipError_t launch_paged_prefill(const PagedDecodeArgs& a, hipStream_t stream);
 
 struct RmsNormArgs {
   const void* x;         // [rows, hidden], row stride ldx

@@ -1,13 +1,13 @@
-"""Paged attention (``src/llmopt/attention/paged_attention.py``) with a gfx950 decode kernel.
+"""Paged attention (``src/llmopt/attention/paged_attention.py``) with gfx950 kernels.
 
 The reference gathers every sequence's K/V into one padded tensor, repeats each KV head for
 its query heads, and runs matmul, softmax and matmul (split into context chunks merged by
-log-sum-exp when the context is long). Here, for one query token per sequence on a HIP device
-(the decode step), :meth:`PagedAttention.forward` calls ``llmopt_paged_attention_decode``,
-which reads K/V from the cache blocks in place, once per KV head for all the query heads that
-share it, with the context split over workgroups and merged the same way. Other calls (a
-prefill chunk, host tensors, shapes the kernel does not take) run the reference's sequence in
-torch.
+log-sum-exp when the context is long). Here, on a HIP device, :meth:`PagedAttention.forward`
+calls ``llmopt_paged_attention_decode`` for one query token per sequence (the decode step) and
+``llmopt_paged_attention_prefill`` for more (a prefill chunk, with the causal mask): both read
+K/V from the cache blocks in place, once per KV head for all the query heads that share it, with
+an online softmax. Other calls (host tensors, shapes the kernels do not take) run the
+reference's sequence in torch.
 """
 
 from __future__ import annotations
@@ -123,17 +123,22 @@ class PagedAttention:
         q_len = query_lens if query_lens is not None else int(query.shape[2])
         if q_len == 0:
             return torch.zeros((seqs, self.num_heads, 0, self.head_dim), dtype=query.dtype, device=query.device)
-        if q_len == 1 and self.backend == "hip" and query.device.type == "cuda":
+        if self.backend == "hip" and query.device.type == "cuda":
             from llmopt.kernels import ops
 
             try:
-                out = ops.paged_decode_attention(
-                    query[:, :, 0, :], cache.key_cache[layer_idx], cache.value_cache[layer_idx], block_ids,
+                if q_len == 1:
+                    out = ops.paged_decode_attention(
+                        query[:, :, 0, :], cache.key_cache[layer_idx], cache.value_cache[layer_idx], block_ids,
+                        context_lens, self.scale, self.config.softcap,
+                    )
+                    return out.unsqueeze(2)
+                return ops.paged_prefill_attention(
+                    query[:, :, :q_len], cache.key_cache[layer_idx], cache.value_cache[layer_idx], block_ids,
                     context_lens, self.scale, self.config.softcap,
                 )
-                return out.unsqueeze(2)
             except NotImplementedError:
-                pass  # a shape outside the kernel: the torch sequence below
+                pass  # a shape outside the kernels: the torch sequence below
         keys, values, valid = cache.gather(layer_idx, block_ids, context_lens)
         k = keys.permute(0, 2, 1, 3)
         v = values.permute(0, 2, 1, 3)

@@ -89,6 +89,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
          ctypes.c_float, ctypes.c_float, _p, _p, _size, _p],
     ),
     "llmopt_argmax_rows": (_int, [_p, _int, _i64, _i64, _i64, _p, _p]),
+    "llmopt_paged_attention_prefill": (
+        _int,
+        [_p, _int, _i64, _i64, _i64, _p, _p, _int, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64,
+         ctypes.c_float, ctypes.c_float, _p, _i64, _i64, _i64, _p],
+    ),
     "llmopt_paged_attention_decode_rope": (
         _int,
         [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _i64, _int, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p,

@@ -40,6 +40,7 @@ __all__ = [
     "rope_kv_write_decode",
     "paged_decode_attention_rope",
     "argmax_rows",
+    "paged_prefill_attention",
     "unpack_nibbles",
 ]
 
@@ -519,6 +520,48 @@ def paged_decode_attention(
     )
     return out
 
+
+
+def paged_prefill_attention(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_ids: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    softcap: float = 0.0,
+) -> torch.Tensor:
+    """Prefill attention for ``query [seq, heads, q_len, head_dim]`` (any strides with a unit
+    inner stride) over one layer's paged caches, this step's K/V already written: query token j
+    sits at ``context_lens - q_len + j`` and sees the keys up to its own position. Returns
+    ``[seq, heads, q_len, head_dim]`` in the query's dtype -- a view of a ``[seq, q_len, heads,
+    head_dim]`` buffer, the layout the output projection reads. Raises ``NotImplementedError``
+    for shapes the kernel does not take (as :func:`paged_decode_attention`)."""
+    nb, bs, kvh, hd, cdt = _layer_cache(key_cache, value_cache)
+    if query.dim() != 4 or int(query.shape[3]) != hd:
+        raise ValueError(f"query of shape {tuple(query.shape)} does not match head_dim {hd}")
+    if query.dtype not in DTYPE_CODES:
+        raise TypeError(f"unsupported query dtype {query.dtype}")
+    seqs, heads, q_len = (int(d) for d in query.shape[:3])
+    dev = key_cache.device
+    q = query if query.stride(3) == 1 else query.contiguous()
+    out = torch.empty(seqs, q_len, heads, hd, dtype=query.dtype, device=dev)
+    view = out.permute(0, 2, 1, 3)
+    if seqs == 0 or q_len == 0:
+        return view
+    _check_rows("paged_prefill_attention", seqs, block_ids=block_ids, context_lens=context_lens.reshape(-1))
+    table = _int32(block_ids, dev)
+    lens = _int32(context_lens, dev)
+    call(
+        load_library().llmopt_paged_attention_prefill(
+            q.data_ptr(), DTYPE_CODES[q.dtype], q.stride(0), q.stride(2), q.stride(1), key_cache.data_ptr(),
+            value_cache.data_ptr(), cdt, nb, bs, kvh, hd, table.data_ptr(), int(table.shape[1]), lens.data_ptr(),
+            seqs, heads, q_len, float(scale), float(softcap), out.data_ptr(), q_len * heads * hd, heads * hd, hd,
+            _stream_handle(dev),
+        ),
+        "llmopt_paged_attention_prefill",
+    )
+    return view
 
 
 def paged_decode_attention_rope(

@@ -134,3 +134,54 @@ def test_multi_token_write_stops_at_the_first_hole():
     # sequence 1: positions 3..16 over blocks 4-7, then the row ends
     np.testing.assert_array_equal(kc2[0, 4, 3, 0], keys[1, 0, 0])
     np.testing.assert_array_equal(kc2[0, 7, :, 0], keys[1, 9:13, 0])
+
+
+def test_prefill_single_token_at_the_end_equals_decode():
+    kc, vc = _cache(blocks=32, seed=4)
+    ctx = [12, 20, 9]
+    table = _table(ctx, 4, 6)
+    q = np.random.default_rng(5).standard_normal((3, 4, 8)).astype(np.float32)
+    dec = ao.paged_decode_attention(q, kc, vc, 0, table, np.array(ctx), cache_dtype="float32")
+    pre = ao.paged_prefill_attention(q[:, :, None, :], kc, vc, 0, table, np.array(ctx), cache_dtype="float32")
+    np.testing.assert_array_equal(pre[:, :, 0], dec)
+
+
+def test_prefill_first_token_sees_only_the_first_key():
+    kc, vc = _cache(kv_heads=1, seed=6)
+    table = _table([7], 4, 2)
+    q = np.random.default_rng(7).standard_normal((1, 2, 7, 8)).astype(np.float32)
+    out = ao.paged_prefill_attention(q, kc, vc, 0, table, np.array([7]), cache_dtype="float32")
+    for h in range(2):
+        np.testing.assert_array_equal(out[0, h, 0], vc[0, table[0, 0], 0, 0].astype(np.float64))
+
+
+def test_prefill_identical_keys_average_the_values_up_to_each_position():
+    kc, vc = _cache(kv_heads=1, seed=8)
+    kc[:] = 0.5
+    ctx, q_len = 10, 6  # four cached tokens, then six new ones at positions 4..9
+    table = _table([ctx], 4, 3)
+    q = np.ones((1, 1, q_len, 8), dtype=np.float32)
+    out = ao.paged_prefill_attention(q, kc, vc, 0, table, np.array([ctx]), cache_dtype="float32")
+    vals = np.stack([vc[0, table[0, t // 4], t % 4, 0] for t in range(ctx)]).astype(np.float64)
+    for j in range(q_len):
+        np.testing.assert_allclose(out[0, 0, j], vals[: ctx - q_len + j + 1].mean(axis=0), rtol=1e-12)
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(4, 2), (8, 1)])
+def test_prefill_matches_torch_sdpa_with_causal_and_padding_masks(heads, kv_heads):
+    kc, vc = _cache(blocks=40, kv_heads=kv_heads, seed=heads)
+    ctx, q_len = [12, 20, 5], 5
+    table = _table(ctx, 4, 6)
+    table[1, 1] = -1  # tokens 4-7 of sequence 1 are not keys
+    q = np.random.default_rng(9).standard_normal((3, heads, q_len, 8)).astype(np.float32)
+    out = ao.paged_prefill_attention(q, kc, vc, 0, table, np.array(ctx), cache_dtype="float32")
+    keys, values, valid = ao.kv_gather(kc, vc, 0, table, np.array(ctx))
+    group = heads // kv_heads
+    k = torch.from_numpy(keys).double().permute(0, 2, 1, 3).repeat_interleave(group, dim=1)
+    v = torch.from_numpy(values).double().permute(0, 2, 1, 3).repeat_interleave(group, dim=1)
+    # Position of query j: ctx - q_len + j; key t is visible iff valid and t <= that position.
+    qpos = torch.tensor(ctx)[:, None] - q_len + torch.arange(q_len)[None, :]
+    causal = torch.arange(keys.shape[1])[None, None, :] <= qpos[:, :, None]
+    mask = (torch.from_numpy(valid)[:, None, :] & causal)[:, None]
+    want = torch.nn.functional.scaled_dot_product_attention(torch.from_numpy(q).double(), k, v, attn_mask=mask)
+    np.testing.assert_allclose(out, want.numpy(), rtol=1e-10, atol=1e-12)

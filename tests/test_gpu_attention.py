@@ -159,6 +159,65 @@ def test_module_uses_the_kernel_and_agrees_with_the_torch_sequence():
     assert _rel(fast.float().cpu().numpy(), slow.float().cpu().numpy().astype(np.float64)) <= 2e-2
 
 
+PREFILL_CASES = [  # (ctx, q_len, heads, kv_heads, head_dim, block_size, holes, softcap)
+    ([512, 512], 512, 32, 8, 128, 16, (), 0.0),  # Llama-3-8B heads, prompts with no prefix
+    ([40, 100, 13], 13, 4, 2, 64, 8, (), 0.0),  # a prefix before the 13 new tokens; a partial tile
+    ([300, 77], 64, 16, 1, 128, 16, [(0, 3)], 0.0),  # a hole in the prefix
+    ([33, 64], 33, 8, 8, 64, 32, (), 30.0),  # soft-capped scores, one query head per KV head
+    ([200], 100, 16, 16, 128, 16, (), 0.0),  # sixteen query heads per KV head: one token per tile
+    ([20, 9], 20, 32, 4, 64, 8, (), 0.0),  # context shorter than q_len: early tokens see no key
+]
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("q_dtype", [None, torch.float32])
+@pytest.mark.parametrize("case", range(len(PREFILL_CASES)))
+def test_prefill_attention_matches_oracle(case, q_dtype, cache_dtype):
+    ctx, q_len, heads, kv_heads, head_dim, bs, holes, softcap = PREFILL_CASES[case]
+    q_dtype = q_dtype or cache_dtype
+    width = -(-max(ctx) // bs) + 1
+    blocks = sum(-(-c // bs) for c in ctx) + 3
+    cache = _filled_cache(blocks, bs, kv_heads, head_dim, cache_dtype, seed=case)
+    table = _table(ctx, bs, width, blocks, seed=case, holes=holes)
+    g = torch.Generator().manual_seed(case + 17)
+    # [seq, q_len, heads, d] seen as [seq, heads, q_len, d], the layout the attention layer passes
+    q = torch.randn(len(ctx), q_len, heads, head_dim, generator=g).to(q_dtype)
+    query = q.to(DEV).permute(0, 2, 1, 3)
+    out = ops.paged_prefill_attention(query, cache.key_cache[0], cache.value_cache[0], torch.from_numpy(table).to(DEV),
+                                      torch.tensor(ctx).to(DEV), head_dim**-0.5, softcap)
+    assert out.shape == (len(ctx), heads, q_len, head_dim) and out.dtype == q_dtype
+    ref = ao.paged_prefill_attention(q.permute(0, 2, 1, 3).float().numpy(), cache.key_cache.float().cpu().numpy(),
+                                     cache.value_cache.float().cpu().numpy(), 0, table, np.array(ctx),
+                                     softcap=softcap, cache_dtype=NAMES[cache_dtype])
+    got = out.float().cpu().numpy()
+    assert _rel(got, ref) <= max(TOL[q_dtype], TOL[cache_dtype]), (case, cache_dtype, q_dtype)
+    no_key = ref == 0  # queries that see no key: exact zeros
+    assert not got[no_key.all(axis=-1)].any()
+    # A contiguous [seq, heads, q_len, d] query gives the same output bit for bit.
+    again = ops.paged_prefill_attention(query.contiguous(), cache.key_cache[0], cache.value_cache[0],
+                                        torch.from_numpy(table).to(DEV), torch.tensor(ctx).to(DEV), head_dim**-0.5,
+                                        softcap)
+    assert torch.equal(again, out)
+
+
+def test_prefill_module_uses_the_kernel_and_agrees_with_the_torch_sequence(monkeypatch):
+    ctx, q_len = [160, 96], 96
+    cache = _filled_cache(24, 16, 8, 128, torch.bfloat16, seed=21)
+    table = torch.from_numpy(_table(ctx, 16, 12, 24, seed=21)).to(DEV)
+    lens = torch.tensor(ctx, device=DEV)
+    q = torch.randn(2, 32, q_len, 128, device=DEV).to(torch.bfloat16)
+    calls = []
+    original = ops.paged_prefill_attention
+    monkeypatch.setattr(ops, "paged_prefill_attention", lambda *a, **k: calls.append(1) or original(*a, **k))
+    fast = PagedAttention(32, 8, 128, config=PagedAttentionConfig(block_size=16)).forward(q, cache, 0, table, lens)
+    slow = PagedAttention(32, 8, 128, config=PagedAttentionConfig(block_size=16), backend="sdpa").forward(
+        q, cache, 0, table, lens)
+    assert calls == [1]
+    assert fast.shape == slow.shape == (2, 32, q_len, 128) and fast.dtype == torch.bfloat16
+    # The torch sequence rounds scores, probabilities and partial outputs to bf16 on the way.
+    assert _rel(fast.float().cpu().numpy(), slow.float().cpu().numpy().astype(np.float64)) <= 2e-2
+
+
 @pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("src_dtype", [torch.float32, torch.bfloat16])
 def test_write_decode_bit_exact(cache_dtype, src_dtype):

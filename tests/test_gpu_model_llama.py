@@ -9,7 +9,9 @@
   oracle's dequantized weight (what ``QuantLinear`` caches and multiplies,
   src/llmopt/quantization/quant_linear.py:93-113), torch norms, rotary and gathered-cache
   attention (src/llmopt/model/layers.py, attention/paged_attention.py), run on the host.
-  Bound on the last-position logits, max|a - b| / max|b|: 1.5e-2 per decoder layer.
+  Bound on the last-position logits, max|a - b| / max|b|: 1.5e-2 per decoder layer (the
+  batch of 512-token prompts: no farther from float32 than the reference's own bf16 run, and
+  within twice that bound of it).
 * A deep, narrow decoder (32 layers, hidden 256): bf16 rounding differences grow with depth,
   so the HIP model is held to the accuracy of the reference's own bf16 computation: both are
   compared with the same reference run in float32, and the HIP model's error must stay within
@@ -92,12 +94,13 @@ def test_llama3_8b_width_decoder_end_to_end_prompt_batch(llama_two_layers):
     # through the fused projections and the prefill GEMMs, 512-token contexts in the paged
     # cache), then two teacher-forced decode steps; one decoder layer. Sequences are
     # independent, so the host reference runs three of them (first, middle, last), in bf16 as
-    # the reference computes and in float32. Over 512-token contexts the decode steps' bf16
-    # rounding differences (attention scores, probabilities, the cache) exceed the per-layer
-    # bound of short prompts for both paths, so the HIP model is held to the reference's own
-    # bf16 accuracy against float32, as for the deep decoder below, and the prefill logits to
-    # the per-layer bound (src/llmopt/model/modeling.py:88-131, model/layers.py:39-44,106-108,
-    # 142).
+    # the reference computes and in float32. Over 512-token contexts the bf16 rounding
+    # differences of the two paths' attention exceed the per-layer bound of short prompts: the
+    # reference rounds scores and probabilities to bf16 before the softmax and the P V product,
+    # the HIP kernels keep scores and the softmax in fp32. So every step (the prefill included)
+    # is held to the reference's own bf16 accuracy against float32, as for the deep decoder
+    # below, and within twice the per-layer bound of the reference's bf16 run
+    # (src/llmopt/model/modeling.py:88-131, model/layers.py:39-44,106-108,142).
     gpu, twin = llama_two_layers
     keep_gpu, keep_twin = gpu.layers, twin.layers
     gpu.layers, twin.layers = keep_gpu[:1], keep_twin[:1]
@@ -119,7 +122,7 @@ def test_llama3_8b_width_decoder_end_to_end_prompt_batch(llama_two_layers):
     print("32 x 512-token prompts, 1 layer, per step (prefill, decode...): HIP vs reference bf16",
           ["%.2e" % e for e in errs], "HIP vs fp32", ["%.2e" % e for e in e_hip],
           "reference bf16 vs fp32", ["%.2e" % e for e in e_ref], flush=True)
-    assert errs[0] <= PER_LAYER_BOUND, errs
+    assert e_hip[0] <= e_ref[0] + 2e-3, (e_hip, e_ref)  # the prefill: no farther from fp32
     assert max(e_hip) <= 2 * max(e_ref) + 2e-3, (e_hip, e_ref)
     assert max(errs) <= 2 * PER_LAYER_BOUND, errs
     sure = confident_positions(exact, 2 * (max(e_hip) + max(e_ref)) * float(exact.abs().max()))
