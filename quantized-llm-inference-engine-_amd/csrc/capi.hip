@@ -721,10 +721,9 @@ int llmopt_paged_attention_prefill(const void* query, int q_dtype, int64_t q_seq
   a.out_seq_stride = out_seq_stride;
   a.out_tok_stride = out_tok_stride;
   a.out_head_stride = out_head_stride;
-  // Waves per workgroup: the key tiles of the longest context (the table's width) in turns.
-  const int64_t tiles = (ldb * block_size + 15) / 16;
+  // Waves per workgroup, each with its own 16 / group query tokens over the same key tiles.
   a.splits = 1;
-  a.waves = tiles >= 16 ? 4 : tiles >= 4 ? 2 : 1;
+  a.waves = q_len >= 64 ? 4 : q_len >= 16 ? 2 : 1;
   return hip_status(llmopt::launch_paged_prefill(a, static_cast<hipStream_t>(stream)), "prefill attention launch");
 }
 

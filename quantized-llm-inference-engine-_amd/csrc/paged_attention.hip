@@ -162,9 +162,10 @@ struct Mfma16x16<ActF16> {
 //
 // PRE: prefill, q_len query tokens per sequence. The 16 columns of the B operand are kTpt = 16 / GQ
 // consecutive query tokens x the GQ heads of the KV head (column c: token j0 + c / GQ, head
-// c % GQ); workgroup x takes tokens j0 = x kTpt ..; key t enters column c's softmax iff it is a key
-// and t <= ctx - q_len + token (the reference's causal mask), and the workgroup reads the keys up
-// to its last token's position.
+// c % GQ); wave w of workgroup x takes tokens j0 = (x W + w) kTpt .. and every key tile up to its
+// last token's position, so the W waves walk the same key tiles together (their loads meet in the
+// CU's L1) and each stores its own columns. Key t enters column c's softmax iff it is a key and
+// t <= ctx - q_len + token (the reference's causal mask).
 template <class C, int HD, int GQ, int W, bool ROPE = false, bool PRE = false>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) paged_decode_kernel(const PagedDecodeArgs a) {
   static_assert(!(ROPE && PRE), "the rotary step is a decode-step fusion");
@@ -180,7 +181,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   const int64_t split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
   const int64_t ctx = a.context_lens[s];
   // PRE: this column's query token and head, and the last key position it sees (-1: none).
-  const int64_t j0 = PRE ? split * kTpt : 0;
+  const int64_t j0 = PRE ? (split * W + wave) * kTpt : 0;
   const int64_t q_tok = PRE ? j0 + col / GQ : 0;
   const bool q_ok = !PRE || q_tok < a.q_len;
   const int64_t q_pos = PRE && q_ok ? ctx - a.q_len + q_tok : -1;
@@ -195,7 +196,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
     t_end = ctx < t_begin + a.tiles_per_split * 16 ? ctx : t_begin + a.tiles_per_split * 16;
   }
   // The workgroup's tiles are dealt to its waves in turn: wave w takes tiles w, w + W, ...
-  auto tile_t0 = [&](int64_t j) -> int64_t { return t_begin + 16 * (wave + int64_t(W) * j); };
+  auto tile_t0 = [&](int64_t j) -> int64_t { return PRE ? 16 * j : t_begin + 16 * (wave + int64_t(W) * j); };
   const int64_t row_stride = a.kv_heads * HD;  // elements between two slots
   const uint32_t cache_bytes = uint32_t(a.num_blocks * a.block_size * row_stride * 2);
   const auto krs = make_rsrc(a.key_cache, cache_bytes);
@@ -463,7 +464,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   uint32_t bits[kDepth];
   int32_t rows[kDepth];
   const int64_t n_all = t_end > t_begin ? (t_end - t_begin + 15) / 16 : 0;
-  const int64_t n_tiles = n_all > wave ? (n_all - wave + W - 1) / W : 0;
+  const int64_t n_tiles = PRE ? n_all : n_all > wave ? (n_all - wave + W - 1) / W : 0;
   if (n_tiles > 0) {
     int32_t first[kDepth];
 #pragma unroll
@@ -493,7 +494,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   l_run += __shfl_xor(l_run, 32, 64);
   const int64_t h0 = kvh * GQ;
   const int64_t d0 = (HD / 4) * kb;
-  if constexpr (W == 1) {
+  if constexpr (W == 1 || PRE) {
     if (PRE ? !q_ok : col >= GQ) return;
     const int64_t h = h0 + (PRE ? col % GQ : col);
     float v[4][kNv];
@@ -669,7 +670,8 @@ hipError_t launch_decode_hd(const PagedDecodeArgs& a, hipStream_t stream) {
 template <class C, int HD, int GQ>
 void launch_prefill_group(const PagedDecodeArgs& a, hipStream_t stream) {
   constexpr int kTpt = 16 / GQ;
-  const dim3 grid(unsigned((a.q_len + kTpt - 1) / kTpt), unsigned(a.kv_heads), unsigned(a.num_seqs));
+  const int64_t per = int64_t(kTpt) * a.waves;  // query tokens per workgroup
+  const dim3 grid(unsigned((a.q_len + per - 1) / per), unsigned(a.kv_heads), unsigned(a.num_seqs));
   switch (a.waves) {
     case 1: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 1, false, true>), grid, dim3(64), 0, stream, a); break;
     case 2: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 2, false, true>), grid, dim3(128), 0, stream, a); break;
