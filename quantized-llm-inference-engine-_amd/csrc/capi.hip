@@ -885,6 +885,9 @@ int llmopt_rope(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
   a.ldq = ldq;
   a.ldk = ldk;
   a.dtype = dtype;
+  auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  a.vec = head_dim % 16 == 0 && ldq % 8 == 0 && al(q) && al(q_out) && al(cos_table) && al(sin_table) &&
+          (kv_heads == 0 || (ldk % 8 == 0 && al(k) && al(k_out))) && (!a.v || (ldv % 8 == 0 && al(v) && al(v_out)));
   return hip_status(llmopt::launch_rope(a, static_cast<hipStream_t>(stream)), "rope launch");
 }
 

@@ -216,6 +216,60 @@ __global__ void __launch_bounds__(256) rope_kernel(const RopeArgs a) {
   }
 }
 
+// rope_kernel for 16-byte aligned rows (a.vec, checked on the host; head_dim % 16 == 0): a thread
+// per (head, 8 consecutive pairs i0 .. i0 + 7), the same arithmetic on 16-byte loads and stores.
+template <class Act>
+__global__ void __launch_bounds__(256) rope_vec_kernel(const RopeArgs a) {
+  using Raw = typename Act::raw;
+  const int64_t t = blockIdx.x;
+  const int half = int(a.head_dim / 2);
+  const int64_t g = int64_t(blockIdx.y) * 256 + threadIdx.x;
+  if (g * 8 >= (a.heads + a.kv_heads) * half) return;
+  int64_t p = a.positions[t];
+  p = p < 0 ? 0 : (p >= a.table_rows ? a.table_rows - 1 : p);  // the host checks the range
+  const int64_t head = (g * 8) / half;
+  const int i0 = int(g * 8 - head * half);
+  const bool is_q = head < a.heads;
+  const int64_t hh = is_q ? head : head - a.heads;
+  const Raw* src = static_cast<const Raw*>(is_q ? a.q : a.k) + t * (is_q ? a.ldq : a.ldk) + hh * a.head_dim;
+  Raw* dst = static_cast<Raw*>(is_q ? a.q_out : a.k_out) + (t * (is_q ? a.heads : a.kv_heads) + hh) * a.head_dim;
+  float x1[8], x2[8], c1[8], s1[8], c2[8], s2[8];
+  unpack8<Act>(*reinterpret_cast<const u32x4*>(src + i0), x1);
+  unpack8<Act>(*reinterpret_cast<const u32x4*>(src + i0 + half), x2);
+  const float* cs = a.cos_table + p * a.head_dim;
+  const float* sn = a.sin_table + p * a.head_dim;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const f32x4 ca = *reinterpret_cast<const f32x4*>(cs + i0 + 4 * h);
+    const f32x4 sa = *reinterpret_cast<const f32x4*>(sn + i0 + 4 * h);
+    const f32x4 cb = *reinterpret_cast<const f32x4*>(cs + i0 + half + 4 * h);
+    const f32x4 sb = *reinterpret_cast<const f32x4*>(sn + i0 + half + 4 * h);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // The tables are cast to the activation dtype first (cos.to(q.dtype)).
+      c1[4 * h + e] = Act::load(Act::store(ca[e]));
+      s1[4 * h + e] = Act::load(Act::store(sa[e]));
+      c2[4 * h + e] = Act::load(Act::store(cb[e]));
+      s2[4 * h + e] = Act::load(Act::store(sb[e]));
+    }
+  }
+  float lo[8], hi[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    // rotate_half(x) = [-x2, x1]; every product and the sum rounded as torch rounds them.
+    lo[e] = Act::load(Act::store(Act::load(Act::store(x1[e] * c1[e])) + Act::load(Act::store(-x2[e] * s1[e]))));
+    hi[e] = Act::load(Act::store(Act::load(Act::store(x2[e] * c2[e])) + Act::load(Act::store(x1[e] * s2[e]))));
+  }
+  *reinterpret_cast<u32x4*>(dst + i0) = pack8<Act>(lo);
+  *reinterpret_cast<u32x4*>(dst + i0 + half) = pack8<Act>(hi);
+  if (!is_q && a.v) {
+    const Raw* vs = static_cast<const Raw*>(a.v) + t * a.ldv + hh * a.head_dim;
+    Raw* vd = static_cast<Raw*>(a.v_out) + (t * a.kv_heads + hh) * a.head_dim;
+    *reinterpret_cast<u32x4*>(vd + i0) = *reinterpret_cast<const u32x4*>(vs + i0);
+    *reinterpret_cast<u32x4*>(vd + i0 + half) = *reinterpret_cast<const u32x4*>(vs + i0 + half);
+  }
+}
+
 // Greedy sampling's argmax over each row (the reference's greedy sampler, torch.argmax(logits,
 // dim=-1), src/llmopt/engine/sampler.py:94-95): the index of the first maximum, a NaN counting
 // as larger than every number (the first NaN wins), as torch returns it. One workgroup of 1024
@@ -315,6 +369,14 @@ hipError_t launch_rmsnorm(const RmsNormArgs& a, hipStream_t stream) {
 
 hipError_t launch_rope(const RopeArgs& a, hipStream_t stream) {
   if (a.tokens == 0) return hipSuccess;
+  if (a.vec && !a.key_cache) {
+    const dim3 grid(unsigned(a.tokens), unsigned(((a.heads + a.kv_heads) * (a.head_dim / 16) + 255) / 256));
+    if (a.dtype == kDtBf16)
+      hipLaunchKernelGGL(rope_vec_kernel<ActBf16>, grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL(rope_vec_kernel<ActF16>, grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+  }
   const dim3 grid(unsigned(a.tokens), unsigned(((a.heads + a.kv_heads) * (a.head_dim / 2) + 255) / 256));
   if (a.dtype == kDtBf16)
     hipLaunchKernelGGL(rope_kernel<ActBf16>, grid, dim3(256), 0, stream, a);

@@ -183,6 +183,7 @@ struct RopeArgs {
   const int32_t* block_ids;  // [tokens, ldb]
   const int32_t* offsets;    // [tokens]
   int64_t ldb, num_blocks, block_size;
+  int vec;  // rows and tables 16-byte aligned, head_dim % 16 == 0: 16-byte loads and stores
 };
 hipError_t launch_rope(const RopeArgs& a, hipStream_t stream);
 

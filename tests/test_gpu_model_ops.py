@@ -39,6 +39,23 @@ def test_rope_is_bit_identical_to_the_torch_sequence(dtype, heads, kv_heads, d):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_on_unaligned_rows_is_bit_identical_too(dtype):
+    # Rows off 16-byte alignment take the element-wise kernel: the same results.
+    g = torch.Generator(device=DEV).manual_seed(3)
+    tokens, heads, kv_heads, d = 9, 4, 2, 64
+    rope = RotaryEmbedding(d, 512, base=10000.0).to(DEV)
+    fused = torch.randn(tokens, 1 + (heads + 2 * kv_heads) * d, generator=g, device=DEV).to(dtype)
+    q = fused[:, 1 : 1 + heads * d].view(tokens, heads, d)
+    k = fused[:, 1 + heads * d : 1 + (heads + kv_heads) * d].view(tokens, kv_heads, d)
+    v = fused[:, 1 + (heads + kv_heads) * d :].view(tokens, kv_heads, d)
+    positions = torch.randint(0, 512, (tokens,), generator=g, device=DEV)
+    got_q, got_k, got_v = ops.rope(q, k, positions, rope.cos_cached, rope.sin_cached, v=v)
+    cos, sin = rope(positions, dtype=dtype)
+    want_q, want_k = apply_rotary_pos_emb(q, k, cos[:, None, :], sin[:, None, :])
+    assert torch.equal(got_q, want_q) and torch.equal(got_k, want_k) and torch.equal(got_v, v)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows,hidden", [(1, 4096), (32, 4096), (5, 264)])
 @torch.no_grad()
 def test_rmsnorm_with_residual_matches_the_torch_sequence(dtype, rows, hidden):
