@@ -293,6 +293,35 @@ __global__ void __launch_bounds__(256) swiglu_combine_vec_kernel(const typename 
     *reinterpret_cast<f32x4*>(y + m * ldy + 4 * p) = o;
   }
 }
+// Sixteen fused columns per thread for 16-bit activations (two 16-byte loads, one 16-byte
+// store): twice the bytes in flight per thread of swiglu_combine_vec_kernel.
+template <class Act>
+__global__ void __launch_bounds__(256) swiglu_combine_vec2_kernel(const typename Act::raw* t, int64_t ldt,
+                                                                  typename Act::raw* y, int64_t ldy, int64_t M,
+                                                                  int64_t P2) {
+  using Raw = typename Act::raw;
+  static_assert(sizeof(Raw) == 2, "16-bit activations");
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= M * P2) return;
+  const int64_t m = i / P2;
+  const int64_t p = i - m * P2;
+  const Raw* src = t + m * ldt + 16 * p;
+  const u32x4 v0 = *reinterpret_cast<const u32x4*>(src);
+  const u32x4 v1 = *reinterpret_cast<const u32x4*>(src + 8);
+  const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      // Block b: gate words 4b, 4b + 1, up words 4b + 2, 4b + 3 (four gate, four up columns).
+      const uint32_t gw = w[4 * b + r], uw = w[4 * b + 2 + r];
+      const float lo = swiglu<Act>(Act::load(Raw(gw & 0xFFFFu)), Act::load(Raw(uw & 0xFFFFu)));
+      const float hi = swiglu<Act>(Act::load(Raw(gw >> 16)), Act::load(Raw(uw >> 16)));
+      o[2 * b + r] = uint32_t(Act::store(lo)) | (uint32_t(Act::store(hi)) << 16);
+    }
+  *reinterpret_cast<u32x4*>(y + m * ldy + 8 * p) = u32x4{o[0], o[1], o[2], o[3]};
+}
 }  // namespace
 
 hipError_t launch_swiglu_combine(const void* t, int64_t ldt, void* y, int64_t ldy, int64_t M, int64_t N,
@@ -303,6 +332,17 @@ hipError_t launch_swiglu_combine(const void* t, int64_t ldt, void* y, int64_t ld
   const size_t es = act == kDtF32 ? 4 : 2;
   const bool vec = N % 8 == 0 && reinterpret_cast<uintptr_t>(t) % 16 == 0 && (ldt * es) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(y) % (4 * es) == 0 && (ldy * es) % (4 * es) == 0;
+  if (vec && es == 2 && N % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 && (ldy * es) % 16 == 0) {
+    const int64_t P2 = N / 16;
+    const dim3 grid(unsigned((M * P2 + 255) / 256)), block(256);
+    if (act == kDtBf16)
+      hipLaunchKernelGGL(swiglu_combine_vec2_kernel<ActBf16>, grid, block, 0, stream,
+                         static_cast<const uint16_t*>(t), ldt, static_cast<uint16_t*>(y), ldy, M, P2);
+    else
+      hipLaunchKernelGGL(swiglu_combine_vec2_kernel<ActF16>, grid, block, 0, stream,
+                         static_cast<const uint16_t*>(t), ldt, static_cast<uint16_t*>(y), ldy, M, P2);
+    return hipGetLastError();
+  }
   if (vec) {
     const int64_t P = N / 8;
     const dim3 grid(unsigned((M * P + 255) / 256)), block(256);
