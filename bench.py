@@ -581,11 +581,14 @@ def attention_rates(torch):
     """Decode-step attention of the Llama-3-8B end-to-end workload: 32 sequences with 512-640
     cached tokens (512-token prompts, then up to 128 decoded), 32 query / 8 KV heads of 128,
     block 16, bf16 cache; one layer per call, rotating over 8 layers' caches (> 512 MiB) as a
-    decode step walks the layers. Also: this step's KV write, the reference's torch sequence for
-    the same attention (gather, matmul, softmax, matmul) on the same GPU, and the vocabulary
-    projection of a 32 x 512-token prefill chunk for all positions vs the last ones only."""
+    decode step walks the layers. Also: this step's KV write, the decode step as the model runs
+    it (rotary step, cache write and attention in one launch), the reference's torch sequence for
+    the same attention (gather, matmul, softmax, matmul) on the same GPU, the prefill attention of
+    32 x 512-token prompts (kernel and torch sequence), and the vocabulary projection of a
+    32 x 512-token prefill chunk for all positions vs the last ones only."""
     from llmopt.attention import PagedAttention, PagedAttentionConfig
     from llmopt.cache import PagedKVCache
+    from llmopt.kernels import ops
     from llmopt.logits import last_token_logits
 
     seqs, heads, kv_heads, head_dim, bs, layers = 32, 32, 8, 128, 16, 8
@@ -617,10 +620,48 @@ def attention_rates(torch):
     offsets = (lens - 1).to(torch.int64)
     w_times = kernel_launch_times(torch, lambda i: cache.write_decode(i % layers, table, offsets, new_k, new_k),
                                   2 * layers)
+    # The decode step as the model runs it: rotary step, cache write and attention in one launch,
+    # on the raw q / k / v rows of the fused projection's output.
+    from llmopt.model import RotaryEmbedding
+
+    rot = RotaryEmbedding(head_dim, 8192, base=500000.0).to(dev)
+    qkv = torch.randn(seqs, (heads + 2 * kv_heads) * head_dim, device=dev).to(torch.bfloat16)
+    rq = qkv[:, : heads * head_dim].view(seqs, heads, head_dim)
+    rk = qkv[:, heads * head_dim : (heads + kv_heads) * head_dim].view(seqs, kv_heads, head_dim)
+    rv = qkv[:, (heads + kv_heads) * head_dim :].view(seqs, kv_heads, head_dim)
+    step_times = kernel_launch_times(
+        torch, lambda i: ops.paged_decode_attention_rope(
+            rq, rk, rv, offsets, rot.cos_cached, rot.sin_cached, cache.key_cache[i % layers],
+            cache.value_cache[i % layers], table, lens, offsets.to(torch.int32), head_dim**-0.5), 2 * layers)
+    step_us = statistics.median(step_times)
     print(f"# paged decode attention (32 seqs x 512-640 tokens, 32/8 heads): {us:.1f} us, {gbs:.0f} GB/s; "
-          f"torch sequence {torch_us:.0f} us; KV write {statistics.median(w_times):.1f} us",
-          file=sys.stderr, flush=True)
+          f"torch sequence {torch_us:.0f} us; KV write {statistics.median(w_times):.1f} us; with the rotary "
+          f"step and the cache write in the same launch {step_us:.1f} us", file=sys.stderr, flush=True)
     del cache
+
+    # Prefill attention: 32 prompts of 512 tokens, no prefix, causal.
+    p_len, p_blocks = 512, 32
+    pcache = PagedKVCache(1, seqs * p_blocks, bs, kv_heads, head_dim, dtype=torch.bfloat16, device=dev)
+    pcache.key_cache.normal_()
+    pcache.value_cache.normal_()
+    ptable = torch.arange(seqs * p_blocks, dtype=torch.int32, device=dev).view(seqs, p_blocks)
+    plens = torch.full((seqs,), p_len, dtype=torch.int32, device=dev)
+    pq = torch.randn(seqs, p_len, heads, head_dim, device=dev).to(torch.bfloat16).permute(0, 2, 1, 3)
+    pre_times = kernel_launch_times(
+        torch, lambda i: attn.forward(pq, pcache, 0, ptable, plens), 8)
+    pre_us = statistics.median(pre_times)
+    pre_flop = seqs * heads * (p_len * (p_len + 1) / 2) * head_dim * 4
+    torch_pre = PagedAttention(heads, kv_heads, head_dim, config=PagedAttentionConfig(block_size=bs), backend="sdpa")
+    torch_pre.forward(pq, pcache, 0, ptable, plens)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        torch_pre.forward(pq, pcache, 0, ptable, plens)
+    torch.cuda.synchronize()
+    torch_pre_us = (time.perf_counter() - t0) * 1e6 / 3
+    print(f"# paged prefill attention (32 x 512-token prompts, 32/8 heads, causal): {pre_us:.1f} us, "
+          f"{pre_flop / pre_us / 1e6:.1f} TFLOP/s; torch sequence {torch_pre_us:.0f} us", file=sys.stderr, flush=True)
+    del pcache
 
     # Vocabulary projection of one prefill chunk: every position vs the last ones.
     hidden_size, vocab, q_len = 4096, 128256, 512
@@ -641,6 +682,12 @@ def attention_rates(torch):
             "torch_sequence_us": round(torch_us, 1),
         },
         "kv_write_decode_us": round(statistics.median(w_times), 2),
+        "decode_step_rope_write_attention_us": round(step_us, 2),
+        "prefill_attention": {
+            "workload": "32 prompts x 512 tokens, 32 query / 8 KV heads x 128, causal, block 16, bf16 cache",
+            "us": round(pre_us, 1), "TFLOP/s": round(pre_flop / pre_us / 1e6, 1),
+            "torch_sequence_us": round(torch_pre_us, 1),
+        },
         "lm_head_prefill_chunk": {"tokens": seqs * q_len, "all_positions_us": round(full_us, 1),
                                   "last_positions_us": round(last_us, 1)},
     }
