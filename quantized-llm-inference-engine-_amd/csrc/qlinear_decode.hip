@@ -2584,10 +2584,17 @@ bool try_oneshot_f32(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   // kernels lead (gate_up at two tokens, groups of 64: 39.8 us here against 26 us).
   if (a.M == 2 && tiles >= 1024) return false;
   const int64_t steps = a.K / 128;
-  if (steps % 4 != 0 || steps / 4 > 16) return false;
-  const int nw = int(steps / 4);
+  if (steps % 4 != 0) return false;
+  // Rows longer than 16 chunks of four steps (down, K 14336 at one token): eight-step chunks of
+  // the three piece rows, one token in groups of 128 only (with groups of 64 the form spills).
+  const bool eight = a.M == 1 && a.group == 128 && steps % 8 == 0 && steps / 8 <= 16;
+  const int c = steps / 4 <= 16 ? 4 : eight ? 8 : 0;
+  if (c == 0) return false;
+  const int nw = int(steps / c);
   if (16 * a.G / 4 > int64_t(nw) * 64) return false;  // one scale piece per thread
-  if (a.M == 1)
+  if (c == 8)
+    *err = launch_oneshot_cfg<ActBf16, 8, 3, 3, 1, true>(a, nw, stream);
+  else if (a.M == 1)
     *err = a.group == 64 ? launch_oneshot_cfg<ActBf16, 4, 4, 4, 2, true>(a, nw, stream)
                          : launch_oneshot_cfg<ActBf16, 4, 4, 4, 1, true>(a, nw, stream);
   else

@@ -178,7 +178,9 @@ def test_swiglu_in_fp32(m):
 def test_k_sliced_pieces(n, k, group, symmetric, m, with_bias):
     # One to ten fp32 tokens whose piece rows the K-sliced kernel splits over K (long rows from
     # one token, K = 4096 from 3 tokens in groups of 64 or 6 in groups of 128): the pieces, the
-    # K-sliced kernel with its reduction into fp32 sums, then the combining kernel.
+    # K-sliced kernel with its reduction into fp32 sums, then the combining kernel. One token on
+    # the long rows in groups of 128 takes the one-shot kernel's eight-step chunks instead, the
+    # split and the pieces' sum inside it.
     qt = _host_qt(n, k, 4, group, symmetric, seed=m + n + group)
     dqt = _to_device(qt)
     gen = torch.Generator().manual_seed(m + 100)
