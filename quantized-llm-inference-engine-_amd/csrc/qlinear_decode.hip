@@ -2594,9 +2594,9 @@ bool try_oneshot_f32(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (16 * a.G / 4 > int64_t(nw) * 64) return false;  // one scale piece per thread
   if (c == 8)
     *err = launch_oneshot_cfg<ActBf16, 8, 3, 3, 1, true>(a, nw, stream);
-  else if (a.M == 1)
-    *err = a.group == 64 ? launch_oneshot_cfg<ActBf16, 4, 4, 4, 2, true>(a, nw, stream)
-                         : launch_oneshot_cfg<ActBf16, 4, 4, 4, 1, true>(a, nw, stream);
+  else if (a.M == 1)  // three piece rows: 92 / 62 VGPRs against 104 / 67 for four-row slices
+    *err = a.group == 64 ? launch_oneshot_cfg<ActBf16, 4, 3, 3, 2, true>(a, nw, stream)
+                         : launch_oneshot_cfg<ActBf16, 4, 3, 3, 1, true>(a, nw, stream);
   else
     *err = a.group == 64 ? launch_oneshot_cfg<ActBf16, 4, 8, 4, 2, true>(a, nw, stream)
                          : launch_oneshot_cfg<ActBf16, 4, 8, 4, 1, true>(a, nw, stream);
