@@ -2570,8 +2570,9 @@ bool try_oneshot(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
 }
 
 // fp32 activations of one or two tokens, as three bf16 pieces each (three or six rows), on the
-// one-shot kernel with the split and the pieces' sum inside it: 4-step chunks, groups of 64 or
-// 128, 2/4-bit codes; y and bias fp32.
+// one-shot kernel with the split and the pieces' sum inside it: 4-step chunks (8 for one token
+// on rows longer than 16 four-step chunks, groups of 128), groups of 64 or 128, 2/4-bit codes;
+// y and bias fp32.
 bool try_oneshot_f32(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.act != kDtF32 || a.fmt != kNibble || a.M < 1 || a.M > 2 || a.epilogue != kEpiNone) return false;
   if ((a.group != 128 && a.group != 64) || a.K % 128 != 0 || a.G % 4 != 0) return false;
