@@ -619,31 +619,23 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
   const u32x4 zv = buf_load16(mz, mo, 0);
 
   u32x4 xv[Geo::kXPerLane];
+  // F32X: eight fp32 activations of a token per (token, piece column), loaded once; all three
+  // piece rows are made from them when the slice is staged.
+  constexpr int kTok = (MMAX + 2) / 3;
+  constexpr int kXTok = (kTok * C * 16 + 63) / 64;
+  const int ntok = int(a.M);
+  f32x4 xf[F32X ? kXTok : 1][2];
   if constexpr (F32X) {
-    // Piece (m % 3) of eight fp32 activations of token m / 3: two 16-byte loads.
     const float* xg = static_cast<const float*>(a.x) + int64_t(step0) * 128;
 #pragma unroll
-    for (int e = 0; e < Geo::kXPerLane; ++e) {
+    for (int e = 0; e < kXTok; ++e) {
       int idx = lane + 64 * e;
-      idx = idx < M * C * 16 ? idx : 0;
-      const int m = idx / (C * 16);
-      const int c = idx - m * (C * 16);
-      const int tok = m / 3;
-      const int piece = m - 3 * tok;
+      idx = idx < ntok * C * 16 ? idx : 0;
+      const int tok = idx / (C * 16);
+      const int c = idx - tok * (C * 16);
       const float* src = xg + tok * a.ldx + (c >> 4) * (sstride * 128) + 8 * (c & 15);
-      const f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
-      const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
-      const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-      uint32_t h[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint16_t hi = f32_to_bf16_rne(v[j]);
-        const float r1 = v[j] - bf16_to_f32(hi);  // exact
-        const uint16_t mid = f32_to_bf16_rne(r1);
-        const uint16_t lo = f32_to_bf16_rne(r1 - bf16_to_f32(mid));  // exact remainder
-        h[j] = piece == 0 ? hi : piece == 1 ? mid : lo;
-      }
-      xv[e] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+      xf[e][0] = *reinterpret_cast<const f32x4*>(src);
+      xf[e][1] = *reinterpret_cast<const f32x4*>(src + 4);
     }
   } else {
     const Raw* xg = static_cast<const Raw*>(a.x) + int64_t(step0) * 128;
@@ -682,8 +674,36 @@ __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8)
     for (int i = lane; i < C * 16; i += 64)
       if ((i & 15) >= M) xsum[i] = 0.0f;
   }
+  if constexpr (F32X) {
+    // Rows 3t, 3t + 1, 3t + 2: the hi, mid and lo pieces of token t (x = hi + mid + lo exactly).
 #pragma unroll
-  for (int e = 0; e < Geo::kXPerLane; ++e) {
+    for (int e = 0; e < kXTok; ++e) {
+      const int idx = lane + 64 * e;
+      const int tok = idx / (C * 16);
+      const int c = idx - tok * (C * 16);
+      const float v[8] = {xf[e][0][0], xf[e][0][1], xf[e][0][2], xf[e][0][3],
+                          xf[e][1][0], xf[e][1][1], xf[e][1][2], xf[e][1][3]};
+      uint32_t hi[8], mid[8], lo[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        hi[j] = f32_to_bf16_rne(v[j]);
+        const float r1 = v[j] - bf16_to_f32(uint16_t(hi[j]));  // exact
+        mid[j] = f32_to_bf16_rne(r1);
+        lo[j] = f32_to_bf16_rne(r1 - bf16_to_f32(uint16_t(mid[j])));  // exact remainder
+      }
+      if (idx < ntok * C * 16) {
+        const uint32_t* parts[3] = {hi, mid, lo};
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+          const uint32_t* h = parts[p];
+          xw[(3 * tok + p) * Geo::kRowPieces + c] = arrange<Act, FMT>(
+              u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)});
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < (F32X ? 0 : Geo::kXPerLane); ++e) {
     const int idx = lane + 64 * e;
     const int m = idx / (C * 16);
     const int c = idx - m * (C * 16);
