@@ -37,7 +37,8 @@ struct LinearArgs {
   // Host side only. defer_reduce = 1: a K-sliced decode plan leaves its fp32 partial sums
   // [slices][M][N] at the start of the workspace, launches no reduction, leaves y untouched and
   // stores the slice count in *deferred_planes (which the caller zeroes first); other plans
-  // finish as usual. Only without an epilogue and with out_f32 = 0.
+  // finish as usual. Only without an epilogue (with out_f32 = 1: the fp32-activation path,
+  // whose combining kernel then adds the slices as well as the pieces).
   int defer_reduce;
   int* deferred_planes;
 };

@@ -3011,7 +3011,7 @@ hipError_t launch_ks_cfg(const LinearArgs& a, const KsPlan& p, uint32_t magic, h
                      p.per_slice, magic, partials);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.slices == 1) return e;
-  if (a.defer_reduce && a.deferred_planes && a.epilogue == kEpiNone && !a.out_f32) {
+  if (a.defer_reduce && a.deferred_planes && a.epilogue == kEpiNone) {
     *a.deferred_planes = p.slices;  // the caller's consumer adds the slices up
     return hipSuccess;
   }

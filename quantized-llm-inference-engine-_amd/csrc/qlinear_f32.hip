@@ -61,6 +61,31 @@ __global__ void __launch_bounds__(kThreads) combine_pieces_kernel(const float* t
   y[m * ldy + n] = v;
 }
 
+// The same from a K-sliced launch's partial sums P[s][3 rows][N] (slices not yet added): each
+// piece row's slices in slice order, as the split-K reduction adds them, then the pieces as above
+// -- one kernel instead of the reduction and the combining kernel, with the same sums.
+__global__ void __launch_bounds__(kThreads) combine_slices_kernel(const float* partials, int splits, int64_t N,
+                                                                  const float* bias, float* y, int64_t ldy,
+                                                                  int64_t rows) {
+  const int64_t e = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (e >= rows * N) return;
+  const int64_t m = e / N;
+  const int64_t n = e - m * N;
+  const size_t plane = size_t(3 * rows) * size_t(N);
+  const float* r = partials + size_t(3 * m) * size_t(N) + n;
+  float t[3] = {r[0], r[N], r[2 * N]};
+#pragma unroll 4
+  for (int s = 1; s < splits; ++s) {
+    const float* q = r + size_t(s) * plane;
+    t[0] += q[0];
+    t[1] += q[N];
+    t[2] += q[2 * N];
+  }
+  float v = (t[0] + t[1]) + t[2];
+  if (bias) v += bias[n];
+  y[m * ldy + n] = v;
+}
+
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 struct F32Plan {
@@ -116,6 +141,8 @@ hipError_t launch_linear_f32_pieces(const LinearArgs& a, hipStream_t stream, boo
     b.out_f32 = 1;
     b.workspace = inner;
     b.workspace_bytes = p.inner;
+    b.defer_reduce = 1;  // a K-sliced plan's slices are added by the combining kernel below
+    b.deferred_planes = nullptr;
     return b;
   };
   // A chunk whose shape the decode path refuses (an alignment or a format it does not take)
@@ -127,7 +154,9 @@ hipError_t launch_linear_f32_pieces(const LinearArgs& a, hipStream_t stream, boo
   hipError_t err = hipGetLastError();
   for (int64_t m0 = 0; m0 < a.M && err == hipSuccess; m0 += p.chunk) {
     const int64_t rows = std::min(p.chunk, a.M - m0);
-    const LinearArgs b = chunk_args(m0, rows);
+    LinearArgs b = chunk_args(m0, rows);
+    int planes = 0;
+    b.deferred_planes = &planes;
     bool taken = false;
     err = launch_linear_decode(b, stream, &taken);
     if (err != hipSuccess) break;
@@ -139,9 +168,14 @@ hipError_t launch_linear_f32_pieces(const LinearArgs& a, hipStream_t stream, boo
       err = launch_linear_generic(g, stream);
       continue;
     }
-    hipLaunchKernelGGL(combine_pieces_kernel, dim3(unsigned((rows * a.N + kThreads - 1) / kThreads)),
-                       dim3(kThreads), 0, stream, t, a.N, static_cast<const float*>(a.bias),
-                       static_cast<float*>(a.y) + m0 * a.ldy, a.ldy, rows);
+    const dim3 grid(unsigned((rows * a.N + kThreads - 1) / kThreads));
+    if (planes > 0)
+      hipLaunchKernelGGL(combine_slices_kernel, grid, dim3(kThreads), 0, stream, static_cast<const float*>(inner),
+                         planes, a.N, static_cast<const float*>(a.bias), static_cast<float*>(a.y) + m0 * a.ldy,
+                         a.ldy, rows);
+    else
+      hipLaunchKernelGGL(combine_pieces_kernel, grid, dim3(kThreads), 0, stream, t, a.N,
+                         static_cast<const float*>(a.bias), static_cast<float*>(a.y) + m0 * a.ldy, a.ldy, rows);
     err = hipGetLastError();
   }
   return err;
