@@ -2973,12 +2973,13 @@ KsPlan plan_ks(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   // alternative: down at 3-4 tokens 27 us there).
   // Groups of 64 (nibble codes): the multi-tile kernel takes 9-32 tokens, the skinny one 33-64;
   // here from 9 tokens (3 on rows of K >= 8192: down at 3-4 tokens 15.0-16.0 -> 14.7-14.8 us,
-  // and the fp32 path's three piece rows of one token) and on any grid as well.
+  // and the fp32 path's three piece rows of one token) up to 48 (three token blocks; four
+  // would spill) and on any grid as well.
   const bool bytes = bits == 8;
   const bool g64 = group == 64 && !bytes;
   const bool wide = bytes || g64;  // no resident-activation or N-split form
   const int64_t min_m = K >= 8192 ? (bytes || g64 ? 3 : 5) : (wide ? 9 : 17);
-  if (M > (g64 ? 32 : 64) || M < min_m || (group % 128 != 0 && !g64)) return p;
+  if (M > (g64 ? 48 : 64) || M < min_m || (group % 128 != 0 && !g64)) return p;
   const int64_t tiles = (N + 15) / 16;
   if ((tiles >= 1024 && !wide) || tiles < 1) return p;
   const int64_t block_k = bits == 8 ? 128 : 256;  // codes per block of 128 bytes per row
@@ -3022,8 +3023,10 @@ template <class Act, int FMT, int GS = 1>
 hipError_t launch_ks_mb(const LinearArgs& a, const KsPlan& p, uint32_t magic, hipStream_t stream) {
   if (a.M <= 16) return launch_ks_cfg<Act, 1, FMT, GS>(a, p, magic, stream);
   if (a.M <= 32) return launch_ks_cfg<Act, 2, FMT, GS>(a, p, magic, stream);
-  // Four token blocks with two groups per step would spill (plan_ks stops groups of 64 at 32).
+  // Two groups per step: three token blocks (240 VGPRs); four would spill (plan_ks stops
+  // groups of 64 at 48).
   if constexpr (GS == 1) return launch_ks_cfg<Act, 4, FMT, GS>(a, p, magic, stream);
+  if (a.M <= 48) return launch_ks_cfg<Act, 3, FMT, GS>(a, p, magic, stream);
   return hipErrorInvalidValue;
 }
 

@@ -11,8 +11,8 @@
 // fp32 (LinearArgs::out_f32), and the combining kernel adds them, in a fixed order, with the
 // bias: y = (t_hi + t_mid) + t_lo + b, an fp32 result within fp32 rounding of the reference's
 // fp32 dequantize-then-F.linear. The weight is streamed once per chunk of up to 21 tokens
-// (63 rows, the decode kernels' limit of 64), so the memory-bound cost is that of a bf16 batch
-// three times as tall.
+// (63 rows, the decode kernels' limit of 64; 16 tokens with groups of 64), so the memory-bound
+// cost is that of a bf16 batch three times as tall.
 #include <algorithm>
 
 #include "qcommon.hpp"
@@ -22,7 +22,9 @@ namespace llmopt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int64_t kChunkTokens = 21;  // 3 x 21 = 63 piece rows per decode launch
+// Tokens per decode launch: 3 x 21 = 63 piece rows; with groups of 64, 3 x 16 = 48 (the
+// K-sliced kernel's two-group form stops at 48 rows).
+int64_t chunk_tokens(int64_t group) { return group == 64 ? 16 : 21; }
 
 // xs[3m + p][k] = piece p of x[m][k]. Four columns per thread (16-byte loads where aligned).
 __global__ void __launch_bounds__(kThreads) split_pieces_kernel(const float* x, int64_t ldx, uint16_t* xs,
@@ -96,7 +98,8 @@ struct F32Plan {
 
 F32Plan plan_f32(int64_t M, int64_t N, int64_t K, int64_t group, int bits) {
   F32Plan p;
-  const int64_t chunks = (M + kChunkTokens - 1) / kChunkTokens;
+  const int64_t most = chunk_tokens(group);
+  const int64_t chunks = (M + most - 1) / most;
   p.chunk = (M + chunks - 1) / chunks;
   const int64_t last = M - (chunks - 1) * p.chunk;
   p.xs = align256(size_t(3) * M * K * 2);

@@ -485,7 +485,7 @@ def test_wide_grids_at_33_to_64_tokens_every_format(m, bits, group):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 12, 16, 24, 32, 40, 64])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 12, 16, 24, 32, 33, 40, 48, 49, 64])
 @pytest.mark.parametrize("n, k, bits, symmetric, with_bias", [
     (6144, 4096, 4, True, False), (28672, 4096, 4, True, False), (4100, 4096, 4, False, True),
     (4096, 14336, 4, True, False), (1000, 2048, 2, False, True)])
@@ -493,7 +493,8 @@ def test_linear_groups_of_64(dtype, m, n, k, bits, symmetric, with_bias):
     # Groups of 64 codes (the reference engine's quantize_model_(bits=4, group_size=64),
     # src/llmopt/engine/llm_engine.py:258-264): two groups per 128-code step on the one-shot
     # (M <= 8) and multi-tile (M <= 32) decode kernels, with the code words transposed across
-    # the wave's rows; ragged N, bias, 2-bit codes, long rows; 33-64 tokens on the skinny kernel.
+    # the wave's rows; ragged N, bias, 2-bit codes, long rows; up to 48 tokens on the K-sliced
+    # kernel (three token blocks from 33), 49-64 on the skinny kernel.
     qt = _host_qt(n, k, bits, 64, symmetric, seed=m + n + k)
     gen = torch.Generator().manual_seed(m)
     x = torch.randn(m, k, generator=gen).to(dtype)
@@ -504,7 +505,7 @@ def test_linear_groups_of_64(dtype, m, n, k, bits, symmetric, with_bias):
     assert _rel_err(y[:, torch.from_numpy(cols).to(DEV)], ref) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("m", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 32, 48])
 def test_groups_of_64_one_hot_rows_return_weight_columns(m):
     # One-hot activation rows return the dequantized weight's columns bit for bit: every other
     # group and step adds exactly zero, and s * ((OFF + q) - (OFF + z)) rounds (q - z) * s once.
