@@ -2601,9 +2601,10 @@ bool try_oneshot_f32(const LinearArgs& a, hipStream_t stream, hipError_t* err) {
   if (a.N * a.ldq >= (int64_t(1) << 31) || a.N * a.G * 4 >= (int64_t(1) << 31)) return false;
   const int64_t tiles = (a.N + 15) / 16;
   if (tiles > 0x7FFFFFFF) return false;
-  // Two tokens (six piece rows) over 1024 tiles or more: the split into pieces and the decode
-  // kernels lead (gate_up at two tokens, groups of 64: 39.8 us here against 26 us).
-  if (a.M == 2 && tiles >= 1024) return false;
+  // Two tokens (six piece rows) over 1024 tiles or more, groups of 128: the split into pieces
+  // and the decode kernels lead (gate_up: 24.4 us here against 21.9; with groups of 64 this form
+  // leads, 26.3 against 28.3).
+  if (a.M == 2 && tiles >= 1024 && a.group != 64) return false;
   const int64_t steps = a.K / 128;
   if (steps % 4 != 0) return false;
   // Rows longer than 16 chunks of four steps (down, K 14336 at one token): eight-step chunks of

@@ -72,7 +72,7 @@ def engine_projections():
 
 
 @pytest.mark.parametrize("name", list(PROJECTIONS))
-@pytest.mark.parametrize("m", [1, 32, 2048])
+@pytest.mark.parametrize("m", [1, 2, 16, 32, 2048])
 def test_engine_configuration_projections(engine_projections, name, m):
     # 4-bit symmetric groups of 64, fp32 compute: sampled columns (and, at 2048 tokens, rows)
     # against the reference's fp32 sequence on the host; every output against float64.
