@@ -166,6 +166,7 @@ PREFILL_CASES = [  # (ctx, q_len, heads, kv_heads, head_dim, block_size, holes, 
     ([33, 64], 33, 8, 8, 64, 32, (), 30.0),  # soft-capped scores, one query head per KV head
     ([200], 100, 16, 16, 128, 16, (), 0.0),  # sixteen query heads per KV head: one token per tile
     ([20, 9], 20, 32, 4, 64, 8, (), 0.0),  # context shorter than q_len: early tokens see no key
+    ([90, 50], 50, 8, 2, 128, 16, (), 0.0),  # a prefix; the last wave's later column blocks empty
 ]
 
 
