@@ -70,14 +70,17 @@ class DecoderOnlyModel(nn.Module):
             token_offsets = context_lens - q_len
         pending = None  # each layer's MLP output, added inside the next norm's kernel
         last = len(self.layers) - 1
+        # The final norm takes the last layer's partial sums too unless it first keeps only each
+        # sequence's last row (last_only with several tokens per sequence).
+        defer_last = not last_only or q_len == 1
         for i, layer in enumerate(self.layers):
-            # Every layer but the last may hand its down projection's partial sums to the next
-            # layer's first norm (the final norm takes the last layer's output rows).
+            # A layer may hand its down projection's partial sums to the next norm.
             hidden, pending = layer.forward_chained(hidden, pending, positions, cache=cache, block_ids=block_ids,
                                                     context_lens=context_lens, token_offsets=token_offsets,
-                                                    q_len=q_len, defer_mlp=self.defer_reductions and i < last)
+                                                    q_len=q_len,
+                                                    defer_mlp=self.defer_reductions and (i < last or defer_last))
         seqs = int(hidden.shape[0]) // max(1, q_len)
-        if last_only:
+        if last_only and q_len > 1:
             # The residual add, RMSNorm and lm_head act row by row, so keeping only the last rows
             # first is exact.
             hidden = last_token_hidden(hidden, q_len).contiguous()

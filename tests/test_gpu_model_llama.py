@@ -131,9 +131,10 @@ def test_llama3_8b_width_decoder_end_to_end_prompt_batch(llama_two_layers):
 
 @pytest.mark.timeout(900)
 def test_deferred_down_reductions_are_bit_identical(llama_two_layers):
-    # Layer 0's down projection at 32 decode tokens runs on the K-sliced kernel (seven slices);
-    # with deferred reductions its partial sums go to layer 1's first norm, which adds them up
-    # (llmopt_rmsnorm_planes) instead of a reduction kernel: every logit is the same bits.
+    # The down projection at 32 decode tokens runs on the K-sliced kernel (seven slices); with
+    # deferred reductions layer 0's partial sums go to layer 1's first norm and layer 1's to the
+    # final norm, which add them up (llmopt_rmsnorm_planes) instead of a reduction kernel: every
+    # logit is the same bits.
     from llmopt.kernels import ops
     from llmopt.model import layers as model_layers
 
@@ -158,9 +159,10 @@ def test_deferred_down_reductions_are_bit_identical(llama_two_layers):
     finally:
         model_layers.SwiGLUMLP.forward = real_forward
         gpu.defer_reductions = True
-    # Deferred: the decode steps' layer-0 MLP outputs are partial sums (three steps), the
-    # prefill's (256 rows) and layer 1's are tensors.
-    assert kinds[:8].count(ops.PartialSums.__name__) == 3, kinds
+    # Deferred: the decode steps' MLP outputs are partial sums (two layers, three steps); the
+    # prefill's (256 rows, last positions only) are tensors.
+    assert kinds[:8].count(ops.PartialSums.__name__) == 6, kinds
+    assert kinds[:2] == ["Tensor", "Tensor"], kinds
     assert ops.PartialSums.__name__ not in kinds[8:], kinds
     assert torch.equal(deferred, plain)
 
