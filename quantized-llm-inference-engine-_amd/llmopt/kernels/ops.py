@@ -627,16 +627,21 @@ def paged_decode_attention_rope(
     return out
 
 
-def argmax_rows(x: torch.Tensor) -> torch.Tensor:
+def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``torch.argmax(x, dim=-1)`` of a 2-D device tensor (fp32 / fp16 / bf16, unit inner
     stride) as one kernel: the first maximum of each row, NaN above every number; int64
-    ``[rows]``. The greedy sampler's step (``sampler.py:94-95``)."""
+    ``[rows]``, written into ``out`` when given (contiguous int64 ``[rows]`` on the same device).
+    The greedy sampler's step (``sampler.py:94-95``)."""
     if x.dim() != 2 or x.dtype not in DTYPE_CODES:
         raise ValueError(f"argmax_rows takes a 2-D fp32/fp16/bf16 tensor, got {tuple(x.shape)} {x.dtype}")
     if x.stride(1) != 1:
         x = x.contiguous()
     rows, cols = (int(d) for d in x.shape)
-    out = torch.empty(rows, dtype=torch.long, device=x.device)
+    if out is None:
+        out = torch.empty(rows, dtype=torch.long, device=x.device)
+    elif (out.dtype != torch.long or tuple(out.shape) != (rows,) or not out.is_contiguous()
+          or out.device != x.device):
+        raise ValueError(f"out must be a contiguous int64 [{rows}] tensor on {x.device}")
     if rows == 0:
         return out
     if cols == 0:

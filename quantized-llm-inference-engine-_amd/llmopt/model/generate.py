@@ -35,13 +35,16 @@ class GenerationResult:
         return seqs * (steps - 2) / self.decode_seconds if steps > 2 and self.decode_seconds > 0 else 0.0
 
 
-def _argmax(logits: torch.Tensor) -> torch.Tensor:
-    """The greedy choice of each row: the argmax kernel on HIP devices, torch elsewhere."""
+def _argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The greedy choice of each row: the argmax kernel on HIP devices, torch elsewhere; into
+    ``out`` (int64 [rows]) when given."""
     if logits.is_cuda and logits.dim() == 2 and logits.dtype in (torch.float32, torch.float16, torch.bfloat16):
         from llmopt.kernels import ops
 
-        return ops.argmax_rows(logits)
-    return logits.argmax(-1)
+        return ops.argmax_rows(logits, out=out)
+    if out is None:
+        return logits.argmax(-1)
+    return torch.argmax(logits, -1, out=out)
 
 
 class GreedyGenerator:
@@ -96,21 +99,26 @@ class GreedyGenerator:
         prefill_logits = logits.float()
 
         # ---- decode: static buffers advanced in place ----
-        tok = (forced[:, 0].to(dev) if forced is not None else out[:, 0]).clone()
+        tok = (forced[:, 0].to(dev) if forced is not None else out[:, 0]).contiguous().clone()
         pos = torch.full((seqs,), plen, dtype=torch.long, device=dev)
         lens = torch.full((seqs,), plen + 1, dtype=torch.int32, device=dev)
         nxt = torch.empty(seqs, dtype=torch.long, device=dev)
 
+        # Without teacher forcing the step's argmax is the next step's input: written straight
+        # into tok (the embedding gather has read tok before the argmax writes it).
+        sink = nxt if forced is not None else tok
+
         def step() -> None:
             lg = self.model(tok, pos, cache=cache, block_ids=table, context_lens=lens, q_len=1,
                             last_only=True).last_logits()
-            nxt.copy_(_argmax(lg))
+            _argmax(lg, out=sink)
             pos.add_(1)
             lens.add_(1)
 
         def feed(i: int) -> None:  # after step i: record its token, set the next input
-            out[:, i].copy_(nxt)
-            tok.copy_(forced[:, i].to(dev) if forced is not None else nxt)
+            out[:, i].copy_(sink)
+            if forced is not None:
+                tok.copy_(forced[:, i].to(dev))
 
         if steps > 1:
             step()

@@ -142,3 +142,14 @@ def test_argmax_rows_matches_torch(dtype, rows, cols):
     wide[:, 1 : cols + 1] = x
     odd = wide.to(DEV)[:, 1 : cols + 1]  # rows off 16-byte alignment
     assert torch.equal(ops.argmax_rows(odd).cpu(), want)
+    # Into a caller's buffer (the greedy generator's step input).
+    buf = torch.full((rows,), -7, dtype=torch.long, device=DEV)
+    assert ops.argmax_rows(x.to(DEV), out=buf) is buf and torch.equal(buf.cpu(), want)
+
+
+def test_argmax_rows_out_is_checked():
+    x = torch.randn(4, 100).to(DEV)
+    for bad in (torch.empty(4, dtype=torch.int32, device=DEV), torch.empty(5, dtype=torch.long, device=DEV),
+                torch.empty(8, dtype=torch.long, device=DEV)[::2], torch.empty(4, dtype=torch.long)):
+        with pytest.raises(ValueError):
+            ops.argmax_rows(x, out=bad)
