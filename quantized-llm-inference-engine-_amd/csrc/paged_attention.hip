@@ -181,7 +181,11 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))
   const int wave = W > 1 ? int(threadIdx.x >> 6) : 0;
   const int col = lane & 15;
   const int kb = lane >> 4;
-  const int64_t split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+  // PRE: grid (KV head, sequence, query block), the blocks latest in the prompt (the longest
+  // walks under the causal mask) dispatched first: 32 x 512-token prompts 476 -> 448 us against
+  // query blocks innermost.
+  const int64_t split = PRE ? int64_t(gridDim.z) - 1 - blockIdx.z : blockIdx.x;
+  const int64_t kvh = PRE ? blockIdx.x : blockIdx.y, s = PRE ? blockIdx.y : blockIdx.z;
   const int64_t ctx = a.context_lens[s];
   // PRE: the wave's NCB blocks of 16 columns; block cb holds query tokens j0 + cb kTpt .. + kTpt
   // (column col: token j0 + cb kTpt + col / GQ, head col % GQ) and the last key position each
@@ -737,9 +741,9 @@ void launch_prefill_group(const PagedDecodeArgs& a, hipStream_t stream) {
   constexpr int kTpt = 16 / GQ;
   constexpr int kNcb = kPrefillColumnBlocks;
   const int64_t per = int64_t(kTpt) * kNcb * a.waves;  // query tokens per workgroup
-  const dim3 grid(unsigned((a.q_len + per - 1) / per), unsigned(a.kv_heads), unsigned(a.num_seqs));
+  const dim3 grid(unsigned(a.kv_heads), unsigned(a.num_seqs), unsigned((a.q_len + per - 1) / per));
   const int64_t per1 = int64_t(kTpt) * a.waves;
-  const dim3 grid1(unsigned((a.q_len + per1 - 1) / per1), unsigned(a.kv_heads), unsigned(a.num_seqs));
+  const dim3 grid1(unsigned(a.kv_heads), unsigned(a.num_seqs), unsigned((a.q_len + per1 - 1) / per1));
   switch (a.waves) {
     case 1: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 1, false, true, 1>), grid1, dim3(64), 0, stream, a); break;
     case 2: hipLaunchKernelGGL((paged_decode_kernel<C, HD, GQ, 2, false, true, kNcb>), grid, dim3(128), 0, stream, a); break;
